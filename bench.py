@@ -1,0 +1,203 @@
+"""Decode benchmark: random-init Llama-3.1-8B (bf16), batch 1, on one MI355X.
+
+One timed "step" is one ie_decode_step (decode.cuh:6-9 semantics: embed the last
+token, 32 layers, final norm, lm_head, argmax, token read back to the host) plus
+the reference's device-side token write-back (manager.cpp:84).  The KV cache is
+first filled by ie_prefill over a random prompt, so the timed steps run at real
+positions (prompt_len .. prompt_len + warmup + steps).
+
+Also reported, on the same run:
+  roofline      the dominant decode kernel (fused RMSNorm -> gate/up GEMV -> SwiGLU,
+                234,926,080 algorithmic bytes per launch), timed with HIP events
+                on the stream it runs on, rotating over the 32 layers' weights so
+                the 256 MB Infinity Cache cannot serve repeats.
+  cpu_baseline  the CPU oracle (oracle/, OpenMP) decoding the same model on this
+                host: a bounded sample of decoder layers + lm_head, extrapolated
+                to one token.
+
+    python bench.py [--gpus 1] [--steps 128] [--warmup 16] [--prompt 512]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HIDDEN, FFN, VOCAB, LAYERS = 4096, 14336, 128256, 32
+WEIGHT_BYTES_PER_TOKEN = 15_009_849_344          # every weight byte read once per bs=1 step
+KV_BYTES_PER_POS = 131_072                       # 32 layers x (K+V) x 8 heads x 128 x 2 B
+GATE_UP_BYTES = 2 * FFN * HIDDEN * 2 + 2 * HIDDEN * 2 + FFN * 2
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(prompt: int, n_layers: int = 3) -> dict:
+    """The oracle's decode of the same workload: n_layers decoder layers at
+    position `prompt` plus lm_head, each timed; one token = 32 layers + lm_head."""
+    import numpy as np
+
+    import oracle as orc
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    threads = min(threads, len(os.sched_getaffinity(0)))
+    seed = 0
+    cos, sin = orc.rope_tables()
+    kv = orc.synthetic((2, 8, prompt + 1, 128), seed, 9000, 0.0, 1.0)
+    x0 = orc.synthetic((1, HIDDEN), seed, 9001, 0.0, 1.0)
+    t_layers = []
+    for l in range(n_layers):
+        w = orc.layer_weights(seed, l)
+        x = x0.copy()
+        kk, vv = np.ascontiguousarray(kv[0]), np.ascontiguousarray(kv[1])
+        t0 = time.perf_counter()
+        orc.decoder_layer(x, w, prompt, cos, sin, kk, vv, prompt + 1)
+        t_layers.append(time.perf_counter() - t0)
+    lm = orc.lm_head_weight(seed)
+    fn = orc.final_norm(seed)
+    t0 = time.perf_counter()
+    orc.matmul(orc.rmsnorm(x, fn), lm, out_f32=True)
+    t_lm = time.perf_counter() - t0
+    t_tok = LAYERS * (sum(t_layers) / len(t_layers)) + t_lm
+    return {"value": round(1.0 / t_tok, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle decode at position {prompt}: {n_layers} decoder layers "
+                      f"({', '.join(f'{t * 1e3:.0f}' for t in t_layers)} ms) + lm_head "
+                      f"({t_lm * 1e3:.0f} ms), extrapolated to 32 layers + lm_head = "
+                      f"{t_tok * 1e3:.0f} ms/token"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--kernel-iters", type=int, default=64)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the single-GPU path is the whole deliverable; see DESIGN.md for how it shards)",
+              file=sys.stderr)
+        return 2
+
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from infengine_amd import check, lib
+    from infengine_amd.engine import Context, ModelWeights, Request, ptr
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    ctx = Context(0, graph=not args.no_graph)
+    log("random-init weights (16.06 GB)")
+    W = ModelWeights.random_init(seed=0, std=0.02)
+    total = args.prompt + args.warmup + args.steps + 1
+    req = Request(ctx, W, max_seq_len=total + 8)
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, VOCAB, args.prompt).astype(np.int32)
+    req.tokens[: args.prompt] = torch.from_numpy(ids).cuda()
+
+    log(f"prefill {args.prompt} tokens")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = req.prefill(args.prompt)
+    prefill_s = time.perf_counter() - t0
+    req.tokens[args.prompt] = tok
+
+    seq = args.prompt + 1
+
+    def step(seq_len: int) -> int:
+        t = req.decode_step(seq_len)
+        req.tokens[seq_len: seq_len + 1].copy_(req.token)     # manager.cpp:84 (D2D write-back)
+        return t
+
+    log(f"decode warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step(seq)
+        seq += 1
+    torch.cuda.synchronize()
+    first_pos = seq - 1
+    log(f"decode timed {args.steps}")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(seq)
+        seq += 1
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    last_pos = seq - 2
+    ms_per_step = dt * 1e3 / args.steps
+    tok_s = args.steps / dt
+    kv_bytes = KV_BYTES_PER_POS * sum(p + 1 for p in range(first_pos, last_pos + 1)) / args.steps
+    step_gbps = (WEIGHT_BYTES_PER_TOKEN + kv_bytes) / (dt / args.steps) / 1e9
+
+    # ---- dominant kernel, timed live on its own stream with HIP events
+    log("gate/up GEMV kernel timing")
+    h = torch.empty(FFN, dtype=torch.bfloat16, device="cuda")
+    x = req.data[0]
+    launches = []
+    for i in range(args.kernel_iters + 8):
+        L = W.s.layers[i % LAYERS]
+        launches.append((L.post_attention_layernorm, L.ffn_block.w_gate, L.ffn_block.w_up))
+    stream = ctx.stream
+    for (nw, wg, wu) in launches[:8]:
+        check(lib.ie_ffn_gate_up_decode(ctx.handle, ptr(x), C.c_void_p(nw), C.c_void_p(wg),
+                                        C.c_void_p(wu), ptr(h)))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for (nw, wg, wu) in launches[8:]:
+        check(lib.ie_ffn_gate_up_decode(ctx.handle, ptr(x), C.c_void_p(nw), C.c_void_p(wg),
+                                        C.c_void_p(wu), ptr(h)))
+    e1.record(stream)
+    e1.synchronize()
+    k_us = e0.elapsed_time(e1) * 1e3 / args.kernel_iters
+    k_gbps = GATE_UP_BYTES / (k_us * 1e-6) / 1e9
+
+    out = {
+        "metric": "decode tokens/s + weight-stream HBM GB/s (% of 8 TB/s), Llama-3.1-8B bs=1",
+        "value": round(tok_s, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights ~N(0,0.02), random prompt ids)",
+        "config": {"workload": "llama-3.1-8b decode step, batch 1, 32 layers, random-init bf16",
+                   "batch": 1, "prompt_len": args.prompt,
+                   "decode_positions": [first_pos, last_pos],
+                   "graph": not args.no_graph},
+        "step_GBps": round(step_gbps, 1),
+        "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "prefill": {"seq_len": args.prompt, "ms": round(prefill_s * 1e3, 2),
+                    "tokens_per_s": round(args.prompt / prefill_s, 1)},
+        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4096, SwiGLU, RMSNorm> (gate/up)",
+                     "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "avg_launch_us": round(k_us, 2), "bytes_per_launch": GATE_UP_BYTES},
+    }
+    del req
+    W.free()
+    ctx.close()
+    torch.cuda.synchronize()
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle)")
+        out["cpu_baseline"] = cpu_baseline(args.prompt)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,235 @@
+/*
+ * infengine.h — C-ABI of the MI355X (gfx950) per-token Llama-3.1-8B hot path.
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers and sizes, and
+ * returns an int status (IE_OK == 0, negative on error; ie_last_error() gives
+ * the message).  Token-returning entry points (ie_prefill, ie_decode_step)
+ * return the token id (>= 0) on success.
+ *
+ * Storage type is bf16 (IEEE binary32 truncated to the top 16 bits, passed as
+ * uint16_t); accumulation is fp32 everywhere; logits are fp32.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree):
+ *   config.h:5-27                     -> IE_* shape constants below
+ *   kernels/model_weights.cuh:7-34    -> ie_model_weights and its sub-structs
+ *   prefill.cuh:6-9                   -> ie_prefill
+ *   decode.cuh:6-9                    -> ie_decode_step
+ *   kernels/<op>.cuh host launchers   -> ie_<op> launchers (one per reference op)
+ * cublasHandle_t is replaced by an opaque ie_context (owns the HIP stream and
+ * the small device-side counters some kernels use); `half` becomes bf16.
+ */
+#ifndef INFENGINE_H
+#define INFENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IE_API __attribute__((visibility("default")))
+
+/* config.h:5-27 (InfEngineConfig) */
+#define IE_MAX_CONTEXT_LENGTH 8192
+#define IE_VOCAB_SIZE 128256
+#define IE_NUM_LAYERS 32
+#define IE_HIDDEN_SIZE 4096
+#define IE_NUM_Q_HEADS 32
+#define IE_NUM_KV_HEADS 8
+#define IE_HEAD_DIM 128
+#define IE_FFN_DIM 14336
+#define IE_BF16_SIZE 2
+
+/* status codes */
+#define IE_OK 0
+#define IE_ERR_INVALID_ARG (-1)
+#define IE_ERR_HIP (-2)
+#define IE_ERR_UNSUPPORTED (-3)
+#define IE_ERR_IO (-4)
+#define IE_ERR_FORMAT (-5)
+#define IE_ERR_OOM (-6)
+
+typedef uint16_t ie_bf16;
+
+/* kernels/model_weights.cuh:7-9 — same field names and order, bf16 storage */
+typedef struct ie_transformer_block_weights {
+  ie_bf16* w_k; /* [1024, 4096] */
+  ie_bf16* w_q; /* [4096, 4096], rows grouped per head (attn.cu:25) */
+  ie_bf16* w_v; /* [1024, 4096] */
+  ie_bf16* w_o; /* [4096, 4096] */
+} ie_transformer_block_weights;
+
+typedef struct ie_ffn_block_weights {
+  ie_bf16* w_up;   /* [14336, 4096] */
+  ie_bf16* w_gate; /* [14336, 4096] */
+  ie_bf16* w_down; /* [4096, 14336] */
+} ie_ffn_block_weights;
+
+typedef struct ie_rope_weights {
+  float* cos; /* [8192, 64] fp32 */
+  float* sin; /* [8192, 64] fp32 */
+} ie_rope_weights;
+
+/* kernels/model_weights.cuh:11-19 */
+typedef struct ie_layer {
+  ie_bf16* input_layernorm; /* [4096] */
+  ie_transformer_block_weights transformer;
+  ie_bf16* post_attention_layernorm; /* [4096] */
+  ie_ffn_block_weights ffn_block;
+} ie_layer;
+
+/* kernels/model_weights.cuh:21-34.  `storage` is the library-owned arena that
+ * backs every pointer when the weights were made by ie_model_weights_random_init
+ * or ie_model_weights_from_safetensors; NULL when the caller owns them. */
+typedef struct ie_model_weights {
+  ie_bf16* emb_lookup; /* [128256, 4096] */
+  ie_layer layers[IE_NUM_LAYERS];
+  ie_bf16* final_norm; /* [4096] */
+  ie_bf16* lm_head;    /* [128256, 4096] (untied) */
+  ie_rope_weights rope;
+  void* storage;
+} ie_model_weights;
+
+typedef struct ie_context ie_context;
+
+/* ---- context / errors (replaces cublasCreate/cublasDestroy, manager.cpp:58-59,107) ---- */
+/* stream: a hipStream_t to run on, or NULL to create a private non-blocking stream. */
+IE_API int ie_context_create(ie_context** out, int device, void* stream);
+IE_API int ie_context_destroy(ie_context* ctx);
+IE_API void* ie_context_stream(ie_context* ctx);
+/* Replay decode steps through a captured hipGraph (default on). */
+IE_API int ie_context_set_graph(ie_context* ctx, int enable);
+IE_API const char* ie_last_error(void);
+
+/* ---- sizing (attn.cu:295-307, ffn.cu:35-37) ---- */
+IE_API size_t ie_attn_workspace_size(int max_seq_len);
+IE_API size_t ie_ffn_workspace_size(int max_seq_len);
+IE_API size_t ie_kv_cache_size(void); /* [32][2][8][8192][128] bf16 = 1 GiB */
+
+/* ---- engine entry points (prefill.cuh:6-9, decode.cuh:6-9) ----
+ * Same 11 parameters, order and meaning as the reference; returns the greedy
+ * (argmax) token id, also written to *output_token (device).  output_distr
+ * receives fp32 logits [128256] of the last position.  seq_len counts the
+ * tokens in tokenid_buff; decode_step embeds tokenid_buff[seq_len-1] and writes
+ * its K/V at cache row seq_len-1. */
+IE_API int ie_prefill(ie_context* ctx, const ie_model_weights* weights, int seq_len,
+                      int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                      ie_bf16* attn_buffer, float* output_distr, int* output_token,
+                      void* workspace, void* kv_cache);
+IE_API int ie_decode_step(ie_context* ctx, const ie_model_weights* weights, int seq_len,
+                          int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                          ie_bf16* attn_buffer, float* output_distr, int* output_token,
+                          void* workspace, void* kv_cache);
+
+/* Batched decode (no reference counterpart: manager.h:19-24 RequestContext is
+ * unused there).  `batch` independent sequences; seq_lens is a HOST array;
+ * tokenid_buffs is a device array [batch][8192]; row b's K/V live in
+ * kv_caches + b * ie_kv_cache_size().  data/attn buffers are [batch, 4096];
+ * output_distr [batch, 128256]; output_tokens (device) [batch]; tokens_out
+ * (host, may be NULL) receives the greedy ids. */
+IE_API size_t ie_batch_workspace_size(int batch);
+IE_API int ie_decode_step_batched(ie_context* ctx, const ie_model_weights* weights, int batch,
+                                  const int* seq_lens, int* tokenid_buffs,
+                                  ie_bf16* data_buffer, ie_bf16* attn_buffer,
+                                  float* output_distr, int* output_tokens, int* tokens_out,
+                                  void* workspace, void* kv_caches);
+
+/* ---- weights (model_weights.cu:142-172) ---- */
+/* Random-init Llama-3.1-8B: matrices ~N(0,std), norms ~1+N(0,0.02), rope tables. */
+IE_API int ie_model_weights_random_init(ie_model_weights* out, uint64_t seed, float std);
+IE_API int ie_model_weights_from_safetensors(ie_model_weights* out, const char* const* paths,
+                                             int n_paths);
+IE_API int ie_model_weights_free(ie_model_weights* w);
+/* rope.cu:68-103: Llama-3 scaled RoPE tables, fp32 [8192, 64]; allocates. */
+IE_API int ie_init_rope_buffer(float** cu_rope_cos, float** cu_rope_sin);
+IE_API int ie_cleanup_rope_buffer(float* cu_rope_cos, float* cu_rope_sin);
+/* Deterministic synthetic tensor: out[i] = bf16(mean + std * z_i), z_i an
+ * integer-exact approximate normal keyed by (seed, tensor_id, i). */
+IE_API int ie_fill_synthetic_bf16(ie_bf16* out, size_t n, uint64_t seed, uint64_t tensor_id,
+                                  float mean, float std, void* stream);
+
+/* ---- op launchers (one per reference host launcher); stream may be NULL ---- */
+/* emblookup.cu:7-10 */
+IE_API int ie_emblookup(int seq_len, const int* d_input, const ie_bf16* d_weights,
+                        ie_bf16* d_output, void* stream);
+/* rmsnorm.cu:7-10 (eps 1e-5, hidden 4096) */
+IE_API int ie_rmsnorm(int seq_len, const ie_bf16* d_input, const ie_bf16* d_weight,
+                      ie_bf16* d_output, void* stream);
+/* residual_add.cu:5-8: x += delta */
+IE_API int ie_residual_add(int rows, int cols, ie_bf16* d_x, const ie_bf16* d_delta,
+                           void* stream);
+/* swiglu.cu:8-14: out = silu(gate) * up over [seq_len, 14336] */
+IE_API int ie_swiglu(int seq_len, const ie_bf16* d_gate, const ie_bf16* d_up,
+                     ie_bf16* d_output, void* stream);
+/* rope.cu:20-22: rotate-half pairs (j, j+64) of [num_heads, seq_len|8192, 128] */
+IE_API int ie_apply_rope(int start_pos, int num_heads, int seq_len, const float* d_rope_cos,
+                         const float* d_rope_sin, const ie_bf16* d_input, ie_bf16* d_output,
+                         int is_kv_cache, void* stream);
+/* softmax.cu:10-20: softmax(x / sqrt(128)) over rows of [32, seq_len, seq_len]
+ * (causal) or [32, seq_len] (is_row) */
+IE_API int ie_scale_causal_softmax(int seq_len, const ie_bf16* d_input, ie_bf16* d_output,
+                                   int is_row, void* stream);
+/* ffn.cu:7-33: Y[m,n] = X[m,k] . W[n,k]^T, bf16 out, fp32 accumulate */
+IE_API int ie_multiply_by_weight(ie_context* ctx, int m, int k, int n, const ie_bf16* d_in,
+                                 const ie_bf16* d_w, ie_bf16* d_out);
+/* ffn.cu:39-64: out = down(silu(gate . x) * (up . x)) */
+IE_API int ie_ffn(ie_context* ctx, int seq_len, const ie_bf16* d_in, ie_bf16* d_out,
+                  const ie_bf16* d_wup, const ie_bf16* d_wdown, const ie_bf16* d_wgate,
+                  void* workspace);
+/* attn.cu:309-371: causal GQA self-attention of seq_len rows from position 0;
+ * K/V written to the cache rows 0..seq_len-1 of layer_idx. */
+IE_API int ie_attn(ie_context* ctx, const float* d_rope_cos, const float* d_rope_sin,
+                   int seq_len, const ie_bf16* d_input, const ie_bf16* d_qproj,
+                   const ie_bf16* d_kproj, const ie_bf16* d_vproj, const ie_bf16* d_oproj,
+                   ie_bf16* d_output, void* workspace, void* kv_cache, int layer_idx);
+/* attn.cu:373-439: one decode row at position seq_len-1 */
+IE_API int ie_decode_attn(ie_context* ctx, const float* d_rope_cos, const float* d_rope_sin,
+                          int seq_len, const ie_bf16* d_input, const ie_bf16* d_qproj,
+                          const ie_bf16* d_kproj, const ie_bf16* d_vproj,
+                          const ie_bf16* d_oproj, ie_bf16* d_output, void* workspace,
+                          void* kv_cache, int layer_idx);
+/* lm_head.cu:5-20: logits (fp32) of row seq_len-1 */
+IE_API int ie_lm_head(ie_context* ctx, int seq_len, const ie_bf16* d_input,
+                      const ie_bf16* d_weight, float* d_output);
+/* sampling.cu:54-58: argmax over 128256 fp32 logits (first maximal index,
+ * NaN counts as the maximum, -0.0 == +0.0) */
+IE_API int ie_sample_token_amax(ie_context* ctx, const float* d_logits, int* d_output);
+/* Row-wise argmax over [rows, vocab]. */
+IE_API int ie_sample_argmax_rows(ie_context* ctx, int rows, int vocab, const float* d_logits,
+                                 int* d_output);
+/* Temperature + top-p (nucleus) sampling over [rows, vocab] fp32 logits; no
+ * reference counterpart (sampling.cu has argmax only).  Deterministic:
+ * uniform u = counter RNG(seed, row, step); inverse CDF in token-id order over
+ * the kept set.  workspace: ie_top_p_workspace_size(rows, vocab) bytes. */
+IE_API size_t ie_top_p_workspace_size(int rows, int vocab);
+IE_API int ie_sample_top_p(ie_context* ctx, int rows, int vocab, const float* d_logits,
+                           float temperature, float top_p, uint64_t seed, uint64_t step,
+                           int* d_output, void* workspace);
+
+/* ---- fused decode kernels (building blocks of ie_decode_step, exposed for tests) ---- */
+/* x_resid += W_down . (silu(W_gate . rmsnorm(x_resid)) * (W_up . rmsnorm(x_resid))) */
+IE_API int ie_ffn_block_decode(ie_context* ctx, ie_bf16* d_x_resid, const ie_bf16* d_norm_w,
+                               const ie_bf16* d_wgate, const ie_bf16* d_wup,
+                               const ie_bf16* d_wdown, void* workspace);
+/* h = silu(W_gate . rmsnorm(x)) * (W_up . rmsnorm(x)), one kernel: the dominant
+ * decode kernel (two 117 MB weight streams per layer). */
+IE_API int ie_ffn_gate_up_decode(ie_context* ctx, const ie_bf16* d_x, const ie_bf16* d_norm_w,
+                                 const ie_bf16* d_wgate, const ie_bf16* d_wup, ie_bf16* d_h);
+/* One full decoder layer for a single token at position seq_len-1 (in place on d_x). */
+IE_API int ie_decoder_layer_decode(ie_context* ctx, const ie_model_weights* weights,
+                                   int layer_idx, int seq_len, ie_bf16* d_x,
+                                   ie_bf16* d_attn_out, void* workspace, void* kv_cache);
+/* final RMSNorm + lm_head GEMV to fp32 logits for `rows` rows of [rows, 4096]. */
+IE_API int ie_final_norm_lm_head(ie_context* ctx, int rows, const ie_bf16* d_x,
+                                 const ie_bf16* d_norm_w, const ie_bf16* d_lm_head,
+                                 float* d_logits);
+/* Plain GEMM Y[m,n] = X[m,k] . W[n,k]^T on the MFMA path (any m >= 1). */
+IE_API int ie_gemm_bf16(ie_context* ctx, int m, int k, int n, const ie_bf16* d_x,
+                        const ie_bf16* d_w, ie_bf16* d_y);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INFENGINE_H */

@@ -1,0 +1,940 @@
+// Engine: context, workspace layout, the prefill / decode_step entry points and
+// the extern "C" op launchers.
+//
+// Reference flow being replaced: decode_step (decode.cu:11-49) and prefill
+// (prefill.cu:11-48), which launch ~19 kernels per layer on the legacy stream.
+// decode_step here is 5 kernels per layer:
+//   1. QKV GEMV  (RMSNorm prologue; RoPE + KV-cache write epilogue)
+//   2. GQA decode attention (split context, last-block merge)
+//   3. O GEMV    (residual-add epilogue into data_buffer)
+//   4. gate/up GEMV (RMSNorm prologue; SwiGLU epilogue)
+//   5. down GEMV (residual-add epilogue)
+// then final-norm + lm_head GEMV (fp32 logits) and argmax.  The per-step scalar
+// (seq_len) lives in device memory, so the whole step is captured once into a
+// hipGraph and replayed.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <numbers>
+#include <vector>
+
+#include "ie_kernels.h"
+
+struct ie_context : public ie::Context {};
+
+namespace ie {
+
+namespace {
+thread_local char g_err[1024] = "";
+
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// ---- decode workspace: [q | h | attn1 | partials]
+struct DecodeWs {
+  uint16_t* q;      // [batch][4096]   rotated q
+  uint16_t* h;      // [batch][14336]  SwiGLU output
+  uint16_t* attn1;  // [batch][4096]   attention output (op-level decode_attn only)
+  float* part_o;
+  float* part_ml;
+  uint16_t* xn;     // [batch][4096]   normalised rows (batched path)
+  uint16_t* qkv;    // [batch][6144]   projection (batched path)
+};
+
+size_t decode_ws_bytes(int batch) {
+  return align256((size_t)batch * kHidden * 2) + align256((size_t)batch * kFFN * 2) +
+         align256((size_t)batch * kHidden * 2) + align256(attn_decode_partials_bytes(batch)) +
+         align256((size_t)batch * kHidden * 2) + align256((size_t)batch * kQKVDim * 2);
+}
+
+DecodeWs decode_ws(void* ws, int batch) {
+  char* p = static_cast<char*>(ws);
+  DecodeWs d;
+  d.q = reinterpret_cast<uint16_t*>(p);
+  p += align256((size_t)batch * kHidden * 2);
+  d.h = reinterpret_cast<uint16_t*>(p);
+  p += align256((size_t)batch * kFFN * 2);
+  d.attn1 = reinterpret_cast<uint16_t*>(p);
+  p += align256((size_t)batch * kHidden * 2);
+  const size_t slots = (size_t)batch * kKVHeads * kAttnSplits * kGQA;
+  d.part_o = reinterpret_cast<float*>(p);
+  d.part_ml = d.part_o + slots * kHeadDim;
+  p += align256(attn_decode_partials_bytes(batch));
+  d.xn = reinterpret_cast<uint16_t*>(p);
+  p += align256((size_t)batch * kHidden * 2);
+  d.qkv = reinterpret_cast<uint16_t*>(p);
+  return d;
+}
+
+// ---- prefill workspace: [qkv / attention scratch | rotated q] (attention phase)
+//                         [h]                                   (FFN phase)
+size_t prefill_attn_bytes(int S) {
+  return align256((size_t)S * kQKVDim * 2) + align256((size_t)S * kHidden * 2);
+}
+size_t prefill_ffn_bytes(int S) { return align256((size_t)S * kFFN * 2); }
+
+uint16_t* kv_layer(void* kv, int layer) {
+  return static_cast<uint16_t*>(kv) + (size_t)layer * kKVLayer;
+}
+
+// ---- decode building blocks -------------------------------------------------
+int qkv_rope_gemv(const ie_layer& L, const ie_rope_weights& rope, const uint16_t* x,
+                  const uint16_t* norm_w, uint16_t* q_out, uint16_t* kvl, const int* d_seq_len,
+                  int pos, hipStream_t st) {
+  GemvParams p{};
+  p.x = x;
+  p.norm_w = norm_w;
+  p.w0 = L.transformer.w_q;
+  p.w1 = L.transformer.w_k;
+  p.w2 = L.transformer.w_v;
+  p.out = q_out;
+  p.k_cache = kvl;
+  p.v_cache = kvl + (size_t)kKVHeads * kKVPlane;
+  p.rope_cos = rope.cos;
+  p.rope_sin = rope.sin;
+  p.d_seq_len = d_seq_len;
+  p.pos = pos;
+  p.n_pairs = (kQHeads + 2 * kKVHeads) * 64;
+  return launch_gemv(kHidden, kEpiQkvRope, norm_w != nullptr, p, 1, st);
+}
+
+int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs& w,
+                unsigned int* counters, const int* d_seq_len, int seq_len, int batch,
+                long long cache_stride, hipStream_t st) {
+  AttnDecodeParams a{};
+  a.q = q;
+  a.k_cache = kvl;
+  a.v_cache = kvl + (size_t)kKVHeads * kKVPlane;
+  a.cache_batch_stride = cache_stride;
+  a.out = out;
+  a.part_o = w.part_o;
+  a.part_ml = w.part_ml;
+  a.counters = counters;
+  a.d_seq_len = d_seq_len;
+  a.seq_len = seq_len;
+  return launch_attn_decode(a, batch, st);
+}
+
+int gemv_plain(int K, int epi, const uint16_t* x, const uint16_t* norm_w, const uint16_t* w0,
+               const uint16_t* w1, int n_pairs, uint16_t* out, float* out_f32, int rows,
+               long long out_stride, hipStream_t st) {
+  GemvParams p{};
+  p.x = x;
+  p.norm_w = norm_w;
+  p.w0 = w0;
+  p.w1 = w1;
+  p.out = out;
+  p.out_f32 = out_f32;
+  p.n_pairs = n_pairs;
+  p.x_stride = K;
+  p.out_stride = out_stride;
+  return launch_gemv(K, epi, norm_w != nullptr, p, rows, st);
+}
+
+int decoder_layer_decode(Context* c, const ie_model_weights& W, int layer, uint16_t* x,
+                         uint16_t* attn_out, const DecodeWs& w, void* kv, const int* d_seq_len,
+                         int seq_len) {
+  hipStream_t st = c->stream;
+  const ie_layer& L = W.layers[layer];
+  uint16_t* kvl = kv_layer(kv, layer);
+  IE_TRY(qkv_rope_gemv(L, W.rope, x, L.input_layernorm, w.q, kvl, d_seq_len, seq_len - 1, st));
+  IE_TRY(attn_decode(w.q, kvl, attn_out, w, c->d_counters + kCntAttn, d_seq_len, seq_len, 1, 0,
+                     st));
+  IE_TRY(gemv_plain(kHidden, kEpiResid, attn_out, nullptr, L.transformer.w_o, nullptr,
+                    kHidden / 2, x, nullptr, 1, 0, st));
+  IE_TRY(gemv_plain(kHidden, kEpiSwiglu, x, L.post_attention_layernorm, L.ffn_block.w_gate,
+                    L.ffn_block.w_up, kFFN, w.h, nullptr, 1, 0, st));
+  IE_TRY(gemv_plain(kFFN, kEpiResid, w.h, nullptr, L.ffn_block.w_down, nullptr, kHidden / 2, x,
+                    nullptr, 1, 0, st));
+  return IE_OK;
+}
+
+int enqueue_decode(Context* c, const ie_model_weights& W, int* tokenid_buff, uint16_t* data,
+                   uint16_t* attn, float* logits, int* out_tok, void* ws, void* kv) {
+  hipStream_t st = c->stream;
+  const int* d_sl = c->d_params;
+  const DecodeWs w = decode_ws(ws, 1);
+  IE_TRY(launch_emblookup(1, tokenid_buff, W.emb_lookup, data, d_sl, 0, st));
+  for (int l = 0; l < kLayers; ++l)
+    IE_TRY(decoder_layer_decode(c, W, l, data, attn, w, kv, d_sl, 0));
+  IE_TRY(gemv_plain(kHidden, kEpiF32, data, W.final_norm, W.lm_head, nullptr, kVocab / 2,
+                    nullptr, logits, 1, kVocab, st));
+  IE_TRY(launch_argmax_rows(1, kVocab, logits, out_tok, c->d_slots, c->d_counters + kCntArgmax,
+                            st));
+  return IE_OK;
+}
+
+bool weights_complete(const ie_model_weights& W) {
+  if (!W.emb_lookup || !W.final_norm || !W.lm_head || !W.rope.cos || !W.rope.sin) return false;
+  for (int l = 0; l < kLayers; ++l) {
+    const ie_layer& L = W.layers[l];
+    if (!L.input_layernorm || !L.post_attention_layernorm || !L.transformer.w_q ||
+        !L.transformer.w_k || !L.transformer.w_v || !L.transformer.w_o || !L.ffn_block.w_up ||
+        !L.ffn_block.w_gate || !L.ffn_block.w_down)
+      return false;
+  }
+  return true;
+}
+
+// FNV-1a over the bytes of the weight table (graph cache key).
+uint64_t hash_bytes(const void* p, size_t n, uint64_t h = 1469598103934665603ull) {
+  const unsigned char* b = static_cast<const unsigned char*>(p);
+  for (size_t i = 0; i < n; ++i) h = (h ^ b[i]) * 1099511628211ull;
+  return h;
+}
+
+int set_device(Context* c) {
+  IE_CHECK_HIP(hipSetDevice(c->device));
+  return IE_OK;
+}
+
+// ---- RoPE tables: rope.cu:68-96 (Llama-3 frequency scaling, theta 500000)
+void rope_tables_host(std::vector<float>& cos_t, std::vector<float>& sin_t) {
+  const float theta = 500000.0f;
+  const int factor = 8, low_ff = 1, high_ff = 4, orig = 8192;
+  const int low_wl = orig / low_ff, high_wl = orig / high_ff;
+  float freqs[kHeadDim / 2];
+  for (int i = 0; i < kHeadDim / 2; ++i) {
+    const float freq = 1 / std::pow(theta, 2.0 * i / kHeadDim);
+    const float wavelength = 2 * std::numbers::pi / freq;
+    if (wavelength > low_wl) {
+      freqs[i] = freq / factor;
+    } else if (wavelength < high_wl) {
+      freqs[i] = freq;
+    } else {
+      const float smooth = (orig / wavelength - low_ff) / (high_ff - low_ff);
+      freqs[i] = (1 - smooth) * (freq / factor) + smooth * freq;
+    }
+  }
+  cos_t.resize((size_t)kMaxCtx * 64);
+  sin_t.resize((size_t)kMaxCtx * 64);
+  for (int pos = 0; pos < kMaxCtx; ++pos)
+    for (int i = 0; i < 64; ++i) {
+      const float angle = pos * freqs[i];
+      cos_t[(size_t)pos * 64 + i] = std::cos(angle);
+      sin_t[(size_t)pos * 64 + i] = std::sin(angle);
+    }
+}
+
+}  // namespace
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+const char* get_error() { return g_err; }
+
+}  // namespace ie
+
+using namespace ie;
+
+#define CTX_OK(ctx)                                                   \
+  do {                                                                \
+    IE_REQUIRE((ctx) != nullptr, "%s: null context", __func__);       \
+    IE_TRY(set_device(ctx));                                          \
+  } while (0)
+
+extern "C" {
+
+const char* ie_last_error(void) { return get_error(); }
+
+int ie_context_create(ie_context** out, int device, void* stream) {
+  IE_REQUIRE(out != nullptr, "ie_context_create: out is null");
+  *out = nullptr;
+  int n = 0;
+  IE_CHECK_HIP(hipGetDeviceCount(&n));
+  IE_REQUIRE(device >= 0 && device < n, "ie_context_create: device %d of %d", device, n);
+  IE_CHECK_HIP(hipSetDevice(device));
+  ie_context* c = new ie_context;
+  c->device = device;
+  int rc = IE_OK;
+  do {
+    if (stream) {
+      c->stream = stream_of(stream);
+    } else {
+      if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        rc = IE_ERR_HIP;
+        break;
+      }
+      c->own_stream = true;
+    }
+    if (hipMalloc(&c->d_counters, kNumCounters * sizeof(unsigned int)) != hipSuccess ||
+        hipMalloc(&c->d_slots, kNumSlots * sizeof(unsigned long long)) != hipSuccess ||
+        hipMalloc(&c->d_params, 64 * sizeof(int)) != hipSuccess ||
+        hipHostMalloc(&c->h_params, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(&c->h_token, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+      rc = IE_ERR_OOM;
+      break;
+    }
+    if (hipMemset(c->d_counters, 0, kNumCounters * sizeof(unsigned int)) != hipSuccess ||
+        hipMemset(c->d_slots, 0, kNumSlots * sizeof(unsigned long long)) != hipSuccess ||
+        hipMemset(c->d_params, 0, 64 * sizeof(int)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+      rc = IE_ERR_HIP;
+      break;
+    }
+  } while (0);
+  if (rc != IE_OK) {
+    set_error("ie_context_create: HIP allocation/initialisation failed");
+    ie_context_destroy(c);
+    return rc;
+  }
+  *out = c;
+  return IE_OK;
+}
+
+int ie_context_destroy(ie_context* c) {
+  if (!c) return IE_OK;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+  (void)hipFree(c->d_counters);
+  (void)hipFree(c->d_slots);
+  (void)hipFree(c->d_params);
+  if (c->h_params) (void)hipHostFree(c->h_params);
+  if (c->h_token) (void)hipHostFree(c->h_token);
+  if (c->own_stream && c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+  return IE_OK;
+}
+
+void* ie_context_stream(ie_context* c) { return c ? (void*)c->stream : nullptr; }
+
+int ie_context_set_graph(ie_context* c, int enable) {
+  IE_REQUIRE(c != nullptr, "ie_context_set_graph: null context");
+  c->use_graph = enable != 0;
+  return IE_OK;
+}
+
+size_t ie_attn_workspace_size(int max_seq_len) {
+  const int S = max_seq_len < 1 ? 1 : max_seq_len;
+  const size_t a = decode_ws_bytes(1), b = prefill_attn_bytes(S);
+  return a > b ? a : b;
+}
+
+size_t ie_ffn_workspace_size(int max_seq_len) {
+  const int S = max_seq_len < 1 ? 1 : max_seq_len;
+  const size_t a = decode_ws_bytes(1), b = prefill_ffn_bytes(S);
+  return a > b ? a : b;
+}
+
+size_t ie_kv_cache_size(void) { return (size_t)kLayers * kKVLayer * sizeof(uint16_t); }
+
+size_t ie_batch_workspace_size(int batch) {
+  return decode_ws_bytes(batch < 1 ? 1 : batch);
+}
+
+// ---------------------------------------------------------------- decode_step
+int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
+                   int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                   ie_bf16* attn_buffer, float* output_distr, int* output_token,
+                   void* workspace, void* kv_cache) {
+  (void)aux_buffer;  // normalised activations never leave the GEMV prologues
+  CTX_OK(c);
+  IE_REQUIRE(weights && weights_complete(*weights), "decode_step: incomplete weights");
+  IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "decode_step: seq_len %d out of [1, %d]",
+             seq_len, kMaxCtx);
+  IE_REQUIRE(tokenid_buff && data_buffer && attn_buffer && output_distr && output_token &&
+                 workspace && kv_cache,
+             "decode_step: null buffer");
+  hipStream_t st = c->stream;
+  c->h_params[0] = seq_len;
+  IE_CHECK_HIP(hipMemcpyAsync(c->d_params, c->h_params, sizeof(int), hipMemcpyHostToDevice, st));
+
+  if (c->use_graph) {
+    const void* key[12] = {(const void*)weights, tokenid_buff, data_buffer, attn_buffer,
+                           output_distr, output_token, workspace, kv_cache,
+                           (const void*)(uintptr_t)hash_bytes(weights, sizeof(*weights)),
+                           nullptr, nullptr, nullptr};
+    if (!c->graph_exec || std::memcmp(key, c->graph_key, sizeof key) != 0) {
+      if (c->graph_exec) {
+        IE_CHECK_HIP(hipGraphExecDestroy(c->graph_exec));
+        c->graph_exec = nullptr;
+      }
+      hipGraph_t g = nullptr;
+      IE_CHECK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+      const int rc = enqueue_decode(c, *weights, tokenid_buff, data_buffer, attn_buffer,
+                                    output_distr, output_token, workspace, kv_cache);
+      const hipError_t ec = hipStreamEndCapture(st, &g);
+      if (rc != IE_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+      }
+      IE_CHECK_HIP(ec);
+      const hipError_t ei = hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      IE_CHECK_HIP(ei);
+      std::memcpy(c->graph_key, key, sizeof key);
+    }
+    IE_CHECK_HIP(hipGraphLaunch(c->graph_exec, st));
+  } else {
+    IE_TRY(enqueue_decode(c, *weights, tokenid_buff, data_buffer, attn_buffer, output_distr,
+                          output_token, workspace, kv_cache));
+  }
+  IE_CHECK_HIP(hipMemcpyAsync(c->h_token, output_token, sizeof(int), hipMemcpyDeviceToHost, st));
+  IE_CHECK_HIP(hipStreamSynchronize(st));
+  return c->h_token[0];
+}
+
+// ---------------------------------------------------------------- prefill
+int ie_prefill(ie_context* c, const ie_model_weights* weights, int seq_len, int* tokenid_buff,
+               ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
+               float* output_distr, int* output_token, void* workspace, void* kv_cache) {
+  CTX_OK(c);
+  IE_REQUIRE(weights && weights_complete(*weights), "prefill: incomplete weights");
+  IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "prefill: seq_len %d out of [1, %d]", seq_len,
+             kMaxCtx);
+  IE_REQUIRE(tokenid_buff && data_buffer && aux_buffer && attn_buffer && output_distr &&
+                 output_token && workspace && kv_cache,
+             "prefill: null buffer");
+  const ie_model_weights& W = *weights;
+  hipStream_t st = c->stream;
+  const int S = seq_len;
+  char* wsb = static_cast<char*>(workspace);
+  uint16_t* qkv = reinterpret_cast<uint16_t*>(wsb);
+  uint16_t* qrot = reinterpret_cast<uint16_t*>(wsb + align256((size_t)S * kQKVDim * 2));
+  uint16_t* h = reinterpret_cast<uint16_t*>(wsb);
+
+  IE_TRY(launch_emblookup(S, tokenid_buff, W.emb_lookup, data_buffer, nullptr, 0, st));
+  for (int l = 0; l < kLayers; ++l) {
+    const ie_layer& L = W.layers[l];
+    uint16_t* kvl = kv_layer(kv_cache, l);
+    IE_TRY(launch_rmsnorm(S, data_buffer, L.input_layernorm, aux_buffer, st));
+    GemmParams g{};
+    g.x = aux_buffer;
+    g.w0 = L.transformer.w_q;
+    g.w1 = L.transformer.w_k;
+    g.w2 = L.transformer.w_v;
+    g.n0 = kHidden;
+    g.n1 = kKVDim;
+    g.y = qkv;
+    g.M = S;
+    g.N = kQKVDim;
+    g.K = kHidden;
+    g.ldy = kQKVDim;
+    IE_TRY(launch_gemm(kGemmBf16, g, st));
+    IE_TRY(launch_qkv_rope_scatter(S, 0, qkv, W.rope.cos, W.rope.sin, qrot, kvl,
+                                   kvl + (size_t)kKVHeads * kKVPlane, nullptr, 0, st));
+    AttnPrefillParams a{qrot, kvl, kvl + (size_t)kKVHeads * kKVPlane, attn_buffer, S, 0};
+    IE_TRY(launch_attn_prefill(a, st));
+    GemmParams o{};
+    o.x = attn_buffer;
+    o.w0 = L.transformer.w_o;
+    o.n0 = kHidden;
+    o.y = data_buffer;
+    o.M = S;
+    o.N = kHidden;
+    o.K = kHidden;
+    o.ldy = kHidden;
+    IE_TRY(launch_gemm(kGemmResid, o, st));
+    IE_TRY(launch_rmsnorm(S, data_buffer, L.post_attention_layernorm, aux_buffer, st));
+    GemmParams gu{};
+    gu.x = aux_buffer;
+    gu.w0 = L.ffn_block.w_gate;
+    gu.w1 = L.ffn_block.w_up;
+    gu.y = h;
+    gu.M = S;
+    gu.N = kFFN;
+    gu.K = kHidden;
+    gu.ldy = kFFN;
+    IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
+    GemmParams dn{};
+    dn.x = h;
+    dn.w0 = L.ffn_block.w_down;
+    dn.n0 = kHidden;
+    dn.y = data_buffer;
+    dn.M = S;
+    dn.N = kHidden;
+    dn.K = kFFN;
+    dn.ldy = kHidden;
+    IE_TRY(launch_gemm(kGemmResid, dn, st));
+  }
+  // prefill.cu:41-43: final norm, lm_head on the last row only, argmax
+  IE_TRY(gemv_plain(kHidden, kEpiF32, data_buffer + (size_t)(S - 1) * kHidden, W.final_norm,
+                    W.lm_head, nullptr, kVocab / 2, nullptr, output_distr, 1, kVocab, st));
+  IE_TRY(launch_argmax_rows(1, kVocab, output_distr, output_token, c->d_slots,
+                            c->d_counters + kCntArgmax, st));
+  IE_CHECK_HIP(hipMemcpyAsync(c->h_token, output_token, sizeof(int), hipMemcpyDeviceToHost, st));
+  IE_CHECK_HIP(hipStreamSynchronize(st));
+  return c->h_token[0];
+}
+
+// ---------------------------------------------------------------- batched decode
+int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int batch,
+                           const int* seq_lens, int* tokenid_buffs, ie_bf16* data_buffer,
+                           ie_bf16* attn_buffer, float* output_distr, int* output_tokens,
+                           int* tokens_out, void* workspace, void* kv_caches) {
+  CTX_OK(c);
+  IE_REQUIRE(weights && weights_complete(*weights), "decode_step_batched: incomplete weights");
+  IE_REQUIRE(batch >= 1 && batch <= 16, "decode_step_batched: batch %d out of [1, 16]", batch);
+  IE_REQUIRE(seq_lens && tokenid_buffs && data_buffer && attn_buffer && output_distr &&
+                 output_tokens && workspace && kv_caches,
+             "decode_step_batched: null buffer");
+  for (int b = 0; b < batch; ++b)
+    IE_REQUIRE(seq_lens[b] >= 1 && seq_lens[b] <= kMaxCtx,
+               "decode_step_batched: seq_lens[%d]=%d out of [1, %d]", b, seq_lens[b], kMaxCtx);
+  const ie_model_weights& W = *weights;
+  hipStream_t st = c->stream;
+  for (int b = 0; b < batch; ++b) c->h_params[1 + b] = seq_lens[b];
+  IE_CHECK_HIP(hipMemcpyAsync(c->d_params + 1, c->h_params + 1, batch * sizeof(int),
+                              hipMemcpyHostToDevice, st));
+  const int* d_sl = c->d_params + 1;
+  const DecodeWs w = decode_ws(workspace, batch);
+  const long long cstride = (long long)kLayers * kKVLayer;
+  IE_TRY(launch_emblookup(batch, tokenid_buffs, W.emb_lookup, data_buffer, d_sl, kMaxCtx, st));
+  for (int l = 0; l < kLayers; ++l) {
+    const ie_layer& L = W.layers[l];
+    uint16_t* kvl = kv_layer(kv_caches, l);
+    IE_TRY(launch_rmsnorm(batch, data_buffer, L.input_layernorm, w.xn, st));
+    GemmParams g{};
+    g.x = w.xn;
+    g.w0 = L.transformer.w_q;
+    g.w1 = L.transformer.w_k;
+    g.w2 = L.transformer.w_v;
+    g.n0 = kHidden;
+    g.n1 = kKVDim;
+    g.y = w.qkv;
+    g.M = batch;
+    g.N = kQKVDim;
+    g.K = kHidden;
+    g.ldy = kQKVDim;
+    IE_TRY(launch_gemm(kGemmBf16, g, st));
+    IE_TRY(launch_qkv_rope_scatter(batch, 0, w.qkv, W.rope.cos, W.rope.sin, w.q, kvl,
+                                   kvl + (size_t)kKVHeads * kKVPlane, d_sl, cstride, st));
+    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, c->d_counters + kCntAttn, d_sl, 0, batch,
+                       cstride, st));
+    GemmParams o{};
+    o.x = attn_buffer;
+    o.w0 = L.transformer.w_o;
+    o.n0 = kHidden;
+    o.y = data_buffer;
+    o.M = batch;
+    o.N = kHidden;
+    o.K = kHidden;
+    o.ldy = kHidden;
+    IE_TRY(launch_gemm(kGemmResid, o, st));
+    IE_TRY(launch_rmsnorm(batch, data_buffer, L.post_attention_layernorm, w.xn, st));
+    GemmParams gu{};
+    gu.x = w.xn;
+    gu.w0 = L.ffn_block.w_gate;
+    gu.w1 = L.ffn_block.w_up;
+    gu.y = w.h;
+    gu.M = batch;
+    gu.N = kFFN;
+    gu.K = kHidden;
+    gu.ldy = kFFN;
+    IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
+    GemmParams dn{};
+    dn.x = w.h;
+    dn.w0 = L.ffn_block.w_down;
+    dn.n0 = kHidden;
+    dn.y = data_buffer;
+    dn.M = batch;
+    dn.N = kHidden;
+    dn.K = kFFN;
+    dn.ldy = kHidden;
+    IE_TRY(launch_gemm(kGemmResid, dn, st));
+  }
+  IE_TRY(launch_rmsnorm(batch, data_buffer, W.final_norm, w.xn, st));
+  GemmParams lm{};
+  lm.x = w.xn;
+  lm.w0 = W.lm_head;
+  lm.n0 = kVocab;
+  lm.yf = output_distr;
+  lm.M = batch;
+  lm.N = kVocab;
+  lm.K = kHidden;
+  lm.ldy = kVocab;
+  IE_TRY(launch_gemm(kGemmF32, lm, st));
+  IE_TRY(launch_argmax_rows(batch, kVocab, output_distr, output_tokens, c->d_slots,
+                            c->d_counters + kCntArgmax, st));
+  if (tokens_out) {
+    IE_CHECK_HIP(hipMemcpyAsync(c->h_token, output_tokens, batch * sizeof(int),
+                                hipMemcpyDeviceToHost, st));
+    IE_CHECK_HIP(hipStreamSynchronize(st));
+    std::memcpy(tokens_out, c->h_token, batch * sizeof(int));
+  } else {
+    IE_CHECK_HIP(hipStreamSynchronize(st));
+  }
+  return IE_OK;
+}
+
+// ---------------------------------------------------------------- weights
+int ie_init_rope_buffer(float** cu_rope_cos, float** cu_rope_sin) {
+  IE_REQUIRE(cu_rope_cos && cu_rope_sin, "init_rope_buffer: null output");
+  std::vector<float> ct, stb;
+  rope_tables_host(ct, stb);
+  const size_t bytes = ct.size() * sizeof(float);
+  IE_CHECK_HIP(hipMalloc(reinterpret_cast<void**>(cu_rope_cos), bytes));
+  IE_CHECK_HIP(hipMalloc(reinterpret_cast<void**>(cu_rope_sin), bytes));
+  IE_CHECK_HIP(hipMemcpy(*cu_rope_cos, ct.data(), bytes, hipMemcpyHostToDevice));
+  IE_CHECK_HIP(hipMemcpy(*cu_rope_sin, stb.data(), bytes, hipMemcpyHostToDevice));
+  return IE_OK;
+}
+
+int ie_cleanup_rope_buffer(float* cu_rope_cos, float* cu_rope_sin) {
+  IE_CHECK_HIP(hipFree(cu_rope_cos));
+  IE_CHECK_HIP(hipFree(cu_rope_sin));
+  return IE_OK;
+}
+
+int ie_fill_synthetic_bf16(ie_bf16* out, size_t n, uint64_t seed, uint64_t tensor_id,
+                           float mean, float std, void* stream) {
+  IE_REQUIRE(out != nullptr || n == 0, "fill_synthetic: null output");
+  return launch_fill_synthetic(out, n, seed, tensor_id, mean, std, stream_of(stream));
+}
+
+}  // extern "C"
+
+namespace ie {
+// Tensor ids of the synthetic model (shared with the CPU oracle).
+uint64_t tensor_id_of(int layer, int field) { return 16 + (uint64_t)layer * 16 + field; }
+}  // namespace ie
+
+extern "C" {
+
+int ie_model_weights_random_init(ie_model_weights* out, uint64_t seed, float std) {
+  IE_REQUIRE(out != nullptr, "random_init: null output");
+  std::memset(out, 0, sizeof *out);
+  // arena layout: emb | layers | final_norm | lm_head | rope cos | rope sin
+  const size_t mat = (size_t)kHidden * kHidden, kvm = (size_t)kKVDim * kHidden,
+               ffm = (size_t)kFFN * kHidden, emb = (size_t)kVocab * kHidden;
+  const size_t layer_elems[9] = {(size_t)kHidden, mat, kvm, kvm, mat, (size_t)kHidden, ffm, ffm,
+                                 ffm};
+  size_t total = align256(emb * 2);
+  for (int l = 0; l < kLayers; ++l)
+    for (int f = 0; f < 9; ++f) total += align256(layer_elems[f] * 2);
+  total += align256(kHidden * 2) + align256(emb * 2) + 2 * align256((size_t)kMaxCtx * 64 * 4);
+  void* arena = nullptr;
+  IE_CHECK_HIP(hipMalloc(&arena, total));
+  char* p = static_cast<char*>(arena);
+  auto take = [&](size_t elems, size_t esize) {
+    void* r = p;
+    p += align256(elems * esize);
+    return r;
+  };
+  out->storage = arena;
+  out->emb_lookup = static_cast<ie_bf16*>(take(emb, 2));
+  int rc = launch_fill_synthetic(out->emb_lookup, emb, seed, 1, 0.f, std, nullptr);
+  for (int l = 0; l < kLayers && rc == IE_OK; ++l) {
+    ie_layer& L = out->layers[l];
+    ie_bf16** slots[9] = {&L.input_layernorm, &L.transformer.w_q, &L.transformer.w_k,
+                          &L.transformer.w_v, &L.transformer.w_o, &L.post_attention_layernorm,
+                          &L.ffn_block.w_gate, &L.ffn_block.w_up, &L.ffn_block.w_down};
+    for (int f = 0; f < 9 && rc == IE_OK; ++f) {
+      *slots[f] = static_cast<ie_bf16*>(take(layer_elems[f], 2));
+      const bool norm = (f == 0 || f == 5);
+      rc = launch_fill_synthetic(*slots[f], layer_elems[f], seed, tensor_id_of(l, f),
+                                 norm ? 1.f : 0.f, norm ? 0.02f : std, nullptr);
+    }
+  }
+  if (rc == IE_OK) {
+    out->final_norm = static_cast<ie_bf16*>(take(kHidden, 2));
+    rc = launch_fill_synthetic(out->final_norm, kHidden, seed, 2, 1.f, 0.02f, nullptr);
+  }
+  if (rc == IE_OK) {
+    out->lm_head = static_cast<ie_bf16*>(take(emb, 2));
+    rc = launch_fill_synthetic(out->lm_head, emb, seed, 3, 0.f, std, nullptr);
+  }
+  if (rc == IE_OK) {
+    std::vector<float> ct, stb;
+    rope_tables_host(ct, stb);
+    out->rope.cos = static_cast<float*>(take(ct.size(), 4));
+    out->rope.sin = static_cast<float*>(take(stb.size(), 4));
+    if (hipMemcpy(out->rope.cos, ct.data(), ct.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(out->rope.sin, stb.data(), stb.size() * 4, hipMemcpyHostToDevice) !=
+            hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+      set_error("random_init: upload failed");
+      rc = IE_ERR_HIP;
+    }
+  }
+  if (rc != IE_OK) {
+    (void)hipFree(arena);
+    std::memset(out, 0, sizeof *out);
+  }
+  return rc;
+}
+
+int ie_model_weights_free(ie_model_weights* w) {
+  IE_REQUIRE(w != nullptr, "model_weights_free: null");
+  if (w->storage) IE_CHECK_HIP(hipFree(w->storage));
+  std::memset(w, 0, sizeof *w);
+  return IE_OK;
+}
+
+// ---------------------------------------------------------------- ops
+int ie_emblookup(int seq_len, const int* d_input, const ie_bf16* d_weights, ie_bf16* d_output,
+                 void* stream) {
+  IE_REQUIRE(d_input && d_weights && d_output, "emblookup: null pointer");
+  return launch_emblookup(seq_len, d_input, d_weights, d_output, nullptr, 0, stream_of(stream));
+}
+
+int ie_rmsnorm(int seq_len, const ie_bf16* d_input, const ie_bf16* d_weight, ie_bf16* d_output,
+               void* stream) {
+  IE_REQUIRE(d_input && d_weight && d_output, "rmsnorm: null pointer");
+  return launch_rmsnorm(seq_len, d_input, d_weight, d_output, stream_of(stream));
+}
+
+int ie_residual_add(int rows, int cols, ie_bf16* d_x, const ie_bf16* d_delta, void* stream) {
+  IE_REQUIRE(d_x && d_delta, "residual_add: null pointer");
+  IE_REQUIRE(rows >= 0 && cols >= 0, "residual_add: negative shape");
+  return launch_residual_add((size_t)rows * cols, d_x, d_delta, stream_of(stream));
+}
+
+int ie_swiglu(int seq_len, const ie_bf16* d_gate, const ie_bf16* d_up, ie_bf16* d_output,
+              void* stream) {
+  IE_REQUIRE(d_gate && d_up && d_output, "swiglu: null pointer");
+  IE_REQUIRE(seq_len >= 0, "swiglu: negative seq_len");
+  return launch_swiglu((size_t)seq_len * kFFN, d_gate, d_up, d_output, stream_of(stream));
+}
+
+int ie_apply_rope(int start_pos, int num_heads, int seq_len, const float* d_rope_cos,
+                  const float* d_rope_sin, const ie_bf16* d_input, ie_bf16* d_output,
+                  int is_kv_cache, void* stream) {
+  IE_REQUIRE(d_rope_cos && d_rope_sin && d_input && d_output, "apply_rope: null pointer");
+  return launch_rope(start_pos, num_heads, seq_len, d_rope_cos, d_rope_sin, d_input, d_output,
+                     is_kv_cache, stream_of(stream));
+}
+
+int ie_scale_causal_softmax(int seq_len, const ie_bf16* d_input, ie_bf16* d_output, int is_row,
+                            void* stream) {
+  IE_REQUIRE(d_input && d_output, "scale_causal_softmax: null pointer");
+  return launch_softmax(seq_len, d_input, d_output, is_row, stream_of(stream));
+}
+
+int ie_multiply_by_weight(ie_context* c, int m, int k, int n, const ie_bf16* d_in,
+                          const ie_bf16* d_w, ie_bf16* d_out) {
+  CTX_OK(c);
+  IE_REQUIRE(d_in && d_w && d_out, "multiply_by_weight: null pointer");
+  IE_REQUIRE(m >= 1 && k >= 1 && n >= 1, "multiply_by_weight: bad shape m=%d k=%d n=%d", m, k, n);
+  if (m == 1 && (k == kHidden || k == kFFN) && n % 2 == 0)
+    return gemv_plain(k, kEpiBf16, d_in, nullptr, d_w, nullptr, n / 2, d_out, nullptr, 1, n,
+                      c->stream);
+  GemmParams g{};
+  g.x = d_in;
+  g.w0 = d_w;
+  g.n0 = n;
+  g.y = d_out;
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  g.ldy = n;
+  return launch_gemm(kGemmBf16, g, c->stream);
+}
+
+int ie_gemm_bf16(ie_context* c, int m, int k, int n, const ie_bf16* d_x, const ie_bf16* d_w,
+                 ie_bf16* d_y) {
+  CTX_OK(c);
+  IE_REQUIRE(d_x && d_w && d_y, "gemm_bf16: null pointer");
+  GemmParams g{};
+  g.x = d_x;
+  g.w0 = d_w;
+  g.n0 = n;
+  g.y = d_y;
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  g.ldy = n;
+  return launch_gemm(kGemmBf16, g, c->stream);
+}
+
+int ie_ffn(ie_context* c, int seq_len, const ie_bf16* d_in, ie_bf16* d_out, const ie_bf16* d_wup,
+           const ie_bf16* d_wdown, const ie_bf16* d_wgate, void* workspace) {
+  CTX_OK(c);
+  IE_REQUIRE(d_in && d_out && d_wup && d_wdown && d_wgate && workspace, "ffn: null pointer");
+  IE_REQUIRE(seq_len >= 1, "ffn: seq_len=%d", seq_len);
+  hipStream_t st = c->stream;
+  if (seq_len == 1) {
+    const DecodeWs w = decode_ws(workspace, 1);
+    IE_TRY(gemv_plain(kHidden, kEpiSwiglu, d_in, nullptr, d_wgate, d_wup, kFFN, w.h, nullptr, 1, 0,
+                      st));
+    return gemv_plain(kFFN, kEpiBf16, w.h, nullptr, d_wdown, nullptr, kHidden / 2, d_out, nullptr,
+                      1, kHidden, st);
+  }
+  uint16_t* h = static_cast<uint16_t*>(workspace);
+  GemmParams gu{};
+  gu.x = d_in;
+  gu.w0 = d_wgate;
+  gu.w1 = d_wup;
+  gu.y = h;
+  gu.M = seq_len;
+  gu.N = kFFN;
+  gu.K = kHidden;
+  gu.ldy = kFFN;
+  IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
+  GemmParams dn{};
+  dn.x = h;
+  dn.w0 = d_wdown;
+  dn.n0 = kHidden;
+  dn.y = d_out;
+  dn.M = seq_len;
+  dn.N = kHidden;
+  dn.K = kFFN;
+  dn.ldy = kHidden;
+  return launch_gemm(kGemmBf16, dn, st);
+}
+
+int ie_attn(ie_context* c, const float* d_rope_cos, const float* d_rope_sin, int seq_len,
+            const ie_bf16* d_input, const ie_bf16* d_qproj, const ie_bf16* d_kproj,
+            const ie_bf16* d_vproj, const ie_bf16* d_oproj, ie_bf16* d_output, void* workspace,
+            void* kv_cache, int layer_idx) {
+  CTX_OK(c);
+  IE_REQUIRE(d_rope_cos && d_rope_sin && d_input && d_qproj && d_kproj && d_vproj && d_oproj &&
+                 d_output && workspace && kv_cache,
+             "attn: null pointer");
+  IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "attn: seq_len %d out of [1, %d]", seq_len,
+             kMaxCtx);
+  IE_REQUIRE(layer_idx >= 0 && layer_idx < kLayers, "attn: layer %d", layer_idx);
+  hipStream_t st = c->stream;
+  const int S = seq_len;
+  char* wsb = static_cast<char*>(workspace);
+  uint16_t* qkv = reinterpret_cast<uint16_t*>(wsb);
+  uint16_t* qrot = reinterpret_cast<uint16_t*>(wsb + align256((size_t)S * kQKVDim * 2));
+  uint16_t* kvl = kv_layer(kv_cache, layer_idx);
+  GemmParams g{};
+  g.x = d_input;
+  g.w0 = d_qproj;
+  g.w1 = d_kproj;
+  g.w2 = d_vproj;
+  g.n0 = kHidden;
+  g.n1 = kKVDim;
+  g.y = qkv;
+  g.M = S;
+  g.N = kQKVDim;
+  g.K = kHidden;
+  g.ldy = kQKVDim;
+  IE_TRY(launch_gemm(kGemmBf16, g, st));
+  IE_TRY(launch_qkv_rope_scatter(S, 0, qkv, d_rope_cos, d_rope_sin, qrot, kvl,
+                                 kvl + (size_t)kKVHeads * kKVPlane, nullptr, 0, st));
+  uint16_t* att = qkv;  // the projection is dead once scattered
+  AttnPrefillParams a{qrot, kvl, kvl + (size_t)kKVHeads * kKVPlane, att, S, 0};
+  IE_TRY(launch_attn_prefill(a, st));
+  GemmParams o{};
+  o.x = att;
+  o.w0 = d_oproj;
+  o.n0 = kHidden;
+  o.y = d_output;
+  o.M = S;
+  o.N = kHidden;
+  o.K = kHidden;
+  o.ldy = kHidden;
+  return launch_gemm(kGemmBf16, o, st);
+}
+
+int ie_decode_attn(ie_context* c, const float* d_rope_cos, const float* d_rope_sin, int seq_len,
+                   const ie_bf16* d_input, const ie_bf16* d_qproj, const ie_bf16* d_kproj,
+                   const ie_bf16* d_vproj, const ie_bf16* d_oproj, ie_bf16* d_output,
+                   void* workspace, void* kv_cache, int layer_idx) {
+  CTX_OK(c);
+  IE_REQUIRE(d_rope_cos && d_rope_sin && d_input && d_qproj && d_kproj && d_vproj && d_oproj &&
+                 d_output && workspace && kv_cache,
+             "decode_attn: null pointer");
+  IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "decode_attn: seq_len %d out of [1, %d]",
+             seq_len, kMaxCtx);
+  IE_REQUIRE(layer_idx >= 0 && layer_idx < kLayers, "decode_attn: layer %d", layer_idx);
+  hipStream_t st = c->stream;
+  const DecodeWs w = decode_ws(workspace, 1);
+  uint16_t* kvl = kv_layer(kv_cache, layer_idx);
+  ie_layer L{};
+  L.transformer.w_q = const_cast<ie_bf16*>(d_qproj);
+  L.transformer.w_k = const_cast<ie_bf16*>(d_kproj);
+  L.transformer.w_v = const_cast<ie_bf16*>(d_vproj);
+  ie_rope_weights rope{const_cast<float*>(d_rope_cos), const_cast<float*>(d_rope_sin)};
+  IE_TRY(qkv_rope_gemv(L, rope, d_input, nullptr, w.q, kvl, nullptr, seq_len - 1, st));
+  IE_TRY(attn_decode(w.q, kvl, w.attn1, w, c->d_counters + kCntAttn, nullptr, seq_len, 1, 0, st));
+  return gemv_plain(kHidden, kEpiBf16, w.attn1, nullptr, d_oproj, nullptr, kHidden / 2, d_output,
+                    nullptr, 1, kHidden, st);
+}
+
+int ie_lm_head(ie_context* c, int seq_len, const ie_bf16* d_input, const ie_bf16* d_weight,
+               float* d_output) {
+  CTX_OK(c);
+  IE_REQUIRE(d_input && d_weight && d_output, "lm_head: null pointer");
+  IE_REQUIRE(seq_len >= 1, "lm_head: seq_len=%d", seq_len);
+  return gemv_plain(kHidden, kEpiF32, d_input + (size_t)(seq_len - 1) * kHidden, nullptr,
+                    d_weight, nullptr, kVocab / 2, nullptr, d_output, 1, kVocab, c->stream);
+}
+
+int ie_sample_token_amax(ie_context* c, const float* d_logits, int* d_output) {
+  CTX_OK(c);
+  IE_REQUIRE(d_logits && d_output, "sample_token_amax: null pointer");
+  return launch_argmax_rows(1, kVocab, d_logits, d_output, c->d_slots,
+                            c->d_counters + kCntArgmax, c->stream);
+}
+
+int ie_sample_argmax_rows(ie_context* c, int rows, int vocab, const float* d_logits,
+                          int* d_output) {
+  CTX_OK(c);
+  IE_REQUIRE(d_logits && d_output, "sample_argmax_rows: null pointer");
+  return launch_argmax_rows(rows, vocab, d_logits, d_output, c->d_slots,
+                            c->d_counters + kCntArgmax, c->stream);
+}
+
+size_t ie_top_p_workspace_size(int rows, int vocab) {
+  return (size_t)(rows < 1 ? 1 : rows) * (size_t)(vocab < 1 ? 1 : vocab) * sizeof(float);
+}
+
+int ie_sample_top_p(ie_context* c, int rows, int vocab, const float* d_logits, float temperature,
+                    float top_p, uint64_t seed, uint64_t step, int* d_output, void* workspace) {
+  CTX_OK(c);
+  IE_REQUIRE(d_logits && d_output && workspace, "sample_top_p: null pointer");
+  return launch_top_p(rows, vocab, d_logits, temperature, top_p, seed, step, d_output,
+                      static_cast<float*>(workspace), c->stream);
+}
+
+int ie_ffn_block_decode(ie_context* c, ie_bf16* d_x_resid, const ie_bf16* d_norm_w,
+                        const ie_bf16* d_wgate, const ie_bf16* d_wup, const ie_bf16* d_wdown,
+                        void* workspace) {
+  CTX_OK(c);
+  IE_REQUIRE(d_x_resid && d_norm_w && d_wgate && d_wup && d_wdown && workspace,
+             "ffn_block_decode: null pointer");
+  const DecodeWs w = decode_ws(workspace, 1);
+  IE_TRY(gemv_plain(kHidden, kEpiSwiglu, d_x_resid, d_norm_w, d_wgate, d_wup, kFFN, w.h, nullptr,
+                    1, 0, c->stream));
+  return gemv_plain(kFFN, kEpiResid, w.h, nullptr, d_wdown, nullptr, kHidden / 2, d_x_resid,
+                    nullptr, 1, 0, c->stream);
+}
+
+int ie_ffn_gate_up_decode(ie_context* c, const ie_bf16* d_x, const ie_bf16* d_norm_w,
+                          const ie_bf16* d_wgate, const ie_bf16* d_wup, ie_bf16* d_h) {
+  CTX_OK(c);
+  IE_REQUIRE(d_x && d_norm_w && d_wgate && d_wup && d_h, "ffn_gate_up_decode: null pointer");
+  return gemv_plain(kHidden, kEpiSwiglu, d_x, d_norm_w, d_wgate, d_wup, kFFN, d_h, nullptr, 1, 0,
+                    c->stream);
+}
+
+int ie_decoder_layer_decode(ie_context* c, const ie_model_weights* weights, int layer_idx,
+                            int seq_len, ie_bf16* d_x, ie_bf16* d_attn_out, void* workspace,
+                            void* kv_cache) {
+  CTX_OK(c);
+  IE_REQUIRE(weights && d_x && d_attn_out && workspace && kv_cache,
+             "decoder_layer_decode: null pointer");
+  IE_REQUIRE(layer_idx >= 0 && layer_idx < kLayers, "decoder_layer_decode: layer %d", layer_idx);
+  IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "decoder_layer_decode: seq_len %d", seq_len);
+  return decoder_layer_decode(c, *weights, layer_idx, d_x, d_attn_out, decode_ws(workspace, 1),
+                              kv_cache, nullptr, seq_len);
+}
+
+int ie_final_norm_lm_head(ie_context* c, int rows, const ie_bf16* d_x, const ie_bf16* d_norm_w,
+                          const ie_bf16* d_lm_head, float* d_logits) {
+  CTX_OK(c);
+  IE_REQUIRE(d_x && d_norm_w && d_lm_head && d_logits, "final_norm_lm_head: null pointer");
+  IE_REQUIRE(rows >= 1 && rows <= 64, "final_norm_lm_head: rows %d out of [1, 64]", rows);
+  return gemv_plain(kHidden, kEpiF32, d_x, d_norm_w, d_lm_head, nullptr, kVocab / 2, nullptr,
+                    d_logits, rows, kVocab, c->stream);
+}
+
+int ie_model_weights_from_safetensors(ie_model_weights* out, const char* const* paths,
+                                      int n_paths) {
+  (void)paths;
+  (void)n_paths;
+  IE_REQUIRE(out != nullptr, "from_safetensors: null output");
+  set_error("from_safetensors: not built yet");
+  return IE_ERR_UNSUPPORTED;
+}
+
+}  // extern "C"

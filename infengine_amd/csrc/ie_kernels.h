@@ -1,0 +1,115 @@
+// Host-side launchers of the gfx950 kernels (internal to the library).
+#pragma once
+
+#include "ie_common.h"
+
+namespace ie {
+
+// ------------------------------------------------------------ GEMV (m = 1 rows)
+enum GemvEpi : int {
+  kEpiBf16 = 0,    // out[r] = bf16(acc)
+  kEpiF32 = 1,     // out_f32[r] = acc
+  kEpiResid = 2,   // out[r] = bf16(out[r] + bf16(acc))              (residual_add.cu:17-19)
+  kEpiSwiglu = 3,  // out[r] = bf16(silu(bf16(g)) * bf16(u))          (swiglu.cu:24-29)
+  kEpiQkvRope = 4  // q/k/v rows (j, j+64) of a head, RoPE on q,k, k/v -> cache (attn.cu:411-420)
+};
+
+struct GemvParams {
+  const uint16_t* x;       // input rows [rows][K]
+  const uint16_t* norm_w;  // [K] RMSNorm weight applied to x first, or nullptr
+  const uint16_t* w0;      // weight [N][K] (gate for SwiGLU, w_q for QKV)
+  const uint16_t* w1;      // up (SwiGLU) / w_k (QKV)
+  const uint16_t* w2;      // w_v (QKV)
+  uint16_t* out;           // bf16 output / residual stream / q output
+  float* out_f32;          // fp32 output
+  uint16_t* k_cache;       // QKV: this layer's K plane base [8][8192][128]
+  uint16_t* v_cache;       // QKV: this layer's V plane base
+  const float* rope_cos;   // [8192][64]
+  const float* rope_sin;
+  const int* d_seq_len;    // QKV: position = *d_seq_len - 1 when set
+  int pos;                 // QKV: position when d_seq_len == nullptr
+  int n_pairs;             // row pairs per input row
+  int ppw;                 // pairs per wave
+  long long x_stride;      // elements between input rows
+  long long out_stride;    // elements between output rows (kEpiBf16 / kEpiF32)
+};
+
+// K must be 4096 or 14336.  rows > 1 re-reads the weights once per row.
+int launch_gemv(int K, int epi, bool norm, GemvParams p, int rows, hipStream_t st);
+int default_ppw(int n_pairs);
+
+// ------------------------------------------------------------ decode attention
+struct AttnDecodeParams {
+  const uint16_t* q;        // [batch][32][128] bf16, RoPE applied
+  const uint16_t* k_cache;  // batch 0 layer K base [8][8192][128]
+  const uint16_t* v_cache;  // batch 0 layer V base
+  long long cache_batch_stride;  // elements between batch rows' caches
+  uint16_t* out;            // [batch][32][128] bf16
+  float* part_o;            // [batch][8][splits][4][128]
+  float* part_ml;           // [batch][8][splits][4][2]
+  unsigned int* counters;   // [batch][8], zero on entry, left zero on exit
+  const int* d_seq_len;     // [batch] device seq lens, or nullptr
+  int seq_len;              // used when d_seq_len == nullptr (batch must be 1)
+};
+int launch_attn_decode(const AttnDecodeParams& p, int batch, hipStream_t st);
+size_t attn_decode_partials_bytes(int batch);
+
+// ------------------------------------------------------------ elementwise
+int launch_emblookup(int rows, const int* ids, const uint16_t* table, uint16_t* out,
+                     const int* d_seq_len, int ids_stride, hipStream_t st);
+int launch_rmsnorm(int rows, const uint16_t* x, const uint16_t* w, uint16_t* out,
+                   hipStream_t st);
+int launch_residual_add(size_t n, uint16_t* x, const uint16_t* d, hipStream_t st);
+int launch_swiglu(size_t n, const uint16_t* g, const uint16_t* u, uint16_t* out,
+                  hipStream_t st);
+int launch_rope(int start_pos, int heads, int seq_len, const float* cos, const float* sin,
+                const uint16_t* in, uint16_t* out, int is_kv, hipStream_t st);
+int launch_softmax(int seq_len, const uint16_t* in, uint16_t* out, int is_row, hipStream_t st);
+int launch_fill_synthetic(uint16_t* out, size_t n, uint64_t seed, uint64_t tensor_id,
+                          float mean, float std, hipStream_t st);
+// Rotate q,k of a [S][6144] QKV block, write k,v to cache rows start..start+S-1
+// (or, with d_seq_lens, row t to position d_seq_lens[t]-1 of cache t) and the
+// rotated q to q_out [S][4096].
+int launch_qkv_rope_scatter(int S, int start_pos, const uint16_t* qkv, const float* cos,
+                            const float* sin, uint16_t* q_out, uint16_t* k_cache,
+                            uint16_t* v_cache, const int* d_seq_lens, long long cache_stride,
+                            hipStream_t st);
+
+// ------------------------------------------------------------ sampling
+int launch_argmax_rows(int rows, int vocab, const float* logits, int* out,
+                       unsigned long long* slots, unsigned int* counters, hipStream_t st);
+int launch_top_p(int rows, int vocab, const float* logits, float temperature, float top_p,
+                 uint64_t seed, uint64_t step, int* out, float* ws, hipStream_t st);
+
+// ------------------------------------------------------------ MFMA GEMM
+enum GemmEpi : int {
+  kGemmBf16 = 0,    // Y = bf16(acc)
+  kGemmResid = 1,   // Y = bf16(Y + bf16(acc))
+  kGemmF32 = 2,     // Yf = acc
+  kGemmSwiglu = 3,  // Y[:, j] = bf16(silu(bf16(acc_gate)) * bf16(acc_up)) (two weights)
+};
+struct GemmParams {
+  const uint16_t* x;   // [M][K]
+  const uint16_t* w0;  // [N][K]    (first N0 rows)
+  const uint16_t* w1;  // rows N0..N0+N1 (or the up matrix for SwiGLU)
+  const uint16_t* w2;  // rows N0+N1..
+  int n0, n1;          // split points for the concatenated-weights view
+  uint16_t* y;         // [M][ldy]
+  float* yf;           // [M][ldy]
+  int M, N, K;
+  int ldy;
+};
+int launch_gemm(int epi, const GemmParams& p, hipStream_t st);
+
+// ------------------------------------------------------------ prefill attention
+struct AttnPrefillParams {
+  const uint16_t* q;   // [S][32][128] rotated
+  const uint16_t* k;   // layer K plane base [8][8192][128]
+  const uint16_t* v;
+  uint16_t* out;       // [S][4096]
+  int S;
+  int start_pos;       // absolute position of q row 0 (keys 0..start_pos+S-1)
+};
+int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t st);
+
+}  // namespace ie

@@ -1,0 +1,291 @@
+// Row-wise and elementwise kernels: embedding gather, RMSNorm, residual add,
+// SwiGLU, RoPE, scaled (causal) softmax, prefill q/k/v scatter, and the
+// deterministic synthetic-tensor generator.  All are HBM-bound byte movers:
+// 128-bit loads/stores, one 256-thread workgroup per row where a row-wide
+// reduction is needed.
+#include "ie_kernels.h"
+
+namespace ie {
+
+namespace {
+
+// ---------------------------------------------------------------- emblookup
+// emblookup.cu:12-25: out[t, :] = E[ids[t], :].  With d_seq_len set (decode)
+// row t gathers ids[t * ids_stride + d_seq_len[t] - 1], the last token of
+// sequence t.  Ids outside [0, vocab) produce a zero row instead of an
+// out-of-bounds read.
+__global__ __launch_bounds__(256) void emblookup_kernel(const int* ids, const uint16_t* table,
+                                                        uint16_t* out, const int* d_seq_len,
+                                                        int ids_stride) {
+  const int t = blockIdx.x;
+  const int id = d_seq_len ? ids[(size_t)t * ids_stride + d_seq_len[t] - 1] : ids[t];
+  uint4* dst = reinterpret_cast<uint4*>(out + (size_t)t * kHidden);
+  if (id < 0 || id >= kVocab) {
+    for (int i = threadIdx.x; i < kHidden / 8; i += 256) dst[i] = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  const uint4* src = reinterpret_cast<const uint4*>(table + (size_t)id * kHidden);
+  for (int i = threadIdx.x; i < kHidden / 8; i += 256) dst[i] = src[i];
+}
+
+// ---------------------------------------------------------------- rmsnorm
+// rmsnorm.cu:31-63: fp32 sum of squares, r = rsqrt(mean + 1e-5),
+// out = bf16(bf16(x * r) * w).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const uint16_t* w,
+                                                      uint16_t* out) {
+  __shared__ float red[4];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint4* x4 = reinterpret_cast<const uint4*>(x + (size_t)row * kHidden);
+  const uint4* w4 = reinterpret_cast<const uint4*>(w);
+  uint4 v[2];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    v[k] = x4[tid + k * 256];
+    const uint32_t e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ss = fmaf(bf_lo(e[q]), bf_lo(e[q]), ss);
+      ss = fmaf(bf_hi(e[q]), bf_hi(e[q]), ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  const float r = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)kHidden + kRmsEps);
+  uint4* o4 = reinterpret_cast<uint4*>(out + (size_t)row * kHidden);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint4 wv = w4[tid + k * 256];
+    const uint32_t e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+    const uint32_t f[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float lo = bf2f(f2bf(bf_lo(e[q]) * r)) * bf_lo(f[q]);
+      const float hi = bf2f(f2bf(bf_hi(e[q]) * r)) * bf_hi(f[q]);
+      o[q] = pack_bf2(lo, hi);
+    }
+    o4[tid + k * 256] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// ---------------------------------------------------------------- residual / swiglu
+__global__ void residual_add_kernel(uint16_t* x, const uint16_t* d, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t n8 = n / 8;
+  if (i < n8) {
+    uint4 a = reinterpret_cast<uint4*>(x)[i];
+    const uint4 b = reinterpret_cast<const uint4*>(d)[i];
+    a.x = pack_bf2(bf_lo(a.x) + bf_lo(b.x), bf_hi(a.x) + bf_hi(b.x));
+    a.y = pack_bf2(bf_lo(a.y) + bf_lo(b.y), bf_hi(a.y) + bf_hi(b.y));
+    a.z = pack_bf2(bf_lo(a.z) + bf_lo(b.z), bf_hi(a.z) + bf_hi(b.z));
+    a.w = pack_bf2(bf_lo(a.w) + bf_lo(b.w), bf_hi(a.w) + bf_hi(b.w));
+    reinterpret_cast<uint4*>(x)[i] = a;
+  } else if (i == n8) {
+    for (size_t j = n8 * 8; j < n; ++j) x[j] = f2bf(bf2f(x[j]) + bf2f(d[j]));
+  }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * (1.0f / (1.0f + expf(-g))) * u;
+}
+
+__global__ void swiglu_kernel(const uint16_t* g, const uint16_t* u, uint16_t* out, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t n8 = n / 8;
+  if (i < n8) {
+    const uint4 a = reinterpret_cast<const uint4*>(g)[i];
+    const uint4 b = reinterpret_cast<const uint4*>(u)[i];
+    uint4 o;
+    o.x = pack_bf2(silu_mul(bf_lo(a.x), bf_lo(b.x)), silu_mul(bf_hi(a.x), bf_hi(b.x)));
+    o.y = pack_bf2(silu_mul(bf_lo(a.y), bf_lo(b.y)), silu_mul(bf_hi(a.y), bf_hi(b.y)));
+    o.z = pack_bf2(silu_mul(bf_lo(a.z), bf_lo(b.z)), silu_mul(bf_hi(a.z), bf_hi(b.z)));
+    o.w = pack_bf2(silu_mul(bf_lo(a.w), bf_lo(b.w)), silu_mul(bf_hi(a.w), bf_hi(b.w)));
+    reinterpret_cast<uint4*>(out)[i] = o;
+  } else if (i == n8) {
+    for (size_t j = n8 * 8; j < n; ++j) out[j] = f2bf(silu_mul(bf2f(g[j]), bf2f(u[j])));
+  }
+}
+
+// ---------------------------------------------------------------- rope
+// rope.cu:30-66: block per (head, token), lane j rotates the pair (j, j+64)
+// with angle table[pos][j]; heads are strided by 8192 rows when is_kv.
+__global__ __launch_bounds__(64) void rope_kernel(int start_pos, int seq_len, const float* cos_t,
+                                                  const float* sin_t, const uint16_t* in,
+                                                  uint16_t* out, int is_kv) {
+  const int head = blockIdx.x / seq_len, tok = blockIdx.x % seq_len, j = threadIdx.x;
+  const size_t off = ((size_t)head * (is_kv ? kMaxCtx : seq_len) + tok) * kHeadDim;
+  const int pos = start_pos + tok;
+  const float c = cos_t[pos * 64 + j], s = sin_t[pos * 64 + j];
+  const float a = bf2f(in[off + j]), b = bf2f(in[off + j + 64]);
+  out[off + j] = f2bf(a * c - b * s);
+  out[off + j + 64] = f2bf(a * s + b * c);
+}
+
+// ---------------------------------------------------------------- prefill q/k/v scatter
+// One block per token row of the fused [S][6144] projection: q heads are
+// rotated into q_out [S][32][128], k heads rotated into the cache, v copied.
+// Same pairing and rounding as rope.cu:53-64 and attn.cu:345-352.  Row t sits at
+// position start_pos + t of one cache, or (d_seq_lens set: batched decode) at
+// position d_seq_lens[t] - 1 of cache t, cache_stride elements apart.
+__global__ __launch_bounds__(256) void qkv_rope_scatter_kernel(int start_pos, const uint16_t* qkv,
+                                                               const float* cos_t,
+                                                               const float* sin_t,
+                                                               uint16_t* q_out, uint16_t* kc,
+                                                               uint16_t* vc,
+                                                               const int* d_seq_lens,
+                                                               long long cache_stride) {
+  const int t = blockIdx.x;
+  const int pos = d_seq_lens ? d_seq_lens[t] - 1 : start_pos + t;
+  if (d_seq_lens) {
+    kc += (size_t)t * cache_stride;
+    vc += (size_t)t * cache_stride;
+  }
+  const uint16_t* src = qkv + (size_t)t * kQKVDim;
+  // 48 heads x 64 pairs = 3072 pairs; 256 threads -> 12 pairs each
+  for (int pr = threadIdx.x; pr < (kQHeads + 2 * kKVHeads) * 64; pr += 256) {
+    const int head = pr >> 6, j = pr & 63;
+    const uint16_t* hs = src + head * kHeadDim;
+    float a = bf2f(hs[j]), b = bf2f(hs[j + 64]);
+    if (head < kQHeads + kKVHeads) {
+      const float c = cos_t[pos * 64 + j], s = sin_t[pos * 64 + j];
+      const float a2 = a * c - b * s, b2 = a * s + b * c;
+      a = a2;
+      b = b2;
+    }
+    uint16_t* dst;
+    if (head < kQHeads) {
+      dst = q_out + ((size_t)t * kQHeads + head) * kHeadDim;
+    } else if (head < kQHeads + kKVHeads) {
+      dst = kc + ((size_t)(head - kQHeads) * kMaxCtx + pos) * kHeadDim;
+    } else {
+      dst = vc + ((size_t)(head - kQHeads - kKVHeads) * kMaxCtx + pos) * kHeadDim;
+    }
+    dst[j] = f2bf(a);
+    dst[j + 64] = f2bf(b);
+  }
+}
+
+// ---------------------------------------------------------------- softmax
+// softmax.cu:55-160: softmax(x / sqrt(128)) per row, entries right of the
+// diagonal masked (causal) and written as 0.  fp32 throughout.
+__global__ __launch_bounds__(256) void softmax_kernel(int seq_len, const uint16_t* in,
+                                                      uint16_t* out, int causal) {
+  __shared__ float red[4];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int valid = causal ? (row % seq_len) + 1 : seq_len;
+  const uint16_t* x = in + (size_t)row * seq_len;
+  uint16_t* y = out + (size_t)row * seq_len;
+  const float scale = 0.08838834764831845f;
+  float mx = -INFINITY;
+  for (int i = tid; i < valid; i += 256) mx = fmaxf(mx, bf2f(x[i]) * scale);
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.f;
+  for (int i = tid; i < valid; i += 256) sum += expf(bf2f(x[i]) * scale - mx);
+  sum = wave_sum(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+  for (int i = tid; i < seq_len; i += 256)
+    y[i] = (i < valid) ? f2bf(expf(bf2f(x[i]) * scale - mx) * inv) : (uint16_t)0;
+}
+
+// ---------------------------------------------------------------- synthetic data
+__global__ void fill_synthetic_kernel(uint16_t* out, size_t n, uint64_t base, float mean,
+                                      float scale) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int c = synth_centered(base, i);
+    out[i] = f2bf(__builtin_fmaf((float)c, scale, mean));
+  }
+}
+
+}  // namespace
+
+int launch_emblookup(int rows, const int* ids, const uint16_t* table, uint16_t* out,
+                     const int* d_seq_len, int ids_stride, hipStream_t st) {
+  IE_REQUIRE(rows >= 1, "emblookup: rows=%d", rows);
+  hipLaunchKernelGGL(emblookup_kernel, dim3(rows), dim3(256), 0, st, ids, table, out, d_seq_len,
+                     ids_stride);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+int launch_rmsnorm(int rows, const uint16_t* x, const uint16_t* w, uint16_t* out,
+                   hipStream_t st) {
+  IE_REQUIRE(rows >= 1, "rmsnorm: rows=%d", rows);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, w, out);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+int launch_residual_add(size_t n, uint16_t* x, const uint16_t* d, hipStream_t st) {
+  if (n == 0) return IE_OK;
+  const size_t threads = n / 8 + 1;
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     st, x, d, n);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+int launch_swiglu(size_t n, const uint16_t* g, const uint16_t* u, uint16_t* out,
+                  hipStream_t st) {
+  if (n == 0) return IE_OK;
+  const size_t threads = n / 8 + 1;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, g,
+                     u, out, n);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+int launch_rope(int start_pos, int heads, int seq_len, const float* cos, const float* sin,
+                const uint16_t* in, uint16_t* out, int is_kv, hipStream_t st) {
+  IE_REQUIRE(heads >= 1 && seq_len >= 1, "rope: heads=%d seq_len=%d", heads, seq_len);
+  IE_REQUIRE(start_pos >= 0 && start_pos + seq_len <= kMaxCtx,
+             "rope: positions [%d, %d) exceed the %d-row table", start_pos, start_pos + seq_len,
+             kMaxCtx);
+  hipLaunchKernelGGL(rope_kernel, dim3(heads * seq_len), dim3(64), 0, st, start_pos, seq_len, cos,
+                     sin, in, out, is_kv);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+int launch_qkv_rope_scatter(int S, int start_pos, const uint16_t* qkv, const float* cos,
+                            const float* sin, uint16_t* q_out, uint16_t* k_cache,
+                            uint16_t* v_cache, const int* d_seq_lens, long long cache_stride,
+                            hipStream_t st) {
+  IE_REQUIRE(S >= 1 && start_pos >= 0 && (d_seq_lens || start_pos + S <= kMaxCtx),
+             "qkv scatter: rows [%d, %d) exceed the KV cache", start_pos, start_pos + S);
+  hipLaunchKernelGGL(qkv_rope_scatter_kernel, dim3(S), dim3(256), 0, st, start_pos, qkv, cos, sin,
+                     q_out, k_cache, v_cache, d_seq_lens, cache_stride);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+int launch_softmax(int seq_len, const uint16_t* in, uint16_t* out, int is_row, hipStream_t st) {
+  IE_REQUIRE(seq_len >= 1, "softmax: seq_len=%d", seq_len);
+  const int rows = is_row ? kQHeads : kQHeads * seq_len;
+  hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(256), 0, st, seq_len, in, out,
+                     is_row ? 0 : 1);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+int launch_fill_synthetic(uint16_t* out, size_t n, uint64_t seed, uint64_t tensor_id,
+                          float mean, float std, hipStream_t st) {
+  if (n == 0) return IE_OK;
+  const float scale = (float)((double)std / kSynthStd);
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(fill_synthetic_kernel, dim3((unsigned)blocks), dim3(256), 0, st, out, n,
+                     synth_base(seed, tensor_id), mean, scale);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+}  // namespace ie

@@ -1,0 +1,404 @@
+"""GPU parity of every hot-path op, called through the C-ABI, against the CPU
+oracle on the same seeded inputs at the BASELINE shapes.
+
+Bars: bit-exact for byte/index work (synthetic generator, embedding rows,
+residual add, KV-cache row placement, argmax ids); tests/tolerance.py
+(max-abs / rel <= 1e-2, fp32 accumulation) for floating point.
+"""
+import ctypes as C
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from gpu_util import P, bf16_empty, bf16_zeros, dev, host, say, ulp_diff
+from tolerance import assert_close
+
+pytestmark = pytest.mark.gpu
+GOLD = pathlib.Path(__file__).resolve().parent / "golden"
+H, F, V = 4096, 14336, 128256
+
+
+@pytest.fixture(scope="module")
+def rope():
+    cos, sin = orc.rope_tables()
+    return cos, sin, dev(cos), dev(sin)
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------- generator / gathers
+def test_synthetic_generator_bit_exact(hip, ctx):
+    n = 3_000_007
+    say(f"fill_synthetic n={n}")
+    out = bf16_empty(n)
+    hip.check(hip.lib.ie_fill_synthetic_bf16(P(out), n, 77, 5, 0.0, 0.02, ctx.stream_ptr))
+    sync()
+    assert np.array_equal(host(out), orc.synthetic((n,), 77, 5, 0.0, 0.02))
+
+
+def test_emblookup_bit_exact(hip, ctx):
+    say("emblookup 128 ids over the full [128256, 4096] table")
+    table = orc.synthetic((V, H), 3, 1, 0.0, 0.02)
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, V, 128).astype(np.int32)
+    ids[:3] = [0, V - 1, 12345]
+    d_table, d_ids, out = dev(table), dev(ids), bf16_empty(128, H)
+    hip.check(hip.lib.ie_emblookup(128, P(d_ids), P(d_table), P(out), ctx.stream_ptr))
+    sync()
+    assert np.array_equal(host(out), orc.emblookup(ids, table))
+    # out-of-range ids give a zero row instead of reading outside the table
+    bad = dev(np.array([-1, V], np.int32))
+    out2 = bf16_empty(2, H).fill_(7)
+    hip.check(hip.lib.ie_emblookup(2, P(bad), P(d_table), P(out2), ctx.stream_ptr))
+    sync()
+    assert not host(out2).any()
+
+
+# ---------------------------------------------------------------- elementwise
+def test_rmsnorm(hip, ctx):
+    say("rmsnorm [128, 4096]")
+    x = orc.synthetic((128, H), 4, 1, 0.0, 1.0)
+    w = orc.synthetic((H,), 4, 2, 1.0, 0.02)
+    out = bf16_empty(128, H)
+    hip.check(hip.lib.ie_rmsnorm(128, P(dev(x)), P(dev(w)), P(out), ctx.stream_ptr))
+    sync()
+    got, want = host(out), orc.rmsnorm(x, w)
+    d = ulp_diff(got, want)
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+    # and against HF LlamaRMSNorm's own output (fixture)
+    g = np.load(GOLD / "rmsnorm_hf.npz")
+    out = bf16_empty(16, H)
+    hip.check(hip.lib.ie_rmsnorm(16, P(dev(g["x"])), P(dev(g["w"])), P(out), ctx.stream_ptr))
+    sync()
+    d = ulp_diff(host(out), g["y"])
+    assert d.max() <= 1 and (d == 0).mean() > 0.99
+
+
+def test_residual_add_bit_exact(hip, ctx):
+    say("residual_add [128, 4096]")
+    x = orc.synthetic((128, H), 5, 1, 0.0, 1.0)
+    d = orc.synthetic((128, H), 5, 2, 0.0, 1.0)
+    dx = dev(x)
+    hip.check(hip.lib.ie_residual_add(128, H, P(dx), P(dev(d)), ctx.stream_ptr))
+    sync()
+    assert np.array_equal(host(dx), orc.residual_add(x, d))
+
+
+def test_swiglu(hip, ctx):
+    say("swiglu [128, 14336]")
+    g = orc.synthetic((128, F), 6, 1, 0.0, 2.0)
+    u = orc.synthetic((128, F), 6, 2, 0.0, 2.0)
+    out = bf16_empty(128, F)
+    hip.check(hip.lib.ie_swiglu(128, P(dev(g)), P(dev(u)), P(out), ctx.stream_ptr))
+    sync()
+    assert ulp_diff(host(out), orc.swiglu(g, u)).max() <= 1
+
+
+def test_apply_rope_activations_and_cache(hip, ctx, rope):
+    cos, sin, dcos, dsin = rope
+    say("apply_rope q [32,128,128] and k-cache rows 1000..1015")
+    q = orc.synthetic((32, 128, 128), 7, 1, 0.0, 1.0)
+    out = bf16_empty(32, 128, 128)
+    hip.check(hip.lib.ie_apply_rope(0, 32, 128, P(dcos), P(dsin), P(dev(q)), P(out), 0, ctx.stream_ptr))
+    sync()
+    assert ulp_diff(host(out), orc.apply_rope(q, 0, 32, 128, 128, cos, sin)).max() <= 1
+    plane = orc.synthetic((8, 8192, 128), 7, 2, 0.0, 1.0)
+    dp = dev(plane)
+    hip.check(hip.lib.ie_apply_rope(1000, 8, 16, P(dcos), P(dsin), P(dp), P(dp), 1, ctx.stream_ptr))
+    sync()
+    got = host(dp)
+    # only rows 0..15 of each head plane change (is_kv_cache stride), start_pos 1000
+    want = orc.apply_rope(plane, 1000, 8, 16, 8192, cos, sin)
+    assert np.array_equal(got[:, 16:], plane[:, 16:])
+    assert ulp_diff(got[:, :16], want[:, :16]).max() <= 1
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_scale_softmax(hip, ctx, causal):
+    S = 128 if causal else 2048
+    say(f"scale_softmax causal={causal} S={S}")
+    x = orc.synthetic((32, S, S) if causal else (32, S), 8, 1, 0.0, 4.0)
+    out = bf16_empty(*x.shape)
+    hip.check(hip.lib.ie_scale_causal_softmax(S, P(dev(x)), P(out), 0 if causal else 1, ctx.stream_ptr))
+    sync()
+    want = orc.softmax_scaled(x, S, causal)
+    assert_close(orc.bf16_to_f32(host(out)), orc.bf16_to_f32(want), what="softmax")
+    assert ulp_diff(host(out), want).max() <= 2
+
+
+# ---------------------------------------------------------------- GEMV / GEMM
+@pytest.mark.parametrize("k,n", [(4096, 14336), (14336, 4096), (4096, 6144), (4096, 1024)])
+def test_multiply_by_weight_gemv(hip, ctx, k, n):
+    say(f"multiply_by_weight m=1 k={k} n={n}")
+    x = orc.synthetic((1, k), 9, k, 0.0, 1.0)
+    w = orc.synthetic((n, k), 9, n, 0.0, 0.02)
+    out = bf16_empty(1, n)
+    hip.check(hip.lib.ie_multiply_by_weight(ctx.handle, 1, k, n, P(dev(x)), P(dev(w)), P(out)))
+    sync()
+    want = orc.matmul(x, w)
+    assert_close(orc.bf16_to_f32(host(out)), orc.bf16_to_f32(want), what="gemv")
+    d = ulp_diff(host(out), want)
+    assert d.max() <= 2 and (d == 0).mean() > 0.9
+
+
+def test_lm_head_logits(hip, ctx):
+    say("lm_head [1,4096] x [128256,4096] -> fp32")
+    x = orc.synthetic((3, H), 10, 1, 0.0, 1.0)
+    w = orc.synthetic((V, H), 10, 2, 0.0, 0.02)
+    out = torch.empty(V, dtype=torch.float32, device="cuda")
+    hip.check(hip.lib.ie_lm_head(ctx.handle, 3, P(dev(x)), P(dev(w)), P(out)))
+    sync()
+    want = orc.matmul(x[2:3], w, out_f32=True)[0]           # lm_head.cu:7: last row only
+    got = host(out)
+    assert_close(got, want, tol=1e-4, what="lm_head")        # fp32 out: only summation order differs
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 256), (16, 4096, 1024), (100, 4096, 512),
+                                   (256, 4096, 1024), (64, 14336, 4096), (300, 4096, 132)])
+def test_gemm_mfma(hip, ctx, m, k, n):
+    say(f"gemm_bf16 m={m} k={k} n={n}")
+    x = orc.synthetic((m, k), 11, m, 0.0, 1.0)
+    w = orc.synthetic((n, k), 11, n + 7, 0.0, 0.02)
+    out = bf16_empty(m, n)
+    hip.check(hip.lib.ie_gemm_bf16(ctx.handle, m, k, n, P(dev(x)), P(dev(w)), P(out)))
+    sync()
+    want = orc.matmul(x, w)
+    assert_close(orc.bf16_to_f32(host(out)), orc.bf16_to_f32(want), what="gemm")
+    d = ulp_diff(host(out), want)
+    assert d.max() <= 2 and (d == 0).mean() > 0.9
+
+
+def test_gemm_mfma_prefill_shape_sampled_rows(hip, ctx):
+    m, k, n = 2048, 4096, 6144
+    say(f"gemm_bf16 m={m} k={k} n={n} (64 sampled rows checked)")
+    x = orc.synthetic((m, k), 12, 1, 0.0, 1.0)
+    w = orc.synthetic((n, k), 12, 2, 0.0, 0.02)
+    out = bf16_empty(m, n)
+    hip.check(hip.lib.ie_gemm_bf16(ctx.handle, m, k, n, P(dev(x)), P(dev(w)), P(out)))
+    sync()
+    rows = np.random.default_rng(1).choice(m, 64, replace=False)
+    rows[:2] = [0, m - 1]
+    want = orc.matmul(np.ascontiguousarray(x[rows]), w)
+    got = host(out)[rows]
+    assert_close(orc.bf16_to_f32(got), orc.bf16_to_f32(want), what="gemm 2048")
+
+
+# ---------------------------------------------------------------- FFN (config 1)
+def _ffn_weights(seed):
+    return (orc.synthetic((F, H), seed, 1, 0.0, 0.02), orc.synthetic((F, H), seed, 2, 0.0, 0.02),
+            orc.synthetic((H, F), seed, 3, 0.0, 0.02))
+
+
+def test_ffn_block_decode_config1(hip, ctx):
+    """x + W_down(silu(W_gate n) * (W_up n)), n = rmsnorm(x): the fused decode FFN."""
+    say("ffn_block_decode (config 1)")
+    wg, wu, wd = _ffn_weights(13)
+    x = orc.synthetic((1, H), 13, 10, 0.0, 1.0)
+    nw = orc.synthetic((H,), 13, 11, 1.0, 0.02)
+    dx = dev(x)
+    ws = torch.zeros(hip.lib.ie_ffn_workspace_size(1), dtype=torch.uint8, device="cuda")
+    hip.check(hip.lib.ie_ffn_block_decode(ctx.handle, P(dx), P(dev(nw)), P(dev(wg)), P(dev(wu)),
+                                          P(dev(wd)), P(ws)))
+    sync()
+    want = orc.residual_add(x, orc.ffn(orc.rmsnorm(x, nw), wg, wu, wd))
+    got = orc.bf16_to_f32(host(dx))
+    assert_close(got, orc.bf16_to_f32(want), what="ffn block")
+    assert_close(got - orc.bf16_to_f32(x), orc.bf16_to_f32(want) - orc.bf16_to_f32(x),
+                 tol=2e-2, what="ffn block delta")
+
+
+@pytest.mark.parametrize("S", [1, 64])
+def test_ffn_op(hip, ctx, S):
+    say(f"ffn op seq_len={S}")
+    wg, wu, wd = _ffn_weights(14)
+    x = orc.synthetic((S, H), 14, 10, 0.0, 1.0)
+    out = bf16_empty(S, H)
+    ws = torch.zeros(hip.lib.ie_ffn_workspace_size(S), dtype=torch.uint8, device="cuda")
+    hip.check(hip.lib.ie_ffn(ctx.handle, S, P(dev(x)), P(out), P(dev(wu)), P(dev(wd)), P(dev(wg)),
+                             P(ws)))
+    sync()
+    assert_close(orc.bf16_to_f32(host(out)), orc.bf16_to_f32(orc.ffn(x, wg, wu, wd)), what="ffn")
+
+
+# ---------------------------------------------------------------- attention
+def _attn_weights(seed):
+    w = orc.layer_weights(seed, 0)
+    return w, {k: dev(v) for k, v in w.items()}
+
+
+def test_decode_attn_config2(hip, ctx, rope):
+    """decode_attn at position 2047 over 2047 cached rows; KV placement bit-exact."""
+    cos, sin, dcos, dsin = rope
+    say("decode_attn seq_len=2048 layer 5")
+    w, dw = _attn_weights(15)
+    layer, pos = 5, 2047
+    kv = torch.zeros(hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+    kv5 = kv.view(32, 2, 8, 8192, 128)[layer]
+    prior = orc.synthetic((2, 8, pos, 128), 15, 500, 0.0, 1.0)
+    kv5[:, :, :pos] = dev(prior)
+    x = orc.synthetic((1, H), 15, 501, 0.0, 1.0)           # the already-normalised input
+    out = bf16_empty(1, H)
+    ws = torch.zeros(hip.lib.ie_attn_workspace_size(1), dtype=torch.uint8, device="cuda")
+    hip.check(hip.lib.ie_decode_attn(ctx.handle, P(dcos), P(dsin), pos + 1, P(dev(x)),
+                                     P(dw["w_q"]), P(dw["w_k"]), P(dw["w_v"]), P(dw["w_o"]),
+                                     P(out), P(ws), P(kv), layer))
+    sync()
+    # oracle: projections, rope at pos, cache write, attention, O projection
+    q = orc.apply_rope(orc.matmul(x, w["w_q"]), pos, 32, 1, 1, cos, sin)
+    k = orc.apply_rope(orc.matmul(x, w["w_k"]), pos, 8, 1, 1, cos, sin)
+    v = orc.matmul(x, w["w_v"])
+    planes = np.zeros((2, 8, 8192, 128), np.uint16)
+    planes[:, :, :pos] = prior
+    planes[0, :, pos] = k.reshape(8, 128)
+    planes[1, :, pos] = v.reshape(8, 128)
+    a = orc.attention(q, planes[0], planes[1], pos, 8192)
+    want = orc.matmul(a, w["w_o"])
+    assert_close(orc.bf16_to_f32(host(out)), orc.bf16_to_f32(want), what="decode_attn")
+    got_kv = host(kv.view(32, 2, 8, 8192, 128)[layer])
+    assert np.array_equal(got_kv[:, :, :pos], prior)                # earlier rows untouched
+    assert not got_kv[:, :, pos + 1:].any()                          # later rows untouched
+    assert ulp_diff(got_kv[:, :, pos], planes[:, :, pos]).max() <= 2 # new row at seq_len-1
+    others = kv.view(32, 2, 8, 8192, 128)
+    assert int(torch.count_nonzero(others[:layer])) == 0
+    assert int(torch.count_nonzero(others[layer + 1:])) == 0
+
+
+def test_attn_prefill_op(hip, ctx, rope):
+    cos, sin, dcos, dsin = rope
+    S, layer = 96, 2
+    say(f"attn (prefill) seq_len={S}")
+    w, dw = _attn_weights(16)
+    x = orc.synthetic((S, H), 16, 600, 0.0, 1.0)
+    kv = torch.zeros(hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+    out = bf16_empty(S, H)
+    ws = torch.zeros(hip.lib.ie_attn_workspace_size(S), dtype=torch.uint8, device="cuda")
+    hip.check(hip.lib.ie_attn(ctx.handle, P(dcos), P(dsin), S, P(dev(x)), P(dw["w_q"]),
+                              P(dw["w_k"]), P(dw["w_v"]), P(dw["w_o"]), P(out), P(ws), P(kv),
+                              layer))
+    sync()
+    q = orc.matmul(x, w["w_q"])
+    k = orc.matmul(x, w["w_k"])
+    v = orc.matmul(x, w["w_v"])
+    qr = np.stack([orc.apply_rope(q[t], t, 32, 1, 1, cos, sin) for t in range(S)])
+    kr = np.stack([orc.apply_rope(k[t], t, 8, 1, 1, cos, sin) for t in range(S)])
+    planes = np.zeros((2, 8, 8192, 128), np.uint16)
+    planes[0, :, :S] = kr.reshape(S, 8, 128).transpose(1, 0, 2)
+    planes[1, :, :S] = v.reshape(S, 8, 128).transpose(1, 0, 2)
+    a = orc.attention(qr.reshape(S, H), planes[0], planes[1], 0, 8192)
+    want = orc.matmul(a, w["w_o"])
+    assert_close(orc.bf16_to_f32(host(out)), orc.bf16_to_f32(want), what="attn prefill")
+    got_kv = host(kv.view(32, 2, 8, 8192, 128)[layer])
+    assert ulp_diff(got_kv[:, :, :S], planes[:, :, :S]).max() <= 2
+    assert not got_kv[:, :, S:].any()
+
+
+def test_decoder_layer_decode_config2(hip, ctx, rope):
+    """One full fused decoder layer, token at position 2047."""
+    cos, sin, dcos, dsin = rope
+    from infengine_amd.engine import ModelWeights
+    say("decoder_layer_decode layer 0 pos 2047 (random-init weights)")
+    seed, layer, pos = 31, 0, 2047
+    W = ModelWeights.random_init(seed=seed, std=0.02)
+    kv = torch.zeros(hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+    prior = orc.synthetic((2, 8, pos, 128), seed, 700, 0.0, 1.0)
+    kv.view(32, 2, 8, 8192, 128)[layer][:, :, :pos] = dev(prior)
+    x = orc.synthetic((1, H), seed, 701, 0.0, 1.0)
+    dx = dev(x)
+    attn = bf16_empty(1, H)
+    ws = torch.zeros(hip.lib.ie_attn_workspace_size(1), dtype=torch.uint8, device="cuda")
+    hip.check(hip.lib.ie_decoder_layer_decode(ctx.handle, W.ref(), layer, pos + 1, P(dx), P(attn),
+                                              P(ws), P(kv)))
+    sync()
+    w = orc.layer_weights(seed, layer)
+    planes = np.zeros((2, 8, 8192, 128), np.uint16)
+    planes[:, :, :pos] = prior
+    xo = x.copy()
+    orc.decoder_layer(xo, w, pos, cos, sin, planes[0], planes[1], 8192)
+    got = orc.bf16_to_f32(host(dx))
+    assert_close(got, orc.bf16_to_f32(xo), what="decoder layer")
+    assert_close(got - orc.bf16_to_f32(x), orc.bf16_to_f32(xo) - orc.bf16_to_f32(x), tol=2e-2,
+                 what="decoder layer delta")
+    got_kv = host(kv.view(32, 2, 8, 8192, 128)[layer])
+    assert np.array_equal(got_kv[:, :, :pos], prior)
+    assert ulp_diff(got_kv[:, :, pos], planes[:, :, pos]).max() <= 2
+    W.free()
+
+
+# ---------------------------------------------------------------- sampling (config 3)
+def test_argmax_fixtures_bit_exact(hip, ctx):
+    say("argmax rows (torch.argmax fixtures: ties, NaN, signed zeros)")
+    g = np.load(GOLD / "argmax_torch.npz")
+    logits = dev(g["logits"])
+    out = torch.full((logits.shape[0],), -7, dtype=torch.int32, device="cuda")
+    hip.check(hip.lib.ie_sample_argmax_rows(ctx.handle, logits.shape[0], V, P(logits), P(out)))
+    sync()
+    assert host(out).tolist() == g["expect"].tolist()
+    one = torch.empty(1, dtype=torch.int32, device="cuda")
+    for r in range(logits.shape[0]):                       # single-row entry point, repeated
+        hip.check(hip.lib.ie_sample_token_amax(ctx.handle, P(logits[r]), P(one)))
+        sync()
+        assert int(one.item()) == int(g["expect"][r])
+
+
+def test_top_p_fixture_and_oracle(hip, ctx):
+    say("top-p T=0.7 p=0.9 on HF fixture logits")
+    g = np.load(GOLD / "top_p_hf.npz")
+    logits = dev(g["logits"])
+    R = logits.shape[0]
+    out = torch.empty(R, dtype=torch.int32, device="cuda")
+    ws = torch.empty(hip.lib.ie_top_p_workspace_size(R, V), dtype=torch.uint8, device="cuda")
+    for step in range(8):
+        hip.check(hip.lib.ie_sample_top_p(ctx.handle, R, V, P(logits), 0.7, 0.9, 1234, step,
+                                          P(out), P(ws)))
+        sync()
+        for r in range(R):
+            kept = np.unpackbits(g["kept"][r])[:V].astype(bool)
+            tok = int(out[r].item())
+            want, info = orc.top_p(g["logits"][r], 0.7, 0.9, 1234, r, step)
+            assert kept[tok]
+            margin = min(info["t"] - info["lo"], info["hi"] - info["t"]) / info["z_kept"]
+            if margin > 1e-6:
+                assert tok == want, (r, step, tok, want)
+
+
+def test_final_norm_lm_head_sampling_config3(hip, ctx):
+    """Config 3: final RMSNorm + lm_head GEMV -> fp32 logits, argmax and top-p, B=1 and B=16."""
+    say("final_norm_lm_head rows=16 + argmax + top-p")
+    R = 16
+    x = orc.synthetic((R, H), 41, 1, 0.0, 1.0)
+    nw = orc.synthetic((H,), 41, 2, 1.0, 0.02)
+    wl = orc.synthetic((V, H), 41, 3, 0.0, 0.02)
+    dwl = dev(wl)
+    logits = torch.empty(R, V, dtype=torch.float32, device="cuda")
+    hip.check(hip.lib.ie_final_norm_lm_head(ctx.handle, R, P(dev(x)), P(dev(nw)), P(dwl),
+                                            P(logits)))
+    one = torch.empty(V, dtype=torch.float32, device="cuda")
+    hip.check(hip.lib.ie_final_norm_lm_head(ctx.handle, 1, P(dev(x[:1])), P(dev(nw)), P(dwl),
+                                            P(one)))
+    sync()
+    want = orc.matmul(orc.rmsnorm(x, nw), wl, out_f32=True)
+    got = host(logits)
+    assert_close(got, want, what="lm_head logits")
+    assert np.array_equal(host(one), got[0])                 # B=1 row == row 0 of B=16, bitwise
+    toks = torch.empty(R, dtype=torch.int32, device="cuda")
+    hip.check(hip.lib.ie_sample_argmax_rows(ctx.handle, R, V, P(logits), P(toks)))
+    sync()
+    for r in range(R):
+        assert int(toks[r].item()) == orc.argmax(got[r])     # identical logits -> identical id
+        top2 = np.sort(want[r])[-2:]
+        if top2[1] - top2[0] > 1e-3 * np.abs(want[r]).max():
+            assert int(toks[r].item()) == orc.argmax(want[r])
+    ws = torch.empty(hip.lib.ie_top_p_workspace_size(R, V), dtype=torch.uint8, device="cuda")
+    hip.check(hip.lib.ie_sample_top_p(ctx.handle, R, V, P(logits), 0.7, 0.9, 99, 3, P(toks),
+                                      P(ws)))
+    sync()
+    for r in range(R):
+        want_tok, info = orc.top_p(got[r], 0.7, 0.9, 99, r, 3)
+        margin = min(info["t"] - info["lo"], info["hi"] - info["t"]) / info["z_kept"]
+        if margin > 1e-6:
+            assert int(toks[r].item()) == want_tok
