@@ -110,7 +110,6 @@ int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs&
   a.out = out;
   a.part_o = w.part_o;
   a.part_ml = w.part_ml;
-  a.counters = counters;
   a.d_seq_len = d_seq_len;
   a.seq_len = seq_len;
   return launch_attn_decode(a, batch, st);

@@ -107,11 +107,21 @@ __device__ __forceinline__ float dot8(const uint4& w, const uint4& x, float acc)
   return acc;
 }
 
-// Streaming (non-temporal) 128-bit load for data read exactly once.
+// Native 4 x u32 vector.  Register arrays use it instead of HIP's uint4 (a
+// struct with a union, which SROA does not split into registers).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
-  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-  return make_uint4(v[0], v[1], v[2], v[3]);
+
+__device__ __forceinline__ float dot8(const u32x4_t& w, const u32x4_t& x, float acc) {
+  acc = dot2(w[0], x[0], acc);
+  acc = dot2(w[1], x[1], acc);
+  acc = dot2(w[2], x[2], acc);
+  acc = dot2(w[3], x[3], acc);
+  return acc;
+}
+
+// Streaming (non-temporal) 128-bit load for data read exactly once.
+__device__ __forceinline__ u32x4_t ld_stream(const u32x4_t* p) {
+  return __builtin_nontemporal_load(p);
 }
 
 // ---------------------------------------------------------------- wave reductions

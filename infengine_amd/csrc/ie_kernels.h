@@ -47,7 +47,6 @@ struct AttnDecodeParams {
   uint16_t* out;            // [batch][32][128] bf16
   float* part_o;            // [batch][8][splits][4][128]
   float* part_ml;           // [batch][8][splits][4][2]
-  unsigned int* counters;   // [batch][8], zero on entry, left zero on exit
   const int* d_seq_len;     // [batch] device seq lens, or nullptr
   int seq_len;              // used when d_seq_len == nullptr (batch must be 1)
 };

@@ -57,7 +57,7 @@ __device__ __forceinline__ const uint16_t* w_row(const GemmParams& p, int ntile,
 
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p, int m_tiles) {
-  __shared__ uint4 smem[2][2][BN * (BK / 8)];
+  __shared__ u32x4_t smem[2][2][BN * (BK / 8)];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave >> 1, wm = wave & 1;
@@ -79,11 +79,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p, int m_tiles) {
     slot[i] = r * 8 + (c ^ (r & 7));
   }
 
-  uint4 rw[4], rx[4];
+  u32x4_t rw[4], rx[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    rw[i] = *reinterpret_cast<const uint4*>(wsrc[i]);
-    rx[i] = *reinterpret_cast<const uint4*>(xsrc[i]);
+    rw[i] = *reinterpret_cast<const u32x4_t*>(wsrc[i]);
+    rx[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i]);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -107,8 +107,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p, int m_tiles) {
       const int ko = (kt + 1) * BK;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        rw[i] = *reinterpret_cast<const uint4*>(wsrc[i] + ko);
-        rx[i] = *reinterpret_cast<const uint4*>(xsrc[i] + ko);
+        rw[i] = *reinterpret_cast<const u32x4_t*>(wsrc[i] + ko);
+        rx[i] = *reinterpret_cast<const u32x4_t*>(xsrc[i] + ko);
       }
     }
 #pragma unroll

@@ -21,12 +21,13 @@ namespace ie {
 
 namespace {
 
-__device__ __forceinline__ float sumsq8(const uint4& v) {
+__device__ __forceinline__ float sumsq8(const u32x4_t& v) {
   float s = 0.f;
-  s = fmaf(bf_lo(v.x), bf_lo(v.x), s); s = fmaf(bf_hi(v.x), bf_hi(v.x), s);
-  s = fmaf(bf_lo(v.y), bf_lo(v.y), s); s = fmaf(bf_hi(v.y), bf_hi(v.y), s);
-  s = fmaf(bf_lo(v.z), bf_lo(v.z), s); s = fmaf(bf_hi(v.z), bf_hi(v.z), s);
-  s = fmaf(bf_lo(v.w), bf_lo(v.w), s); s = fmaf(bf_hi(v.w), bf_hi(v.w), s);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s = fmaf(bf_lo(v[i]), bf_lo(v[i]), s);
+    s = fmaf(bf_hi(v[i]), bf_hi(v[i]), s);
+  }
   return s;
 }
 
@@ -37,9 +38,9 @@ __device__ __forceinline__ uint32_t norm2(uint32_t x, uint32_t w, float r) {
   return pack_bf2(lo, hi);
 }
 
-__device__ __forceinline__ uint4 norm8(const uint4& x, const uint4& w, float r) {
-  return make_uint4(norm2(x.x, w.x, r), norm2(x.y, w.y, r), norm2(x.z, w.z, r),
-                    norm2(x.w, w.w, r));
+__device__ __forceinline__ u32x4_t norm8(const u32x4_t& x, const u32x4_t& w, float r) {
+  return u32x4_t{norm2(x[0], w[0], r), norm2(x[1], w[1], r), norm2(x[2], w[2], r),
+                 norm2(x[3], w[3], r)};
 }
 
 template <int EPI, int K>
@@ -104,22 +105,47 @@ __device__ __forceinline__ void gemv_epilogue(const GemvParams& p, int pair, int
   }
 }
 
+// Loads of one pipeline step: G 16-byte chunks of each row of a pair.
+template <int G>
+__device__ __forceinline__ void load_step(const u32x4_t* a, const u32x4_t* b, int g0,
+                                          u32x4_t (&wa)[G], u32x4_t (&wb)[G]) {
+#pragma unroll
+  for (int c = 0; c < G; ++c) {
+    wa[c] = ld_stream(a + (g0 + c) * 64);
+    wb[c] = ld_stream(b + (g0 + c) * 64);
+  }
+}
+
 template <int K, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
-  constexpr int NC = K / 512;                // 16-byte chunks per lane per row
-  constexpr int G = (NC % 8 == 0) ? 8 : 7;   // chunks per load group
+  constexpr int NC = K / 512;                 // 16-byte chunks per lane per row
+  constexpr int G = (K == 4096) ? 4 : 7;      // chunks per pipeline step
+  constexpr int NG = NC / G;                  // steps per row pair
   static_assert(NC % G == 0, "K must be a multiple of 512*G");
-  __shared__ uint4 xs[K / 8];
+  __shared__ u32x4_t xs[K / 8];
   __shared__ float red[4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = blockIdx.y;
-  const uint4* x4 = reinterpret_cast<const uint4*>(p.x + (size_t)row * p.x_stride);
+  const int first = (blockIdx.x * 4 + wave) * p.ppw;
+  const int npairs = max(0, min(p.ppw, p.n_pairs - first));
+  const int nsteps = npairs * NG;
 
+  // The wave's first weight loads go out before the x staging / RMSNorm
+  // prologue, which then runs under their latency.
+  u32x4_t ca[G], cb[G], na[G], nb[G];
+  const uint16_t *r0 = nullptr, *r1 = nullptr;
+  if (nsteps > 0) {
+    rows_of_pair<EPI, K>(p, first, r0, r1);
+    load_step<G>(reinterpret_cast<const u32x4_t*>(r0) + lane,
+                 reinterpret_cast<const u32x4_t*>(r1) + lane, 0, ca, cb);
+  }
+
+  const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(p.x + (size_t)row * p.x_stride);
   if constexpr (NORM) {
     float ss = 0.f;
     for (int i = tid; i < K / 8; i += 256) {
-      const uint4 v = x4[i];
+      const u32x4_t v = x4[i];
       xs[i] = v;
       ss += sumsq8(v);
     }
@@ -128,40 +154,46 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     __syncthreads();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float r = rsqrtf(tot / (float)K + kRmsEps);
-    const uint4* w4 = reinterpret_cast<const uint4*>(p.norm_w);
+    const u32x4_t* w4 = reinterpret_cast<const u32x4_t*>(p.norm_w);
     for (int i = tid; i < K / 8; i += 256) xs[i] = norm8(xs[i], w4[i], r);
   } else {
     for (int i = tid; i < K / 8; i += 256) xs[i] = x4[i];
   }
   __syncthreads();
 
-  const int first = (blockIdx.x * 4 + wave) * p.ppw;
-  for (int i = 0; i < p.ppw; ++i) {
-    const int pair = first + i;
-    if (pair >= p.n_pairs) break;
-    const uint16_t *r0, *r1;
-    rows_of_pair<EPI, K>(p, pair, r0, r1);
-    const uint4* a = reinterpret_cast<const uint4*>(r0) + lane;
-    const uint4* b = reinterpret_cast<const uint4*>(r1) + lane;
-    float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll 1
-    for (int g = 0; g < NC; g += G) {
-      uint4 wa[G], wb[G];
-#pragma unroll
-      for (int c = 0; c < G; ++c) {
-        wa[c] = ld_stream(a + (g + c) * 64);
-        wb[c] = ld_stream(b + (g + c) * 64);
-      }
-#pragma unroll
-      for (int c = 0; c < G; ++c) {
-        const uint4 xv = xs[(g + c) * 64 + lane];
-        acc0 = dot8(wa[c], xv, acc0);
-        acc1 = dot8(wb[c], xv, acc1);
+  // Pipeline over (pair, step): the loads of step s+1 (possibly the next
+  // pair's rows) are issued before step s is reduced.
+  float acc0 = 0.f, acc1 = 0.f;
+  for (int s = 0; s < nsteps; ++s) {
+    const int g = s % NG;
+    if (s + 1 < nsteps) {
+      const int s1 = s + 1, g1 = s1 % NG;
+      const uint16_t *q0 = r0, *q1 = r1;
+      if (g1 == 0) rows_of_pair<EPI, K>(p, first + s1 / NG, q0, q1);
+      load_step<G>(reinterpret_cast<const u32x4_t*>(q0) + lane,
+                   reinterpret_cast<const u32x4_t*>(q1) + lane, g1 * G, na, nb);
+      if (g1 == 0) {
+        r0 = q0;
+        r1 = q1;
       }
     }
-    acc0 = wave_sum(acc0);
-    acc1 = wave_sum(acc1);
-    if (lane == 0) gemv_epilogue<EPI>(p, pair, row, acc0, acc1);
+#pragma unroll
+    for (int c = 0; c < G; ++c) {
+      const u32x4_t xv = xs[(g * G + c) * 64 + lane];
+      acc0 = dot8(ca[c], xv, acc0);
+      acc1 = dot8(cb[c], xv, acc1);
+    }
+    if (g == NG - 1) {
+      const float a0 = wave_sum(acc0), a1 = wave_sum(acc1);
+      if (lane == 0) gemv_epilogue<EPI>(p, first + s / NG, row, a0, a1);
+      acc0 = 0.f;
+      acc1 = 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < G; ++c) {
+      ca[c] = na[c];
+      cb[c] = nb[c];
+    }
   }
 }
 
@@ -194,13 +226,18 @@ int launch_k(int epi, bool norm, const GemvParams& p, int rows, hipStream_t st) 
 
 }  // namespace
 
+namespace {
+int g_ppw_override = 0;
+}  // namespace
+
 int default_ppw(int n_pairs) {
-  // Aim for ~2048 waves in flight (256 CUs x 8) so each wave amortises the
-  // staging of x over several row pairs without starving the chip.
-  int ppw = n_pairs / 2048;
-  if (ppw < 1) ppw = 1;
-  if (ppw > 32) ppw = 32;
-  return ppw;
+  if (g_ppw_override > 0) return g_ppw_override;
+  // One row pair per wave measured fastest on MI355X for every decode shape
+  // (QKV, O, gate/up, down, lm_head): the most waves, hence the most 16-byte
+  // loads in flight per CU, while the software pipeline already hides the
+  // x staging behind the first loads.
+  (void)n_pairs;
+  return 1;
 }
 
 int launch_gemv(int K, int epi, bool norm, GemvParams p, int rows, hipStream_t st) {
@@ -216,3 +253,9 @@ int launch_gemv(int K, int epi, bool norm, GemvParams p, int rows, hipStream_t s
 }
 
 }  // namespace ie
+
+extern "C" int ie_tune_gemv_pairs_per_wave(int ppw) {
+  IE_REQUIRE(ppw >= 0 && ppw <= 64, "tune_gemv_pairs_per_wave: %d out of [0, 64]", ppw);
+  ie::g_ppw_override = ppw;
+  return IE_OK;
+}

@@ -45,6 +45,7 @@ def _load() -> C.CDLL:
     lib = C.CDLL(str(LIB_PATH))
     P, I, U64, F, SZ = C.c_void_p, C.c_int, C.c_uint64, C.c_float, C.c_size_t
     sig = {
+        "orc_set_sum_order": (None, [I]),
         "orc_fill_synthetic": (None, [P, SZ, U64, U64, F, F]),
         "orc_tensor_id": (U64, [I, I]),
         "orc_rope_tables": (None, [P, P]),
@@ -83,6 +84,19 @@ def _u16(a) -> np.ndarray:
     a = np.ascontiguousarray(a)
     assert a.dtype == np.uint16, a.dtype
     return a
+
+
+class reversed_summation:
+    """Context manager: every oracle dot product sums k in descending order.
+    The divergence between the two orders is the fp32 rounding-noise floor."""
+
+    def __enter__(self):
+        _lib.orc_set_sum_order(1)
+        return self
+
+    def __exit__(self, *exc):
+        _lib.orc_set_sum_order(0)
+        return False
 
 
 # ---------------------------------------------------------------- bf16 helpers

@@ -51,14 +51,28 @@ inline uint64_t synth_base(uint64_t seed, uint64_t tensor_id) {
 
 constexpr double kSynthStd = 37837.22627754049;  // sqrt(4 * (65536^2 - 1) / 12)
 
+// Summation order of every fp32 dot product: 0 = ascending k, 1 = descending k.
+// Both are valid fp32 accumulations; running the oracle both ways measures the
+// rounding-noise floor that any fp32-accumulating implementation sits inside.
+int g_sum_reverse = 0;
+
 // fp32 dot product of two bf16 vectors, 8 running partial sums.
 inline float dot_bf16(const uint16_t* a, const uint16_t* b, int k) {
   float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  int i = 0;
-  for (; i + 8 <= k; i += 8)
-    for (int j = 0; j < 8; ++j) s[j] += bf2f(a[i + j]) * bf2f(b[i + j]);
-  float t = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
-  for (; i < k; ++i) t += bf2f(a[i]) * bf2f(b[i]);
+  float t;
+  if (!g_sum_reverse) {
+    int i = 0;
+    for (; i + 8 <= k; i += 8)
+      for (int j = 0; j < 8; ++j) s[j] += bf2f(a[i + j]) * bf2f(b[i + j]);
+    t = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+    for (; i < k; ++i) t += bf2f(a[i]) * bf2f(b[i]);
+  } else {
+    int i = k;
+    for (; i - 8 >= 0; i -= 8)
+      for (int j = 0; j < 8; ++j) s[j] += bf2f(a[i - 1 - j]) * bf2f(b[i - 1 - j]);
+    t = ((s[7] + s[6]) + (s[5] + s[4])) + ((s[3] + s[2]) + (s[1] + s[0]));
+    for (; i > 0; --i) t += bf2f(a[i - 1]) * bf2f(b[i - 1]);
+  }
   return t;
 }
 
@@ -69,6 +83,8 @@ inline float silu_mul(float g, float u) {  // swiglu.cu:24-29
 }  // namespace
 
 extern "C" {
+
+void orc_set_sum_order(int reverse) { g_sum_reverse = reverse ? 1 : 0; }
 
 // ---------------------------------------------------------------- synthetic data
 // Deterministic approximate normal keyed by (seed, tensor_id, index): centred

@@ -37,8 +37,10 @@ def _gpu_stream(request):
         yield
         return
     import torch
+    import gpu_util
     c = request.getfixturevalue("ctx")
     torch.cuda.synchronize()
     torch.cuda.set_stream(c.stream)
     yield
     torch.cuda.synchronize()
+    gpu_util.release()

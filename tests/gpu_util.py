@@ -18,8 +18,22 @@ def host(t: torch.Tensor) -> np.ndarray:
     return a.view(np.uint16) if a.dtype == np.int16 else a
 
 
+# Tensors whose raw pointers were handed to the library in the current test.
+# Holding them here keeps temporaries such as P(dev(x)) alive until the test
+# ends (otherwise torch's caching allocator hands the block to the next
+# allocation while the kernel still reads it).
+_KEEP: list = []
+
+
 def P(t: torch.Tensor | None):
-    return None if t is None else C.c_void_p(t.data_ptr())
+    if t is None:
+        return None
+    _KEEP.append(t)
+    return C.c_void_p(t.data_ptr())
+
+
+def release() -> None:
+    _KEEP.clear()
 
 
 def bf16_empty(*shape) -> torch.Tensor:
@@ -41,3 +55,45 @@ def ulp_diff(a: np.ndarray, b: np.ndarray) -> np.ndarray:
         x = x.astype(np.int32)
         return np.where(x & 0x8000, -(x & 0x7FFF), x)
     return np.abs(key(a) - key(b))
+
+
+def bf16_f32(a: np.ndarray) -> np.ndarray:
+    return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def assert_bf16_close(got: np.ndarray, want: np.ndarray, ulps: int = 2, what: str = "",
+                      floor: float = 1e-3, outlier_frac: float = 0.0):
+    """Element-wise: |got - want| <= ulps * ulp(|want|) + floor * max|want|.
+
+    The absolute floor covers values near zero, where a sign change between two
+    correctly rounded results is a tiny absolute difference but thousands of
+    bf16 steps.  `outlier_frac` admits that fraction of elements beyond the ulp
+    bound (cancellation, e.g. a*c - b*s in RoPE, magnifies a 1-ulp input
+    difference), each still within 1e-2 of the tensor's scale.
+    """
+    g = bf16_f32(got).astype(np.float64)
+    w = bf16_f32(want).astype(np.float64)
+    scale = np.abs(w).max()
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(w), 1e-38))) - 7)
+    allowed = ulps * ulp + floor * scale
+    err = np.abs(g - w)
+    bad = err > allowed
+    msg = (f"{what}: {int(bad.sum())} of {bad.size} elements beyond {ulps} ulp; "
+           f"worst {err.max():.3e} (scale {scale:.3e})")
+    assert bad.mean() <= outlier_frac, msg
+    assert err.max() <= 1e-2 * scale, msg
+
+
+def assert_delta_close(x_in: np.ndarray, got: np.ndarray, want: np.ndarray, tol: float = 2e-2,
+                       what: str = ""):
+    """A residual layer's own contribution (out - in) matches: per element
+    |got - want| <= 2 ulp(want) + tol * max|want - x_in|, i.e. the output is
+    right to its own bf16 rounding plus a small fraction of what the layer added
+    (a bare delta comparison is ill-conditioned where |x_in| >> |delta|)."""
+    g, w, x = (bf16_f32(a).astype(np.float64) for a in (got, want, x_in))
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(w), 1e-38))) - 7)
+    allowed = 2 * ulp + tol * np.abs(w - x).max()
+    err = np.abs(g - w)
+    bad = err > allowed
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements off; worst {err.max():.3e}"
+    assert err.mean() <= tol * np.abs(w - x).mean(), f"{what}: mean error {err.mean():.3e}"

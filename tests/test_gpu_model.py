@@ -2,20 +2,31 @@
 through the C-ABI (ie_decode_step / ie_prefill / ie_decode_step_batched),
 against the CPU oracle regenerating the same weights.
 
-Logits: tests/tolerance.py bar.  Token ids: equal to the oracle's argmax unless
-the oracle's top-2 logits are closer than the tolerance (then either may win).
-KV-cache placement: bit-exact (untouched rows stay as they were).
+Three bars:
+  * per layer: every one of the 32 layers, fed the GPU's own input, matches the
+    oracle layer to tests/tolerance.py (no error accumulation across layers);
+  * integration: ie_decode_step is bitwise identical to chaining the per-layer
+    entry point plus final norm / lm_head / argmax (eager and hipGraph replay);
+  * end to end: logits of the 32-layer stack are within 2x the stack's own fp32
+    noise floor, measured as the oracle vs the oracle with every dot product
+    summed in the opposite order (bf16 storage amplifies rounding-order noise
+    through 32 layers to a few percent on this random-init model).  Token ids
+    equal the oracle's argmax unless its top-2 gap is inside that noise.
+KV-cache placement is bit-exact: untouched rows stay exactly as they were.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
 
 import oracle as orc
-from gpu_util import dev, host, say, ulp_diff
-from tolerance import assert_close
+from gpu_util import P, assert_bf16_close, assert_delta_close, dev, host, say
+from tolerance import TOL, assert_close, rel_errors
 
-pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 SEED = 2024
+POS = 300
 
 
 @pytest.fixture(scope="module")
@@ -33,11 +44,34 @@ def oracle_model():
     return orc.SyntheticModel(SEED, 0.02)
 
 
-def check_token(tok: int, want_logits: np.ndarray, got_logits: np.ndarray):
+@pytest.fixture(scope="module")
+def prior():
+    return orc.synthetic((32, 2, 8, POS, 128), SEED, 900, 0.0, 1.0)
+
+
+@pytest.fixture(scope="module")
+def noise_floor(oracle_model, prior):
+    say("oracle noise floor: ascending vs descending fp32 summation, 32 layers")
+    kv = np.zeros((32, 2, 8, POS + 2, 128), np.uint16)
+    kv[:, :, :, :POS] = prior
+    a = oracle_model.decode(4242, POS, kv)
+    kv[:, :, :, POS:] = 0
+    with orc.reversed_summation():
+        b = oracle_model.decode(4242, POS, kv)
+    mx, mean = rel_errors(b, a)
+    say(f"noise floor: max-abs/scale {mx:.3e}, mean-rel {mean:.3e}")
+    return max(mx, mean)
+
+
+def e2e_tol(noise: float) -> float:
+    return max(TOL, 2.0 * noise)
+
+
+def check_token(tok: int, want_logits: np.ndarray, got_logits: np.ndarray, noise: float):
     assert tok == int(np.argmax(got_logits))          # the GPU's own logits -> first max
     order = np.argsort(want_logits)
     gap = want_logits[order[-1]] - want_logits[order[-2]]
-    if gap > 1e-2 * np.abs(want_logits).max():
+    if gap > 2 * noise * np.abs(want_logits).max():
         assert tok == int(order[-1]), (tok, int(order[-1]), gap)
 
 
@@ -49,56 +83,101 @@ def test_weights_match_oracle_generator(model):
                           orc.final_norm(SEED))
 
 
-@pytest.mark.parametrize("graph", [False, True])
-def test_decode_steps_vs_oracle(hip, model, oracle_model, graph):
-    from infengine_amd.engine import Context, Request
-    P = 300
-    say(f"decode_step x2 from position {P} (graph={graph})")
-    c = Context(0, graph=graph)
-    req = Request(c, model, max_seq_len=P + 8)
-    prior = orc.synthetic((32, 2, 8, P, 128), SEED, 900, 0.0, 1.0)
-    req.kv_view()[:, :, :, :P] = dev(prior).view(torch.bfloat16)
-    tok0 = 4242
-    req.tokens[P] = tok0
-    t1 = req.decode_step(P + 1)
-    got1 = host(req.logits).copy()
-    req.tokens[P + 1] = t1
-    t2 = req.decode_step(P + 2)
-    got2 = host(req.logits).copy()
+def _chained_layers(hip, ctx, model, prior, tok, oracle_check):
+    """Embed tok at position POS and run the 32 layers one entry point call at a
+    time; with oracle_check, compare each layer against the oracle fed the same
+    input.  Returns (hidden, logits, kv)."""
+    kv = torch.zeros(hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+    kv.view(32, 2, 8, 8192, 128)[:, :, :, :POS] = dev(prior)
+    emb = model.view(None, "emb_lookup").view(torch.int16)
+    x = emb[tok:tok + 1].clone()
+    attn = torch.empty(1, 4096, dtype=torch.int16, device="cuda")
+    ws = torch.zeros(hip.lib.ie_attn_workspace_size(1), dtype=torch.uint8, device="cuda")
+    cos, sin = orc.rope_tables()
+    for l in range(32):
+        x_in = host(x).copy()
+        hip.check(hip.lib.ie_decoder_layer_decode(ctx.handle, model.ref(), l, POS + 1, P(x),
+                                                  P(attn), P(ws), P(kv)))
+        torch.cuda.synchronize()
+        if oracle_check:
+            w = orc.layer_weights(SEED, l)
+            planes = np.zeros((2, 8, POS + 1, 128), np.uint16)
+            planes[:, :, :POS] = prior[l]
+            xo = x_in.copy()
+            orc.decoder_layer(xo, w, POS, cos, sin, planes[0], planes[1], POS + 1)
+            got = orc.bf16_to_f32(host(x))
+            assert_close(got, orc.bf16_to_f32(xo), what=f"layer {l}")
+            assert_delta_close(x_in, host(x), xo, what=f"layer {l} delta")
+            gkv = host(kv.view(32, 2, 8, 8192, 128)[l, :, :, POS])
+            assert_bf16_close(gkv, planes[:, :, POS], what=f"layer {l} kv row", outlier_frac=1e-3)
+    logits = torch.empty(128256, dtype=torch.float32, device="cuda")
+    hip.check(hip.lib.ie_final_norm_lm_head(ctx.handle, 1, P(x),
+                                            P(model.view(None, "final_norm")),
+                                            P(model.view(None, "lm_head")), P(logits)))
     torch.cuda.synchronize()
+    return host(x), host(logits), kv
 
-    kv = np.zeros((32, 2, 8, P + 2, 128), np.uint16)
-    kv[:, :, :, :P] = prior
-    want1 = oracle_model.decode(tok0, P, kv)
-    assert_close(got1, want1, what="decode step 1 logits")
-    check_token(t1, want1, got1)
-    want2 = oracle_model.decode(t1, P + 1, kv)
-    assert_close(got2, want2, what="decode step 2 logits")
-    check_token(t2, want2, got2)
-    gkv = host(req.kv.view(torch.int16).view(32, 2, 8, 8192, 128)[:, :, :, :P + 3])
-    assert np.array_equal(gkv[:, :, :, :P], prior)               # old rows untouched
-    assert not gkv[:, :, :, P + 2].any()                          # next row still empty
-    d = ulp_diff(gkv[:, :, :, P:P + 2], kv[:, :, :, P:P + 2])
-    assert np.mean(d <= 2) > 0.99
-    if graph:
-        test_decode_steps_vs_oracle.graph_logits = (got1, got2)
-    else:
-        test_decode_steps_vs_oracle.eager_logits = (got1, got2)
+
+def test_every_layer_matches_oracle(hip, ctx, model, prior):
+    say("32 layers one at a time vs the oracle (each fed the GPU's input)")
+    _chained_layers(hip, ctx, model, prior, 4242, oracle_check=True)
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_decode_step_equals_chained_layers(hip, ctx, model, prior, graph):
+    from infengine_amd.engine import Context, Request
+    say(f"decode_step (graph={graph}) vs chained per-layer calls, bitwise")
+    _, want_logits, want_kv = _chained_layers(hip, ctx, model, prior, 4242, oracle_check=False)
+    c = Context(0, graph=graph)
+    req = Request(c, model, max_seq_len=POS + 8)
+    req.kv_view()[:, :, :, :POS] = dev(prior).view(torch.bfloat16)
+    req.tokens[POS] = 4242
+    for rep in range(3 if graph else 1):          # graph replays: same input, same output
+        req.kv_view()[:, :, :, POS:] = 0
+        tok = req.decode_step(POS + 1)
+        got = host(req.logits)
+        assert np.array_equal(got, want_logits), f"replay {rep}"
+        assert tok == int(np.argmax(want_logits))
+        assert int(req.token.item()) == tok
+    gkv = host(req.kv.view(torch.int16).view(32, 2, 8, 8192, 128)[:, :, :, :POS + 2])
+    assert np.array_equal(gkv, host(want_kv.view(32, 2, 8, 8192, 128)[:, :, :, :POS + 2]))
+    c.close()
+    torch.cuda.set_stream(ctx.stream)
+
+
+def test_decode_steps_vs_oracle(hip, model, oracle_model, prior, noise_floor):
+    from infengine_amd.engine import Context, Request
+    say(f"decode_step x2 from position {POS} vs oracle (tol {e2e_tol(noise_floor):.3e})")
+    c = Context(0, graph=True)
+    req = Request(c, model, max_seq_len=POS + 8)
+    req.kv_view()[:, :, :, :POS] = dev(prior).view(torch.bfloat16)
+    req.tokens[POS] = 4242
+    t1 = req.decode_step(POS + 1)
+    got1 = host(req.logits).copy()
+    req.tokens[POS + 1] = t1
+    t2 = req.decode_step(POS + 2)
+    got2 = host(req.logits).copy()
+    gkv = host(req.kv.view(torch.int16).view(32, 2, 8, 8192, 128)[:, :, :, :POS + 3])
     c.close()
 
+    kv = np.zeros((32, 2, 8, POS + 2, 128), np.uint16)
+    kv[:, :, :, :POS] = prior
+    want1 = oracle_model.decode(4242, POS, kv)
+    assert_close(got1, want1, tol=e2e_tol(noise_floor), what="decode step 1 logits")
+    check_token(t1, want1, got1, noise_floor)
+    want2 = oracle_model.decode(t1, POS + 1, kv)
+    assert_close(got2, want2, tol=e2e_tol(noise_floor), what="decode step 2 logits")
+    check_token(t2, want2, got2, noise_floor)
+    assert np.array_equal(gkv[:, :, :, :POS], prior)              # old rows untouched
+    assert gkv[:, :, :, POS:POS + 2].any(axis=-1).all()            # rows POS, POS+1 written
+    assert not gkv[:, :, :, POS + 2].any()                         # next row still empty
+    assert_bf16_close(gkv[0, :, :, POS:POS + 2], kv[0, :, :, POS:POS + 2], what="layer-0 kv", outlier_frac=1e-3)
 
-def test_graph_replay_bitwise_equals_eager():
-    g = getattr(test_decode_steps_vs_oracle, "graph_logits", None)
-    e = getattr(test_decode_steps_vs_oracle, "eager_logits", None)
-    if g is None or e is None:
-        pytest.skip("needs both decode runs")
-    assert np.array_equal(g[0], e[0]) and np.array_equal(g[1], e[1])
 
-
-def test_prefill_then_decode_vs_oracle(hip, model, oracle_model):
+def test_prefill_then_decode_vs_oracle(hip, model, oracle_model, noise_floor):
     from infengine_amd.engine import Context, Request
     S = 16
-    say(f"prefill seq_len={S} then decode_step")
+    say(f"prefill seq_len={S} then decode_step vs oracle")
     rng = np.random.default_rng(5)
     ids = rng.integers(0, 128256, S).astype(np.int32)
     c = Context(0)
@@ -106,30 +185,31 @@ def test_prefill_then_decode_vs_oracle(hip, model, oracle_model):
     req.tokens[:S] = torch.from_numpy(ids).cuda()
     t = req.prefill(S)
     got = host(req.logits).copy()
-    kv = np.zeros((32, 2, 8, S + 2, 128), np.uint16)
-    want = oracle_model.prefill(ids, kv)
-    assert_close(got, want, what="prefill logits")
-    check_token(t, want, got)
     gkv = host(req.kv.view(torch.int16).view(32, 2, 8, 8192, 128)[:, :, :, :S + 1])
-    assert np.mean(ulp_diff(gkv[:, :, :, :S], kv[:, :, :, :S]) <= 2) > 0.99
-    assert not gkv[:, :, :, S].any()
-    # decode the sampled token at position S
     req.tokens[S] = t
     t2 = req.decode_step(S + 1)
     got2 = host(req.logits).copy()
-    want2 = oracle_model.decode(t, S, kv)
-    assert_close(got2, want2, what="decode after prefill")
-    check_token(t2, want2, got2)
     # invariant: decode at position S == last row of a causal prefill over S+1 tokens
     req2 = Request(c, model, max_seq_len=S + 8)
     req2.tokens[:S + 1] = torch.from_numpy(np.append(ids, t).astype(np.int32)).cuda()
     req2.prefill(S + 1)
-    assert_close(host(req2.logits), got2, what="prefill(S+1) vs prefill(S)+decode")
+    got3 = host(req2.logits).copy()
     c.close()
 
+    kv = np.zeros((32, 2, 8, S + 2, 128), np.uint16)
+    want = oracle_model.prefill(ids, kv)
+    tol = e2e_tol(noise_floor)
+    assert_close(got, want, tol=tol, what="prefill logits")
+    check_token(t, want, got, noise_floor)
+    assert_bf16_close(gkv[0, :, :, :S], kv[0, :, :, :S], what="layer-0 kv", outlier_frac=1e-3)
+    assert gkv[:, :, :, :S].any(axis=-1).all() and not gkv[:, :, :, S].any()
+    want2 = oracle_model.decode(t, S, kv)
+    assert_close(got2, want2, tol=tol, what="decode after prefill")
+    check_token(t2, want2, got2, noise_floor)
+    assert_close(got3, got2, tol=tol, what="prefill(S+1) vs prefill(S)+decode")
 
-def test_batched_decode_matches_single(hip, model):
-    import ctypes as C
+
+def test_batched_decode_matches_single(hip, model, noise_floor):
     from infengine_amd.engine import Context, Request, ptr
     B = 3
     lens = [101, 257, 64]
@@ -161,6 +241,7 @@ def test_batched_decode_matches_single(hip, model):
                                              ptr(kvs)))
     torch.cuda.synchronize()
     for b in range(B):
-        assert_close(host(logits[b]), singles[b][1], what=f"batched row {b}")
-        assert list(th)[b] == int(out[b].item())
+        assert_close(host(logits[b]), singles[b][1], tol=e2e_tol(noise_floor),
+                     what=f"batched row {b}")
+        assert list(th)[b] == int(out[b].item()) == int(np.argmax(host(logits[b])))
     c.close()
