@@ -94,7 +94,8 @@ typedef struct ie_model_weights {
 typedef struct ie_context ie_context;
 
 /* ---- context / errors (replaces cublasCreate/cublasDestroy, manager.cpp:58-59,107) ---- */
-/* stream: a hipStream_t to run on, or NULL to create a private non-blocking stream. */
+/* stream: the hipStream_t every call on this context runs on; NULL means the
+ * legacy default stream (the reference's implicit ordering). */
 IE_API int ie_context_create(ie_context** out, int device, void* stream);
 IE_API int ie_context_destroy(ie_context* ctx);
 IE_API void* ie_context_stream(ie_context* ctx);

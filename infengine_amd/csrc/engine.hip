@@ -131,10 +131,9 @@ int gemv_plain(int K, int epi, const uint16_t* x, const uint16_t* norm_w, const 
   return launch_gemv(K, epi, norm_w != nullptr, p, rows, st);
 }
 
-int decoder_layer_decode(Context* c, const ie_model_weights& W, int layer, uint16_t* x,
-                         uint16_t* attn_out, const DecodeWs& w, void* kv, const int* d_seq_len,
-                         int seq_len) {
-  hipStream_t st = c->stream;
+int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, int layer,
+                         uint16_t* x, uint16_t* attn_out, const DecodeWs& w, void* kv,
+                         const int* d_seq_len, int seq_len) {
   const ie_layer& L = W.layers[layer];
   uint16_t* kvl = kv_layer(kv, layer);
   IE_TRY(qkv_rope_gemv(L, W.rope, x, L.input_layernorm, w.q, kvl, d_seq_len, seq_len - 1, st));
@@ -149,14 +148,14 @@ int decoder_layer_decode(Context* c, const ie_model_weights& W, int layer, uint1
   return IE_OK;
 }
 
-int enqueue_decode(Context* c, const ie_model_weights& W, int* tokenid_buff, uint16_t* data,
-                   uint16_t* attn, float* logits, int* out_tok, void* ws, void* kv) {
-  hipStream_t st = c->stream;
+int enqueue_decode(Context* c, hipStream_t st, const ie_model_weights& W, int* tokenid_buff,
+                   uint16_t* data, uint16_t* attn, float* logits, int* out_tok, void* ws,
+                   void* kv) {
   const int* d_sl = c->d_params;
   const DecodeWs w = decode_ws(ws, 1);
   IE_TRY(launch_emblookup(1, tokenid_buff, W.emb_lookup, data, d_sl, 0, st));
   for (int l = 0; l < kLayers; ++l)
-    IE_TRY(decoder_layer_decode(c, W, l, data, attn, w, kv, d_sl, 0));
+    IE_TRY(decoder_layer_decode(c, st, W, l, data, attn, w, kv, d_sl, 0));
   IE_TRY(gemv_plain(kHidden, kEpiF32, data, W.final_norm, W.lm_head, nullptr, kVocab / 2,
                     nullptr, logits, 1, kVocab, st));
   IE_TRY(launch_argmax_rows(1, kVocab, logits, out_tok, c->d_slots, c->d_counters + kCntArgmax,
@@ -251,14 +250,10 @@ int ie_context_create(ie_context** out, int device, void* stream) {
   c->device = device;
   int rc = IE_OK;
   do {
-    if (stream) {
-      c->stream = stream_of(stream);
-    } else {
-      if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
-        rc = IE_ERR_HIP;
-        break;
-      }
-      c->own_stream = true;
+    c->stream = stream_of(stream);
+    if (hipStreamCreateWithFlags(&c->capture, hipStreamNonBlocking) != hipSuccess) {
+      rc = IE_ERR_HIP;
+      break;
     }
     if (hipMalloc(&c->d_counters, kNumCounters * sizeof(unsigned int)) != hipSuccess ||
         hipMalloc(&c->d_slots, kNumSlots * sizeof(unsigned long long)) != hipSuccess ||
@@ -288,14 +283,14 @@ int ie_context_create(ie_context** out, int device, void* stream) {
 int ie_context_destroy(ie_context* c) {
   if (!c) return IE_OK;
   (void)hipSetDevice(c->device);
-  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  (void)hipStreamSynchronize(c->stream);
   if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
   (void)hipFree(c->d_counters);
   (void)hipFree(c->d_slots);
   (void)hipFree(c->d_params);
   if (c->h_params) (void)hipHostFree(c->h_params);
   if (c->h_token) (void)hipHostFree(c->h_token);
-  if (c->own_stream && c->stream) (void)hipStreamDestroy(c->stream);
+  if (c->capture) (void)hipStreamDestroy(c->capture);
   delete c;
   return IE_OK;
 }
@@ -353,11 +348,13 @@ int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
         IE_CHECK_HIP(hipGraphExecDestroy(c->graph_exec));
         c->graph_exec = nullptr;
       }
+      // captured on the private stream (capture is not allowed on the legacy
+      // default stream), replayed on the context's stream
       hipGraph_t g = nullptr;
-      IE_CHECK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-      const int rc = enqueue_decode(c, *weights, tokenid_buff, data_buffer, attn_buffer,
-                                    output_distr, output_token, workspace, kv_cache);
-      const hipError_t ec = hipStreamEndCapture(st, &g);
+      IE_CHECK_HIP(hipStreamBeginCapture(c->capture, hipStreamCaptureModeThreadLocal));
+      const int rc = enqueue_decode(c, c->capture, *weights, tokenid_buff, data_buffer,
+                                    attn_buffer, output_distr, output_token, workspace, kv_cache);
+      const hipError_t ec = hipStreamEndCapture(c->capture, &g);
       if (rc != IE_OK) {
         if (g) (void)hipGraphDestroy(g);
         return rc;
@@ -370,7 +367,7 @@ int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
     }
     IE_CHECK_HIP(hipGraphLaunch(c->graph_exec, st));
   } else {
-    IE_TRY(enqueue_decode(c, *weights, tokenid_buff, data_buffer, attn_buffer, output_distr,
+    IE_TRY(enqueue_decode(c, st, *weights, tokenid_buff, data_buffer, attn_buffer, output_distr,
                           output_token, workspace, kv_cache));
   }
   IE_CHECK_HIP(hipMemcpyAsync(c->h_token, output_token, sizeof(int), hipMemcpyDeviceToHost, st));
@@ -914,8 +911,8 @@ int ie_decoder_layer_decode(ie_context* c, const ie_model_weights* weights, int 
              "decoder_layer_decode: null pointer");
   IE_REQUIRE(layer_idx >= 0 && layer_idx < kLayers, "decoder_layer_decode: layer %d", layer_idx);
   IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "decoder_layer_decode: seq_len %d", seq_len);
-  return decoder_layer_decode(c, *weights, layer_idx, d_x, d_attn_out, decode_ws(workspace, 1),
-                              kv_cache, nullptr, seq_len);
+  return decoder_layer_decode(c, c->stream, *weights, layer_idx, d_x, d_attn_out,
+                              decode_ws(workspace, 1), kv_cache, nullptr, seq_len);
 }
 
 int ie_final_norm_lm_head(ie_context* c, int rows, const ie_bf16* d_x, const ie_bf16* d_norm_w,

@@ -197,8 +197,8 @@ constexpr double kSynthStd = 37837.22627754049;
 // ---------------------------------------------------------------- context
 struct Context {
   int device = 0;
-  hipStream_t stream = nullptr;
-  bool own_stream = false;
+  hipStream_t stream = nullptr;    // nullptr = the legacy default stream
+  hipStream_t capture = nullptr;   // private stream the decode graph is captured on
   unsigned int* d_counters = nullptr;       // self-resetting last-block counters
   unsigned long long* d_slots = nullptr;    // 64-bit reduction slots (argmax)
   int* d_params = nullptr;                  // device copy of per-step scalars

@@ -169,34 +169,6 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(AttnDecodeParams
   dst[lane] = pack_bf2(o0 * inv, o1 * inv);
 }
 
-// Causal prefill attention, one workgroup per (query row t, kv head g): q row t
-// sits at absolute position start_pos + t and attends to cache rows
-// 0..start_pos+t (attn.cu:355-363 with the causal mask of softmax.cu:55-107).
-// Output row t is [32 heads][128], the permuted layout of attn_permute.cu:15-31.
-__global__ __launch_bounds__(256) void attn_prefill_rows_kernel(AttnPrefillParams p) {
-  const int t = blockIdx.x, g = blockIdx.y;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int dl = lane & 15;
-  const int h = g * kGQA + wave;
-  const int S = p.start_pos + t + 1;
-  __shared__ float sc[4][kAttnTile];
-  const uint16_t* Kh = p.k + (size_t)g * kKVPlane;
-  const uint16_t* Vh = p.v + (size_t)g * kKVPlane;
-  const u32x4_t qv =
-      reinterpret_cast<const u32x4_t*>(p.q + ((size_t)t * kQHeads + h) * kHeadDim)[dl];
-  float m, l, acc[8];
-  attend_tiles(Kh, Vh, qv, S, 0, (S + kAttnTile - 1) / kAttnTile, sc, m, l, acc);
-  if (lane < 16) {
-    const float inv = 1.0f / l;
-    uint4 o;
-    o.x = pack_bf2(acc[0] * inv, acc[1] * inv);
-    o.y = pack_bf2(acc[2] * inv, acc[3] * inv);
-    o.z = pack_bf2(acc[4] * inv, acc[5] * inv);
-    o.w = pack_bf2(acc[6] * inv, acc[7] * inv);
-    reinterpret_cast<uint4*>(p.out + (size_t)t * kHidden + h * kHeadDim)[dl] = o;
-  }
-}
-
 }  // namespace
 
 size_t attn_decode_partials_bytes(int batch) {
@@ -212,14 +184,6 @@ int launch_attn_decode(const AttnDecodeParams& p, int batch, hipStream_t st) {
                      st, p);
   IE_CHECK_LAUNCH();
   hipLaunchKernelGGL(attn_decode_merge_kernel, dim3(kKVHeads, batch), dim3(256), 0, st, p);
-  IE_CHECK_LAUNCH();
-  return IE_OK;
-}
-
-int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t st) {
-  IE_REQUIRE(p.S >= 1 && p.start_pos >= 0 && p.start_pos + p.S <= kMaxCtx,
-             "attn_prefill: rows [%d, %d) exceed the KV cache", p.start_pos, p.start_pos + p.S);
-  hipLaunchKernelGGL(attn_prefill_rows_kernel, dim3(p.S, kKVHeads), dim3(256), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
