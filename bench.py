@@ -12,8 +12,8 @@ Also reported, on the same run:
                 on the stream it runs on, rotating over the 32 layers' weights so
                 the 256 MB Infinity Cache cannot serve repeats.
   cpu_baseline  the CPU oracle (oracle/, OpenMP) decoding the same model on this
-                host: a bounded sample of decoder layers + lm_head, extrapolated
-                to one token.
+                host: whole decode steps (32 layers + lm_head + argmax) for about
+                10 s after one untimed step.
 
     python bench.py [--gpus 1] [--steps 128] [--warmup 16] [--prompt 512]
 """
@@ -33,15 +33,20 @@ WEIGHT_BYTES_PER_TOKEN = 15_009_849_344          # every weight byte read once p
 KV_BYTES_PER_POS = 131_072                       # 32 layers x (K+V) x 8 heads x 128 x 2 B
 GATE_UP_BYTES = 2 * FFN * HIDDEN * 2 + 2 * HIDDEN * 2 + FFN * 2
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per gate/up launch from rocprofv3 FETCH_SIZE (x2.000) + WRITE_SIZE (x1.000), each
+# factor calibrated on a 256 MiB copy; profiles/decode_gemv_hbm_traffic.md.
+GATE_UP_TRAFFIC = 235_190_000
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(prompt: int, n_layers: int = 3) -> dict:
-    """The oracle's decode of the same workload: n_layers decoder layers at
-    position `prompt` plus lm_head, each timed; one token = 32 layers + lm_head."""
+def cpu_baseline(prompt: int, budget_s: float = 10.0) -> dict:
+    """The oracle decoding the same model on this host: full decode steps
+    (embedding, 32 decoder layers, final norm, lm_head, argmax) at positions
+    prompt, prompt+1, ... against a synthetic KV prefix, for about budget_s
+    seconds.  Weights are generated once beforehand and not timed."""
     import numpy as np
 
     import oracle as orc
@@ -49,27 +54,43 @@ def cpu_baseline(prompt: int, n_layers: int = 3) -> dict:
     threads = min(threads, len(os.sched_getaffinity(0)))
     seed = 0
     cos, sin = orc.rope_tables()
-    kv = orc.synthetic((2, 8, prompt + 1, 128), seed, 9000, 0.0, 1.0)
-    x0 = orc.synthetic((1, HIDDEN), seed, 9001, 0.0, 1.0)
-    t_layers = []
-    for l in range(n_layers):
-        w = orc.layer_weights(seed, l)
-        x = x0.copy()
-        kk, vv = np.ascontiguousarray(kv[0]), np.ascontiguousarray(kv[1])
-        t0 = time.perf_counter()
-        orc.decoder_layer(x, w, prompt, cos, sin, kk, vv, prompt + 1)
-        t_layers.append(time.perf_counter() - t0)
+    layers = [orc.layer_weights(seed, l) for l in range(LAYERS)]
+    emb = orc.embedding(seed)
     lm = orc.lm_head_weight(seed)
     fn = orc.final_norm(seed)
+    cap = prompt + 1024
+    kv = np.zeros((LAYERS, 2, 8, cap, 128), np.uint16)
+    kv[:, :, :, :prompt] = orc.synthetic((LAYERS, 2, 8, prompt, 128), seed, 9000, 0.0, 1.0)
+
+    def step(tok: int, pos: int) -> int:
+        x = orc.emblookup(np.array([tok], np.int32), emb)
+        for l in range(LAYERS):
+            orc.decoder_layer(x, layers[l], pos, cos, sin, kv[l, 0], kv[l, 1], cap)
+        return orc.argmax(orc.matmul(orc.rmsnorm(x, fn), lm, out_f32=True)[0])
+
+    tok = step(1234, prompt)             # untimed: first touch of every weight page
+    pos, n = prompt + 1, 0
     t0 = time.perf_counter()
-    orc.matmul(orc.rmsnorm(x, fn), lm, out_f32=True)
-    t_lm = time.perf_counter() - t0
-    t_tok = LAYERS * (sum(t_layers) / len(t_layers)) + t_lm
-    return {"value": round(1.0 / t_tok, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle decode at position {prompt}: {n_layers} decoder layers "
-                      f"({', '.join(f'{t * 1e3:.0f}' for t in t_layers)} ms) + lm_head "
-                      f"({t_lm * 1e3:.0f} ms), extrapolated to 32 layers + lm_head = "
-                      f"{t_tok * 1e3:.0f} ms/token"}
+    while n < 2 or (time.perf_counter() - t0 < budget_s and pos + 1 < cap):
+        tok = step(tok, pos)
+        pos += 1
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} full oracle decode steps (32 layers + lm_head + argmax) at positions "
+                      f"{prompt + 1}..{pos - 1} after one untimed step, {dt:.1f} s on "
+                      f"{threads} threads"}
+
+
+def calibration_copy(nbytes: int = 256 << 20) -> None:
+    """A plain device-to-device copy of known size, for scaling the HBM
+    FETCH_SIZE / WRITE_SIZE counters of a --pmc run."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def main() -> int:
@@ -81,6 +102,8 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="also run a 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -98,6 +121,8 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.calibration_copy:
+        calibration_copy()
     ctx = Context(0, graph=not args.no_graph)
     log("random-init weights (16.06 GB)")
     W = ModelWeights.random_init(seed=0, std=0.02)
@@ -185,7 +210,7 @@ def main() -> int:
                     "tokens_per_s": round(args.prompt / prefill_s, 1)},
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4096, SwiGLU, RMSNorm> (gate/up)",
                      "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC,
                      "avg_launch_us": round(k_us, 2), "bytes_per_launch": GATE_UP_BYTES},
     }
     del req
