@@ -232,6 +232,19 @@ IE_API int ie_tune_gemv_pairs_per_wave(int ppw);
 /* Plain GEMM Y[m,n] = X[m,k] . W[n,k]^T on the MFMA path (any m >= 1). */
 IE_API int ie_gemm_bf16(ie_context* ctx, int m, int k, int n, const ie_bf16* d_x,
                         const ie_bf16* d_w, ie_bf16* d_y);
+/* The MFMA GEMM with a selectable fused epilogue (no reference counterpart; the
+ * prefill path uses each of them):
+ *   IE_GEMM_BF16    y[m,n] = bf16(X . W0^T)                         (d_y bf16)
+ *   IE_GEMM_RESID   y[m,n] = bf16(y + bf16(X . W0^T))               (d_y bf16, read+written)
+ *   IE_GEMM_F32     y[m,n] = X . W0^T                               (d_y fp32)
+ *   IE_GEMM_SWIGLU  y[m,n] = swiglu(bf16(X . W0^T), bf16(X . W1^T)) (d_y bf16; W0 gate, W1 up)
+ * W0/W1 are [n][k]; n % 4 == 0, k % 64 == 0. */
+#define IE_GEMM_BF16 0
+#define IE_GEMM_RESID 1
+#define IE_GEMM_F32 2
+#define IE_GEMM_SWIGLU 3
+IE_API int ie_gemm_ex(ie_context* ctx, int epilogue, int m, int k, int n, const ie_bf16* d_x,
+                      const ie_bf16* d_w0, const ie_bf16* d_w1, void* d_y);
 
 #ifdef __cplusplus
 }

@@ -101,6 +101,7 @@ SIGNATURES: dict[str, tuple] = {
     "ie_decoder_layer_decode": (_i, [_p, _W, _i, _i, _p, _p, _p, _p]),
     "ie_final_norm_lm_head": (_i, [_p, _i, _p, _p, _p, _p]),
     "ie_gemm_bf16": (_i, [_p, _i, _i, _i, _p, _p, _p]),
+    "ie_gemm_ex": (_i, [_p, _i, _i, _i, _i, _p, _p, _p, _p]),
     "ie_tune_gemv_pairs_per_wave": (_i, [_i]),
 }
 

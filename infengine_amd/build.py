@@ -66,7 +66,10 @@ def build(jobs: int | None = None) -> pathlib.Path:
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(compile_one, sources))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    # -z defs: an unresolved symbol (e.g. a kernel whose host stub was not emitted) fails
+    # the build instead of the first dlopen
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objs),
+          "-o", str(tmp)])
     os.replace(tmp, LIB)
     return LIB
 

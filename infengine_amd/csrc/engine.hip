@@ -738,6 +738,30 @@ int ie_gemm_bf16(ie_context* c, int m, int k, int n, const ie_bf16* d_x, const i
   return launch_gemm(kGemmBf16, g, c->stream);
 }
 
+int ie_gemm_ex(ie_context* c, int epilogue, int m, int k, int n, const ie_bf16* d_x,
+               const ie_bf16* d_w0, const ie_bf16* d_w1, void* d_y) {
+  CTX_OK(c);
+  IE_REQUIRE(d_x && d_w0 && d_y, "gemm_ex: null pointer");
+  IE_REQUIRE(epilogue >= IE_GEMM_BF16 && epilogue <= IE_GEMM_SWIGLU, "gemm_ex: bad epilogue %d",
+             epilogue);
+  IE_REQUIRE(epilogue != IE_GEMM_SWIGLU || d_w1, "gemm_ex: SwiGLU needs the up matrix");
+  static_assert(IE_GEMM_BF16 == kGemmBf16 && IE_GEMM_RESID == kGemmResid &&
+                    IE_GEMM_F32 == kGemmF32 && IE_GEMM_SWIGLU == kGemmSwiglu,
+                "epilogue codes");
+  GemmParams g{};
+  g.x = d_x;
+  g.w0 = d_w0;
+  g.w1 = d_w1;
+  g.n0 = n;
+  if (epilogue == IE_GEMM_F32) g.yf = static_cast<float*>(d_y);
+  else g.y = static_cast<uint16_t*>(d_y);
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  g.ldy = n;
+  return launch_gemm(epilogue, g, c->stream);
+}
+
 int ie_ffn(ie_context* c, int seq_len, const ie_bf16* d_in, ie_bf16* d_out, const ie_bf16* d_wup,
            const ie_bf16* d_wdown, const ie_bf16* d_wgate, void* workspace) {
   CTX_OK(c);

@@ -37,6 +37,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int BM = 128;  // X rows per tile
 constexpr int BN = 128;  // W rows per tile
 constexpr int BK = 64;
+constexpr int kWideMinRows = 128;  // smallest M the wide-tile kernels are considered for
 
 template <int EPI>
 __device__ __forceinline__ const uint16_t* w_row(const GemmParams& p, int ntile, int r) {
@@ -188,6 +189,359 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p, int m_tiles) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide-tile kernel for M >= 128 (prefill): 256 W rows x 128 X rows x 64 k per
+// workgroup of 4 waves; each wave owns 128 W rows x 64 X rows as 4 x 2 tiles of
+// v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators per lane).
+//
+// Operands reach LDS by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds:
+// lane i of a wave writes 16 bytes at LDS base + 16 i), through a 3-stage ring
+// of 48 KiB stages, so the loads for k-step kt+2 are in flight while k-step kt
+// is multiplied.  Each load covers 8 tile rows through its own buffer descriptor
+// (base = the group's first row, size = the rows left in its matrix), so rows
+// past the end of a matrix read as zero, and the k offset is a scalar operand.
+// (The buffer form, not global_load_lds: a FLAT-encoded LDS load makes the
+// compiler treat every later LDS wait as unordered, i.e. lgkmcnt(0).)  The LDS destination of a load is fixed by the lane index, so
+// the bank swizzle is applied on the global side: LDS chunk slot s of tile row r
+// holds global chunk s ^ swz(r).  swz(r) = ((r >> 1) & 7) ^ ((r >> 4) & 1) makes
+// the 16 (or 32) rows that one ds_read_b128 phase touches land in distinct
+// 16-byte bank groups for both a 64-bank and a 128-bank LDS.
+//
+// The loads are counted by vmcnt; the compiler does not track them, so every
+// k-step starts with an explicit "s_waitcnt vmcnt(N); s_barrier": N = the loads
+// of the one younger stage still allowed in flight (12 per wave), 0 on the last
+// step.  No other vector-memory instruction is issued inside the loop.
+namespace wide {
+
+constexpr int BN = 256;  // W rows per tile
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw 32-bit access)
+
+// Tile geometry: BN = 256 W rows x BM (128 or 256) X rows x BK (32 or 64) k, in a ring of
+// STAGES LDS stages.  Every wave owns 128 W rows x 64 X rows, so a workgroup has
+// NW = 2 * BM / 64 waves (4 or 8).
+template <int BM_, int BK_, int STAGES_>
+struct Cfg {
+  static constexpr int BM = BM_;
+  static constexpr int BK = BK_;
+  static constexpr int STAGES = STAGES_;
+  static constexpr int WM = BM / 64;                 // waves along X
+  static constexpr int NW = 2 * WM;                  // waves per workgroup
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
+  static constexpr int RPL = 64 / CPR;               // tile rows per wave-wide load
+  static constexpr int W_CHUNKS = BN * CPR;
+  static constexpr int X_CHUNKS = BM * CPR;
+  static constexpr int STAGE = W_CHUNKS + X_CHUNKS;  // chunks per stage
+  static constexpr int W_LOADS = W_CHUNKS / THREADS; // loads per thread per stage
+  static constexpr int X_LOADS = X_CHUNKS / THREADS;
+  static constexpr int LOADS = W_LOADS + X_LOADS;
+  static constexpr int KSUB = BK / 16;               // MFMA k16 sub-steps per stage
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(STAGES * STAGE * 16 <= 160 * 1024, "LDS");
+  // Chunk slot s of row r holds global chunk s ^ swz(r): the 16 (or 32) consecutive rows one
+  // ds_read_b128 phase touches fall in distinct 16-byte bank groups (64- or 128-bank LDS).
+  static __device__ __forceinline__ int swz(int r) {
+    if constexpr (CPR == 8) return ((r >> 1) & 7) ^ ((r >> 4) & 1);
+    else return ((r >> 2) & 3) ^ ((r >> 4) & 1);
+  }
+};
+
+// Buffer descriptor for the `rows` W rows starting at tile-local row r (all in one matrix).
+template <int EPI>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t w_group(const GemmParams& p, int ntile, int r) {
+  const uint16_t* base;
+  long long rows;
+  if constexpr (EPI == kGemmSwiglu) {
+    // local row r -> [32 gate | 32 up] x 4; output column ntile*128 + (r/64)*32 + r%32
+    const int col = ntile * 128 + (r >> 6) * 32 + (r & 31);
+    base = ((r & 63) < 32 ? p.w0 : p.w1) + (size_t)col * p.K;
+    rows = p.N - col;
+  } else {
+    const int R = ntile * BN + r;
+    const int e0 = min(p.n0, p.N), e1 = min(p.n0 + p.n1, p.N);
+    if (R < e0) {
+      base = p.w0 + (size_t)R * p.K;
+      rows = e0 - R;
+    } else if (R < e1) {
+      base = p.w1 + (size_t)(R - e0) * p.K;
+      rows = e1 - R;
+    } else if (R < p.N) {
+      base = p.w2 + (size_t)(R - e1) * p.K;
+      rows = p.N - R;
+    } else {
+      base = p.w0;
+      rows = 0;
+    }
+  }
+  const long long bytes = rows > 0 ? rows * p.K * 2 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)min(bytes, 0x7fffffffLL), kBufferFlags);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_group(const GemmParams& p, int m0, int r) {
+  const int R = m0 + r;
+  const long long rows = p.M - R;
+  const long long bytes = rows > 0 ? rows * p.K * 2 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(p.x + (size_t)min(R, p.M - 1) * p.K), 0,
+                                           (int)min(bytes, 0x7fffffffLL), kBufferFlags);
+}
+
+// Direct-to-LDS loads of k-step kt into ring slot `stage`.  (Plain device functions, not
+// lambdas: a lambda around the amdgcn builtin inside a kernel template stops the host pass
+// from emitting the kernel's launch stub.)
+template <class C>
+__device__ __forceinline__ void issue_stage(u32x4_t* lds, const __amdgpu_buffer_rsrc_t* rsrc,
+                                            const uint32_t* voff, int wv, int kt, int stage) {
+  const uint32_t soff = (uint32_t)(kt * C::BK * 2);
+#pragma unroll
+  for (int j = 0; j < C::LOADS; ++j) {
+    const bool is_w = j < C::W_LOADS;
+    const int g = wv + C::NW * (is_w ? j : j - C::W_LOADS);
+    u32x4_t* dst = &lds[stage * C::STAGE + (is_w ? 0 : C::W_CHUNKS) + g * 64];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[j], (lds_void*)dst, 16, voff[j], soff, 0, 0);
+  }
+}
+
+// MFMA operand fragments of k16 sub-step kk: lane l supplies tile row base + l%32,
+// k chunk 2*kk + l/32 (4 W fragments, 2 X fragments).
+template <class C>
+__device__ __forceinline__ void read_frags(const u32x4_t* st, int a_row, int b_row, int kk, int fh,
+                                           int fs, bf16x8_t* af, bf16x8_t* bfr) {
+  const int ch = (2 * kk + fh) ^ fs;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) af[i] = __builtin_bit_cast(bf16x8_t, st[a_row + i * 32 * C::CPR + ch]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) bfr[j] = __builtin_bit_cast(bf16x8_t, st[b_row + j * 32 * C::CPR + ch]);
+}
+
+// 8 bf16 at dst (8-byte aligned; 16-byte aligned when a16)
+__device__ __forceinline__ void store16(uint16_t* dst, uint2 lo, uint2 hi, bool a16) {
+  if (a16) {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  } else {
+    reinterpret_cast<uint2*>(dst)[0] = lo;
+    reinterpret_cast<uint2*>(dst)[1] = hi;
+  }
+}
+
+// Wait until at most n stages of loads (n * loads per stage) are in flight, then barrier.
+template <int LOADS, int N>
+__device__ __forceinline__ void wait_stage_n(int n) {
+  if constexpr (N < 0) {
+    return;
+  } else {
+    if (n == N) {
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N * LOADS) : "memory");
+      return;
+    }
+    wait_stage_n<LOADS, N - 1>(n);
+  }
+}
+
+// Logical tile of workgroup b.  Workgroups are dealt round-robin to the 8 XCDs, so each XCD
+// is handed a contiguous range of W tiles (n_tiles / 8); inside it the range is swept in
+// groups of MAPG W tiles x all X tiles, X-tile-major within a group, so the 32 tiles an XCD
+// runs at once share W rows and X rows in its L2.
+template <int MAPG>
+__device__ __forceinline__ void tile_of(int b, int nb, int m_tiles, int& mtile, int& ntile) {
+  const int n_tiles = nb / m_tiles;
+  if (nb % 8 == 0 && n_tiles % (8 * MAPG) == 0) {
+    const int x = b % 8, local = b / 8;
+    const int grp = local / (MAPG * m_tiles), within = local % (MAPG * m_tiles);
+    ntile = x * (n_tiles / 8) + grp * MAPG + within % MAPG;
+    mtile = within / MAPG;
+  } else {
+    const int t = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    mtile = t % m_tiles;
+    ntile = t / m_tiles;
+  }
+}
+
+template <int EPI, int BM, int BK, int STAGES, int MAPG>
+__global__ __launch_bounds__(BM * 2) __attribute__((amdgpu_waves_per_eu(BM / 128, BM / 128)))
+void gemm_wide_kernel(GemmParams p, int m_tiles) {
+  using C = Cfg<BM, BK, STAGES>;
+  __shared__ u32x4_t lds[STAGES * C::STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave / C::WM, wm = wave % C::WM;
+  int mtile, ntile;
+  tile_of<MAPG>(blockIdx.x, gridDim.x, m_tiles, mtile, ntile);
+  const int m0 = mtile * BM;
+
+  // load j of this wave covers tile rows RPL*g .. RPL*g+RPL-1 with g = wave + NW*j;
+  // lane i fills LDS slot (row RPL*g + i/CPR, chunk i%CPR) from global chunk (i%CPR) ^ swz(row)
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  __amdgpu_buffer_rsrc_t rsrc[C::LOADS];
+  uint32_t voff[C::LOADS];
+#pragma unroll
+  for (int j = 0; j < C::LOADS; ++j) {
+    const bool is_w = j < C::W_LOADS;
+    const int g = wv + C::NW * (is_w ? j : j - C::W_LOADS);
+    rsrc[j] = is_w ? w_group<EPI>(p, ntile, g * C::RPL) : x_group(p, m0, g * C::RPL);
+    const int rl = lane / C::CPR, c = (lane % C::CPR) ^ C::swz(g * C::RPL + rl);
+    voff[j] = (uint32_t)((rl * p.K + c * 8) * 2);
+  }
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // fragment addressing: operand lane l supplies tile row base + l%32, k chunk 2*kk + l/32
+  const int fr = lane & 31, fh = lane >> 5, fs = C::swz(fr);
+  const int a_row = (wn * 128 + fr) * C::CPR;
+  const int b_row = C::W_CHUNKS + (wm * 64 + fr) * C::CPR;
+
+  // The epilogue's kernel arguments are pulled into SGPRs here: a scalar load still in
+  // flight inside the loop would force every LDS wait there to lgkmcnt(0).
+  uint16_t* const y = p.y;
+  float* const yf = p.yf;
+  asm volatile("" ::"s"(y), "s"(yf), "s"(p.ldy), "s"(p.M), "s"(p.N));
+
+  const int KT = p.K / BK;
+#pragma unroll
+  for (int s0 = 0; s0 < STAGES - 1; ++s0)
+    if (s0 < KT) issue_stage<C>(lds, rsrc, voff, wv, s0, s0);
+  for (int kt = 0; kt < KT; ++kt) {
+    // stage kt must have landed; the younger stages issued so far may stay in flight
+    wait_stage_n<C::LOADS, STAGES - 2>(min(STAGES - 2, KT - 1 - kt));
+    if (kt + STAGES - 1 < KT)
+      issue_stage<C>(lds, rsrc, voff, wv, kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+    const u32x4_t* st = &lds[(kt % STAGES) * C::STAGE];
+    bf16x8_t af[2][4], bfr[2][2];
+    // fragments of sub-step kk+1 are read while the 8 MFMAs of kk run (the scheduling
+    // fences keep it so: left alone the scheduler reads each fragment just before its use)
+    read_frags<C>(st, a_row, b_row, 0, fh, fs, af[0], bfr[0]);
+#pragma unroll
+    for (int kk = 0; kk < C::KSUB; ++kk) {
+      const int cur = kk & 1;
+      if (kk + 1 < C::KSUB) read_frags<C>(st, a_row, b_row, kk + 1, fh, fs, af[cur ^ 1], bfr[cur ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue: accumulator element 4*g + q of tile (i, j) is
+  //      W row wn*128 + 32*i + 8*g + 4*(lane/32) + q,  X row m0 + wm*64 + 32*j + lane%32
+  if constexpr (EPI == kGemmF32) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int m = m0 + wm * 64 + j * 32 + fr;
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = ntile * BN + wn * 128 + i * 32 + 8 * g + 4 * fh;
+          if (n < p.N)
+            *reinterpret_cast<float4*>(yf + (size_t)m * p.ldy + n) =
+                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        }
+    }
+  } else {
+    // bf16 results go through LDS so that the global stores are whole, coalesced row segments
+    // (a lane's accumulators are 4 columns of 32 different rows; storing them directly writes
+    // every 128-byte line in eight 16-byte pieces).  The tile is [BM][OUTN] bf16 held as
+    // 8-byte units; unit u of row r sits at u ^ (r % 32), which spreads the 32 rows one
+    // write instruction touches over distinct banks without padding.
+    constexpr int OUTN = (EPI == kGemmSwiglu) ? 128 : BN;  // output columns per tile
+    constexpr int UPR = OUTN / 4;                            // 8-byte units per row
+    static_assert(BM * OUTN * 2 <= STAGES * C::STAGE * 16, "output tile must fit the LDS ring");
+    uint2* ot = reinterpret_cast<uint2*>(lds);
+    __syncthreads();  // every wave is done reading the ring
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = wm * 64 + j * 32 + fr;
+      const int sw = r & 31;
+      if constexpr (EPI == kGemmSwiglu) {
+#pragma unroll
+        for (int i = 0; i < 4; i += 2)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            uint32_t o[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              float v[2];
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const float gt = bf2f(f2bf(acc[i][j][4 * g + 2 * q + e]));
+                const float up = bf2f(f2bf(acc[i + 1][j][4 * g + 2 * q + e]));
+                v[e] = gt * (1.0f / (1.0f + expf(-gt))) * up;
+              }
+              o[q] = pack_bf2(v[0], v[1]);
+            }
+            const int u = (2 * wn + i / 2) * 8 + 2 * g + fh;
+            ot[r * UPR + (u ^ sw)] = make_uint2(o[0], o[1]);
+          }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int u = wn * 32 + i * 8 + 2 * g + fh;
+            ot[r * UPR + (u ^ sw)] = make_uint2(pack_bf2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+                                                pack_bf2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]));
+          }
+      }
+    }
+    __syncthreads();
+    // copy-out: 16 bytes (8 columns) per thread, consecutive threads along a row
+    const int n_base = ntile * OUTN;
+    const bool ld16 = (p.ldy & 7) == 0;  // rows 16-byte aligned: one 16-byte store per thread
+#pragma unroll 4
+    for (int P = tid; P < BM * UPR / 2; P += C::THREADS) {
+      const int r = P / (UPR / 2), c2 = P % (UPR / 2);
+      const int m = m0 + r, n = n_base + 8 * c2;
+      if (m >= p.M || n >= p.N) continue;
+      const int sw = r & 31;
+      const uint2 lo = ot[r * UPR + ((2 * c2) ^ sw)], hi = ot[r * UPR + ((2 * c2 + 1) ^ sw)];
+      uint16_t* dst = y + (size_t)m * p.ldy + n;
+      if constexpr (EPI == kGemmResid) {
+        // y = bf16(y + bf16(acc)) (residual_add.cu:17-19); the LDS tile holds bf16(acc)
+        const uint2 a = *reinterpret_cast<const uint2*>(dst);
+        const uint2 o0 = make_uint2(pack_bf2(bf_lo(a.x) + bf_lo(lo.x), bf_hi(a.x) + bf_hi(lo.x)),
+                                    pack_bf2(bf_lo(a.y) + bf_lo(lo.y), bf_hi(a.y) + bf_hi(lo.y)));
+        if (n + 8 <= p.N) {
+          const uint2 b = *reinterpret_cast<const uint2*>(dst + 4);
+          const uint2 o1 = make_uint2(pack_bf2(bf_lo(b.x) + bf_lo(hi.x), bf_hi(b.x) + bf_hi(hi.x)),
+                                      pack_bf2(bf_lo(b.y) + bf_lo(hi.y), bf_hi(b.y) + bf_hi(hi.y)));
+          store16(dst, o0, o1, ld16);
+        } else {
+          *reinterpret_cast<uint2*>(dst) = o0;
+        }
+      } else {
+        if (n + 8 <= p.N) store16(dst, lo, hi, ld16);
+        else *reinterpret_cast<uint2*>(dst) = lo;
+      }
+    }
+  }
+}
+
+}  // namespace wide
+
+template <int EPI, int BM = 128, int BK = 64, int STAGES = 3, int MAPG = 1>
+int launch_wide(const GemmParams& p, hipStream_t st) {
+  const int m_tiles = (p.M + BM - 1) / BM;
+  const int n_tiles = (EPI == kGemmSwiglu) ? (p.N + 127) / 128 : (p.N + wide::BN - 1) / wide::BN;
+  const long long blocks = (long long)m_tiles * n_tiles;
+  IE_REQUIRE(blocks <= 0x7fffffff, "gemm: too many tiles");
+  hipLaunchKernelGGL((wide::gemm_wide_kernel<EPI, BM, BK, STAGES, MAPG>), dim3((unsigned)blocks),
+                     dim3(BM * 2), 0, st, p, m_tiles);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
 template <int EPI>
 int launch_e(const GemmParams& p, hipStream_t st) {
   const int m_tiles = (p.M + BM - 1) / BM;
@@ -206,11 +560,44 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
   IE_REQUIRE(p.K % BK == 0, "gemm: K=%d must be a multiple of %d", p.K, BK);
   IE_REQUIRE(p.N % 4 == 0, "gemm: N=%d must be a multiple of 4", p.N);
   IE_REQUIRE(p.ldy >= p.N, "gemm: ldy=%d < N=%d", p.ldy, p.N);
-  switch (epi) {
-    case kGemmBf16: return launch_e<kGemmBf16>(p, st);
-    case kGemmResid: return launch_e<kGemmResid>(p, st);
-    case kGemmF32: return launch_e<kGemmF32>(p, st);
-    case kGemmSwiglu: return launch_e<kGemmSwiglu>(p, st);
+  // a 16-row load group must not straddle two weight matrices
+  IE_REQUIRE(epi == kGemmSwiglu || ((p.n0 >= p.N || p.n0 % 16 == 0) &&
+                                    (p.n0 + p.n1 >= p.N || (p.n0 + p.n1) % 16 == 0)),
+             "gemm: weight split points n0=%d n0+n1=%d inside N=%d must be multiples of 16", p.n0,
+             p.n0 + p.n1, p.N);
+  // Tile shape by a cost model: time = rounds of workgroups over the 256 CUs x the time of one
+  // tile at the measured per-CU rate of that shape (256x256: 1085, 256x128: 900,
+  // 128x128: 750 TFLOP/s over the chip at full occupancy).  Big tiles win when they fill the
+  // chip (QKV, gate/up at S = 2048); at small S the 128 x 128 tile keeps more CUs busy.
+  const bool swiglu = epi == kGemmSwiglu;
+  auto cost = [&](int tm, int tn_out, double us_per_tile) {
+    const long long tiles = (long long)((p.M + tm - 1) / tm) * ((p.N + tn_out - 1) / tn_out);
+    return (double)((tiles + 255) / 256) * us_per_tile;
+  };
+  const double c_small = cost(128, swiglu ? 64 : 128, 128.0 * 128 / 750.0);
+  const double c_wide = p.M >= kWideMinRows ? cost(128, swiglu ? 128 : 256, 256.0 * 128 / 900.0) : 1e30;
+  const double c_big = (p.M >= kWideMinRows && epi != kGemmF32)
+                           ? cost(256, swiglu ? 128 : 256, 256.0 * 256 / 1085.0) : 1e30;
+  if (c_big < c_wide && c_big < c_small) {
+    switch (epi) {
+      case kGemmBf16: return launch_wide<kGemmBf16, 256, 64, 2>(p, st);
+      case kGemmResid: return launch_wide<kGemmResid, 256, 64, 2>(p, st);
+      case kGemmSwiglu: return launch_wide<kGemmSwiglu, 256, 64, 2>(p, st);
+    }
+  } else if (c_wide < c_small) {
+    switch (epi) {
+      case kGemmBf16: return launch_wide<kGemmBf16>(p, st);
+      case kGemmResid: return launch_wide<kGemmResid>(p, st);
+      case kGemmF32: return launch_wide<kGemmF32>(p, st);
+      case kGemmSwiglu: return launch_wide<kGemmSwiglu>(p, st);
+    }
+  } else {
+    switch (epi) {
+      case kGemmBf16: return launch_e<kGemmBf16>(p, st);
+      case kGemmResid: return launch_e<kGemmResid>(p, st);
+      case kGemmF32: return launch_e<kGemmF32>(p, st);
+      case kGemmSwiglu: return launch_e<kGemmSwiglu>(p, st);
+    }
   }
   set_error("gemm: bad epilogue %d", epi);
   return IE_ERR_INVALID_ARG;

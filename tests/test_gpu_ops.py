@@ -187,6 +187,49 @@ def test_gemm_mfma_prefill_shape_sampled_rows(hip, ctx):
     assert_close(orc.bf16_to_f32(got), orc.bf16_to_f32(want), what="gemm 2048")
 
 
+GEMM_EPI = {"bf16": 0, "resid": 1, "f32": 2, "swiglu": 3}
+
+
+@pytest.mark.parametrize("epi", list(GEMM_EPI))
+@pytest.mark.parametrize("m,n", [(300, 1000), (2048, 6144), (2048, 4096)])
+def test_gemm_epilogues(hip, ctx, epi, m, n):
+    """Every fused epilogue of the MFMA GEMM on each tile shape the launcher picks: a ragged
+    size (128 x 128 tiles), and the prefill sizes that select 256 x 256 tiles (bf16 / resid at
+    n = 6144, SwiGLU at n = 4096) and 256 x 128 tiles (the others); sampled rows at m = 2048."""
+    k = 4096
+    say(f"gemm_ex {epi} m={m} k={k} n={n}")
+    x = orc.synthetic((m, k), 21, m, 0.0, 1.0)
+    w0 = orc.synthetic((n, k), 21, n + 1, 0.0, 0.02)
+    w1 = orc.synthetic((n, k), 21, n + 2, 0.0, 0.02)
+    y0 = orc.synthetic((m, n), 21, n + 3, 0.0, 1.0)
+    if epi == "f32":
+        out = torch.empty(m, n, dtype=torch.float32, device="cuda")
+    else:
+        out = dev(y0) if epi == "resid" else bf16_empty(m, n)
+    hip.check(hip.lib.ie_gemm_ex(ctx.handle, GEMM_EPI[epi], m, k, n, P(dev(x)), P(dev(w0)),
+                                 P(dev(w1)), P(out)))
+    sync()
+    rows = np.arange(m) if m <= 512 else np.random.default_rng(2).choice(m, 48, replace=False)
+    rows[:2] = [0, m - 1]
+    xs = np.ascontiguousarray(x[rows])
+    got = host(out)[rows]
+    if epi == "f32":
+        assert_close(got, orc.matmul(xs, w0, out_f32=True), tol=1e-4, what="gemm f32")
+        return
+    if epi == "bf16":
+        want = orc.matmul(xs, w0)
+    elif epi == "resid":
+        want = orc.residual_add(np.ascontiguousarray(y0[rows]), orc.matmul(xs, w0))
+    else:
+        want = orc.swiglu(orc.matmul(xs, w0), orc.matmul(xs, w1))
+    assert_close(orc.bf16_to_f32(got), orc.bf16_to_f32(want), what=f"gemm {epi}")
+    # SwiGLU compounds a 1-ulp difference in gate or up (summation order) through g*silu(g)*u;
+    # the residual add cancels (y0 ~ -acc), so a 1-ulp product difference can be several ulps
+    # of a small sum: admit 1e-3 of such elements (each still within 1e-2 of the scale)
+    assert_bf16_close(got, want, ulps=4 if epi == "swiglu" else 2, what=f"gemm {epi}",
+                      outlier_frac=1e-3 if epi == "resid" else 0.0)
+
+
 # ---------------------------------------------------------------- FFN (config 1)
 def _ffn_weights(seed):
     return (orc.synthetic((F, H), seed, 1, 0.0, 0.02), orc.synthetic((F, H), seed, 2, 0.0, 0.02),
