@@ -229,6 +229,9 @@ IE_API int ie_final_norm_lm_head(ie_context* ctx, int rows, const ie_bf16* d_x,
  * (0 restores the built-in per-shape choice).  Affects kernels launched after
  * the call, on every context of the process. */
 IE_API int ie_tune_gemv_pairs_per_wave(int ppw);
+/* Tuning (no reference counterpart): force the decode GEMV's waves per workgroup
+ * (4, 8 or 16; 0 restores the built-in choice).  Same scope as above. */
+IE_API int ie_tune_gemv_waves(int waves);
 /* Plain GEMM Y[m,n] = X[m,k] . W[n,k]^T on the MFMA path (any m >= 1). */
 IE_API int ie_gemm_bf16(ie_context* ctx, int m, int k, int n, const ie_bf16* d_x,
                         const ie_bf16* d_w, ie_bf16* d_y);

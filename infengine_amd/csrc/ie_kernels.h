@@ -37,6 +37,7 @@ struct GemvParams {
 // K must be 4096 or 14336.  rows > 1 re-reads the weights once per row.
 int launch_gemv(int K, int epi, bool norm, GemvParams p, int rows, hipStream_t st);
 int default_ppw(int n_pairs);
+int gemv_waves(int K, int epi, int n_pairs);
 
 // ------------------------------------------------------------ decode attention
 struct AttnDecodeParams {

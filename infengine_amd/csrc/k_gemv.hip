@@ -116,18 +116,18 @@ __device__ __forceinline__ void load_step(const u32x4_t* a, const u32x4_t* b, in
   }
 }
 
-template <int K, int EPI, bool NORM>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+template <int K, int EPI, bool NORM, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   constexpr int NC = K / 512;                 // 16-byte chunks per lane per row
   constexpr int G = (K == 4096) ? 4 : 7;      // chunks per pipeline step
   constexpr int NG = NC / G;                  // steps per row pair
   static_assert(NC % G == 0, "K must be a multiple of 512*G");
   __shared__ u32x4_t xs[K / 8];
-  __shared__ float red[4];
+  __shared__ float red[WAVES];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = blockIdx.y;
-  const int first = (blockIdx.x * 4 + wave) * p.ppw;
+  const int first = (blockIdx.x * WAVES + wave) * p.ppw;
   const int npairs = max(0, min(p.ppw, p.n_pairs - first));
   const int nsteps = npairs * NG;
 
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(p.x + (size_t)row * p.x_stride);
   if constexpr (NORM) {
     float ss = 0.f;
-    for (int i = tid; i < K / 8; i += 256) {
+    for (int i = tid; i < K / 8; i += WAVES * 64) {
       const u32x4_t v = x4[i];
       xs[i] = v;
       ss += sumsq8(v);
@@ -152,12 +152,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     ss = wave_sum(ss);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) tot += red[w];
     const float r = rsqrtf(tot / (float)K + kRmsEps);
     const u32x4_t* w4 = reinterpret_cast<const u32x4_t*>(p.norm_w);
-    for (int i = tid; i < K / 8; i += 256) xs[i] = norm8(xs[i], w4[i], r);
+    for (int i = tid; i < K / 8; i += WAVES * 64) xs[i] = norm8(xs[i], w4[i], r);
   } else {
-    for (int i = tid; i < K / 8; i += 256) xs[i] = x4[i];
+    for (int i = tid; i < K / 8; i += WAVES * 64) xs[i] = x4[i];
   }
   __syncthreads();
 
@@ -197,13 +199,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   }
 }
 
-template <int K, int EPI, bool NORM>
-int launch_t(const GemvParams& p, int rows, hipStream_t st) {
+template <int K, int EPI, bool NORM, int WAVES>
+int launch_w(const GemvParams& p, int rows, hipStream_t st) {
   const int waves = (p.n_pairs + p.ppw - 1) / p.ppw;
-  dim3 grid((waves + 3) / 4, rows);
-  hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM>), grid, dim3(256), 0, st, p);
+  dim3 grid((waves + WAVES - 1) / WAVES, rows);
+  hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES>), grid, dim3(WAVES * 64), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
+}
+
+template <int K, int EPI, bool NORM>
+int launch_t(const GemvParams& p, int rows, hipStream_t st) {
+  switch (gemv_waves(K, EPI, p.n_pairs)) {
+    case 8: return launch_w<K, EPI, NORM, 8>(p, rows, st);
+    case 16: return launch_w<K, EPI, NORM, 16>(p, rows, st);
+    default: return launch_w<K, EPI, NORM, 4>(p, rows, st);
+  }
 }
 
 template <int K>
@@ -228,7 +239,19 @@ int launch_k(int epi, bool norm, const GemvParams& p, int rows, hipStream_t st) 
 
 namespace {
 int g_ppw_override = 0;
+int g_waves_override = 0;
 }  // namespace
+
+// Waves per workgroup: each workgroup stages (and for RMSNorm ops normalises) the whole input
+// vector once, so more waves per workgroup means less of that per weight byte, at the price of
+// coarser occupancy.
+int gemv_waves(int K, int epi, int n_pairs) {
+  if (g_waves_override > 0) return g_waves_override;
+  (void)K;
+  (void)epi;
+  (void)n_pairs;
+  return 8;
+}
 
 int default_ppw(int n_pairs) {
   if (g_ppw_override > 0) return g_ppw_override;
@@ -253,6 +276,13 @@ int launch_gemv(int K, int epi, bool norm, GemvParams p, int rows, hipStream_t s
 }
 
 }  // namespace ie
+
+extern "C" int ie_tune_gemv_waves(int waves) {
+  IE_REQUIRE(waves == 0 || waves == 4 || waves == 8 || waves == 16,
+             "tune_gemv_waves: %d not one of 0 (default), 4, 8, 16", waves);
+  ie::g_waves_override = waves;
+  return IE_OK;
+}
 
 extern "C" int ie_tune_gemv_pairs_per_wave(int ppw) {
   IE_REQUIRE(ppw >= 0 && ppw <= 64, "tune_gemv_pairs_per_wave: %d out of [0, 64]", ppw);

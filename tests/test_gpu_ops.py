@@ -272,16 +272,20 @@ def _attn_weights(seed):
     return w, {k: dev(v) for k, v in w.items()}
 
 
-def test_decode_attn_config2(hip, ctx, rope):
-    """decode_attn at position 2047 over 2047 cached rows; KV placement bit-exact."""
+@pytest.mark.parametrize("pos", [0, 99, 2047, 3000])
+def test_decode_attn_config2(hip, ctx, rope, pos):
+    """decode_attn at position pos over pos cached rows (config 2: 2047); KV placement
+    bit-exact.  Covers one row, a partial 64-row tile, one tile per split (2048) and
+    several tiles per split (3001)."""
     cos, sin, dcos, dsin = rope
-    say("decode_attn seq_len=2048 layer 5")
+    say(f"decode_attn seq_len={pos + 1} layer 5")
     w, dw = _attn_weights(15)
-    layer, pos = 5, 2047
+    layer = 5
     kv = torch.zeros(hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
     kv5 = kv.view(32, 2, 8, 8192, 128)[layer]
     prior = orc.synthetic((2, 8, pos, 128), 15, 500, 0.0, 1.0)
-    kv5[:, :, :pos] = dev(prior)
+    if pos:
+        kv5[:, :, :pos] = dev(prior)
     x = orc.synthetic((1, H), 15, 501, 0.0, 1.0)           # the already-normalised input
     out = bf16_empty(1, H)
     ws = torch.zeros(hip.lib.ie_attn_workspace_size(1), dtype=torch.uint8, device="cuda")
