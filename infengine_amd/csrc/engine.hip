@@ -99,9 +99,11 @@ int qkv_rope_gemv(const ie_layer& L, const ie_rope_weights& rope, const uint16_t
   return launch_gemv(kHidden, kEpiQkvRope, norm_w != nullptr, p, 1, st);
 }
 
+// merge: also write the bf16 attention output to `out` (merge kernel, up to kAttnSplits
+// splits); otherwise only the partials are written, for an O projection that merges them.
 int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs& w,
-                unsigned int* counters, const int* d_seq_len, int seq_len, int batch,
-                long long cache_stride, hipStream_t st) {
+                const int* d_seq_len, int seq_len, int batch, long long cache_stride, bool merge,
+                hipStream_t st) {
   AttnDecodeParams a{};
   a.q = q;
   a.k_cache = kvl;
@@ -112,7 +114,8 @@ int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs&
   a.part_ml = w.part_ml;
   a.d_seq_len = d_seq_len;
   a.seq_len = seq_len;
-  return launch_attn_decode(a, batch, st);
+  a.max_splits = merge ? kAttnSplits : kAttnFusedSplits;
+  return launch_attn_decode(a, batch, merge, st);
 }
 
 int gemv_plain(int K, int epi, const uint16_t* x, const uint16_t* norm_w, const uint16_t* w0,
@@ -131,16 +134,38 @@ int gemv_plain(int K, int epi, const uint16_t* x, const uint16_t* norm_w, const 
   return launch_gemv(K, epi, norm_w != nullptr, p, rows, st);
 }
 
+// True when the decode step merges the attention partials inside the O projection (no
+// merge launch); the host-known context bound decides (graph capture keys on it).
+bool attn_fused(int seq_len) { return seq_len <= kAttnFusedMaxCtx; }
+
+// seq_len: the context length; with d_seq_len set the kernels read it from there and seq_len
+// only bounds it on the host (it picks the attention path).
 int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, int layer,
                          uint16_t* x, uint16_t* attn_out, const DecodeWs& w, void* kv,
                          const int* d_seq_len, int seq_len) {
+  (void)c;
   const ie_layer& L = W.layers[layer];
   uint16_t* kvl = kv_layer(kv, layer);
   IE_TRY(qkv_rope_gemv(L, W.rope, x, L.input_layernorm, w.q, kvl, d_seq_len, seq_len - 1, st));
-  IE_TRY(attn_decode(w.q, kvl, attn_out, w, c->d_counters + kCntAttn, d_seq_len, seq_len, 1, 0,
-                     st));
-  IE_TRY(gemv_plain(kHidden, kEpiResid, attn_out, nullptr, L.transformer.w_o, nullptr,
-                    kHidden / 2, x, nullptr, 1, 0, st));
+  const bool fused = attn_fused(seq_len);
+  IE_TRY(attn_decode(w.q, kvl, attn_out, w, d_seq_len, seq_len, 1, 0, !fused, st));
+  if (fused) {
+    // O projection + residual, its input merged from the split partials in its prologue
+    GemvParams p{};
+    p.w0 = L.transformer.w_o;
+    p.out = x;
+    p.n_pairs = kHidden / 2;
+    p.x_stride = kHidden;
+    p.d_seq_len = d_seq_len;
+    p.pos = seq_len;
+    p.attn_part_o = w.part_o;
+    p.attn_part_ml = w.part_ml;
+    p.attn_max_splits = kAttnFusedSplits;
+    IE_TRY(launch_gemv(kHidden, kEpiResid, false, p, 1, st));
+  } else {
+    IE_TRY(gemv_plain(kHidden, kEpiResid, attn_out, nullptr, L.transformer.w_o, nullptr,
+                      kHidden / 2, x, nullptr, 1, 0, st));
+  }
   IE_TRY(gemv_plain(kHidden, kEpiSwiglu, x, L.post_attention_layernorm, L.ffn_block.w_gate,
                     L.ffn_block.w_up, kFFN, w.h, nullptr, 1, 0, st));
   IE_TRY(gemv_plain(kFFN, kEpiResid, w.h, nullptr, L.ffn_block.w_down, nullptr, kHidden / 2, x,
@@ -148,14 +173,14 @@ int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, 
   return IE_OK;
 }
 
-int enqueue_decode(Context* c, hipStream_t st, const ie_model_weights& W, int* tokenid_buff,
-                   uint16_t* data, uint16_t* attn, float* logits, int* out_tok, void* ws,
-                   void* kv) {
+int enqueue_decode(Context* c, hipStream_t st, const ie_model_weights& W, int seq_len,
+                   int* tokenid_buff, uint16_t* data, uint16_t* attn, float* logits, int* out_tok,
+                   void* ws, void* kv) {
   const int* d_sl = c->d_params;
   const DecodeWs w = decode_ws(ws, 1);
   IE_TRY(launch_emblookup(1, tokenid_buff, W.emb_lookup, data, d_sl, 0, st));
   for (int l = 0; l < kLayers; ++l)
-    IE_TRY(decoder_layer_decode(c, st, W, l, data, attn, w, kv, d_sl, 0));
+    IE_TRY(decoder_layer_decode(c, st, W, l, data, attn, w, kv, d_sl, seq_len));
   IE_TRY(gemv_plain(kHidden, kEpiF32, data, W.final_norm, W.lm_head, nullptr, kVocab / 2,
                     nullptr, logits, 1, kVocab, st));
   IE_TRY(launch_argmax_rows(1, kVocab, logits, out_tok, c->d_slots, c->d_counters + kCntArgmax,
@@ -342,7 +367,9 @@ int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
     const void* key[12] = {(const void*)weights, tokenid_buff, data_buffer, attn_buffer,
                            output_distr, output_token, workspace, kv_cache,
                            (const void*)(uintptr_t)hash_bytes(weights, sizeof(*weights)),
-                           nullptr, nullptr, nullptr};
+                           // the captured attention path depends on the context length
+                           (const void*)(uintptr_t)(attn_fused(seq_len) ? 1 : 2), nullptr,
+                           nullptr};
     if (!c->graph_exec || std::memcmp(key, c->graph_key, sizeof key) != 0) {
       if (c->graph_exec) {
         IE_CHECK_HIP(hipGraphExecDestroy(c->graph_exec));
@@ -352,7 +379,7 @@ int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
       // default stream), replayed on the context's stream
       hipGraph_t g = nullptr;
       IE_CHECK_HIP(hipStreamBeginCapture(c->capture, hipStreamCaptureModeThreadLocal));
-      const int rc = enqueue_decode(c, c->capture, *weights, tokenid_buff, data_buffer,
+      const int rc = enqueue_decode(c, c->capture, *weights, seq_len, tokenid_buff, data_buffer,
                                     attn_buffer, output_distr, output_token, workspace, kv_cache);
       const hipError_t ec = hipStreamEndCapture(c->capture, &g);
       if (rc != IE_OK) {
@@ -367,8 +394,8 @@ int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
     }
     IE_CHECK_HIP(hipGraphLaunch(c->graph_exec, st));
   } else {
-    IE_TRY(enqueue_decode(c, st, *weights, tokenid_buff, data_buffer, attn_buffer, output_distr,
-                          output_token, workspace, kv_cache));
+    IE_TRY(enqueue_decode(c, st, *weights, seq_len, tokenid_buff, data_buffer, attn_buffer,
+                          output_distr, output_token, workspace, kv_cache));
   }
   IE_CHECK_HIP(hipMemcpyAsync(c->h_token, output_token, sizeof(int), hipMemcpyDeviceToHost, st));
   IE_CHECK_HIP(hipStreamSynchronize(st));
@@ -500,8 +527,7 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     IE_TRY(launch_gemm(kGemmBf16, g, st));
     IE_TRY(launch_qkv_rope_scatter(batch, 0, w.qkv, W.rope.cos, W.rope.sin, w.q, kvl,
                                    kvl + (size_t)kKVHeads * kKVPlane, d_sl, cstride, st));
-    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, c->d_counters + kCntAttn, d_sl, 0, batch,
-                       cstride, st));
+    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, batch, cstride, true, st));
     GemmParams o{};
     o.x = attn_buffer;
     o.w0 = L.transformer.w_o;
@@ -865,7 +891,7 @@ int ie_decode_attn(ie_context* c, const float* d_rope_cos, const float* d_rope_s
   L.transformer.w_v = const_cast<ie_bf16*>(d_vproj);
   ie_rope_weights rope{const_cast<float*>(d_rope_cos), const_cast<float*>(d_rope_sin)};
   IE_TRY(qkv_rope_gemv(L, rope, d_input, nullptr, w.q, kvl, nullptr, seq_len - 1, st));
-  IE_TRY(attn_decode(w.q, kvl, w.attn1, w, c->d_counters + kCntAttn, nullptr, seq_len, 1, 0, st));
+  IE_TRY(attn_decode(w.q, kvl, w.attn1, w, nullptr, seq_len, 1, 0, true, st));
   return gemv_plain(kHidden, kEpiBf16, w.attn1, nullptr, d_oproj, nullptr, kHidden / 2, d_output,
                     nullptr, 1, kHidden, st);
 }

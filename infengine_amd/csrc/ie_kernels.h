@@ -27,11 +27,16 @@ struct GemvParams {
   const float* rope_cos;   // [8192][64]
   const float* rope_sin;
   const int* d_seq_len;    // QKV: position = *d_seq_len - 1 when set
-  int pos;                 // QKV: position when d_seq_len == nullptr
+  int pos;                 // QKV: position when d_seq_len == nullptr (attention input: length)
   int n_pairs;             // row pairs per input row
   int ppw;                 // pairs per wave
   long long x_stride;      // elements between input rows
   long long out_stride;    // elements between output rows (kEpiBf16 / kEpiF32)
+  // K = 4096 residual GEMV only: the input row is the decode attention output, built in the
+  // prologue from the split partials (part_o / part_ml of batch row 0, splits of d_seq_len)
+  const float* attn_part_o;
+  const float* attn_part_ml;
+  int attn_max_splits;
 };
 
 // K must be 4096 or 14336.  rows > 1 re-reads the weights once per row.
@@ -50,8 +55,20 @@ struct AttnDecodeParams {
   float* part_ml;           // [batch][8][splits][4][2]
   const int* d_seq_len;     // [batch] device seq lens, or nullptr
   int seq_len;              // used when d_seq_len == nullptr (batch must be 1)
+  int max_splits;           // splits per kv head cap: kAttnFusedSplits or kAttnSplits
 };
-int launch_attn_decode(const AttnDecodeParams& p, int batch, hipStream_t st);
+// Splits per (sequence, kv head) for a context of ntiles 64-row tiles: one tile per wave
+// (two tile groups per split) up to the cap.  Device and host must agree on it.
+__host__ __device__ inline int attn_decode_splits(int ntiles, int max_splits) {
+  const int n = (ntiles + 1) / 2;
+  return n < 1 ? 1 : (n < max_splits ? n : max_splits);
+}
+// The O projection merges the partials itself while the context needs at most this many
+// splits (<= 1024 rows at one tile per wave; longer contexts run several tiles per wave).
+constexpr int kAttnFusedSplits = 8;
+constexpr int kAttnFusedMaxCtx = 4096;  // beyond: merge kernel + up to kAttnSplits splits
+// merge = also launch the merge kernel (bf16 output in p.out)
+int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStream_t st);
 size_t attn_decode_partials_bytes(int batch);
 
 // ------------------------------------------------------------ elementwise

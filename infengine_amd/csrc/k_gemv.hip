@@ -116,7 +116,55 @@ __device__ __forceinline__ void load_step(const u32x4_t* a, const u32x4_t* b, in
   }
 }
 
-template <int K, int EPI, bool NORM, int WAVES>
+// The decode attention output for the O projection, merged from the split partials straight
+// into the staged input vector: 8 dims of one q head per item, same arithmetic as the merge
+// kernel (weights exp(m_s - max m), o = sum_s w_s o_s / sum_s w_s l_s).
+template <int WAVES>
+__device__ __forceinline__ void stage_attention(const GemvParams& p, u32x4_t* xs) {
+  const int S = p.d_seq_len ? *p.d_seq_len : p.pos;
+  const int ns = attn_decode_splits((S + kAttnTile - 1) / kAttnTile, p.attn_max_splits);
+  for (int i = threadIdx.x; i < kQHeads * kHeadDim / 8; i += WAVES * 64) {
+    const int h = i >> 4, c = i & 15;
+    const size_t slot0 = ((size_t)(h / kGQA) * kAttnSplits) * kGQA + (h % kGQA);
+    float2 ml[kAttnFusedSplits];
+    float4 oa[kAttnFusedSplits], ob[kAttnFusedSplits];
+#pragma unroll
+    for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
+      if (sp < ns) {
+        const size_t slot = slot0 + (size_t)sp * kGQA;
+        ml[sp] = *reinterpret_cast<const float2*>(p.attn_part_ml + slot * 2);
+        const float4* po = reinterpret_cast<const float4*>(p.attn_part_o + slot * kHeadDim + c * 8);
+        oa[sp] = po[0];
+        ob[sp] = po[1];
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < kAttnFusedSplits; ++sp)
+      if (sp < ns) M = fmaxf(M, ml[sp].x);
+    float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
+      if (sp < ns) {
+        const float w = ml[sp].y > 0.f ? __expf(ml[sp].x - M) : 0.f;
+        L = fmaf(ml[sp].y, w, L);
+        o[0] = fmaf(oa[sp].x, w, o[0]);
+        o[1] = fmaf(oa[sp].y, w, o[1]);
+        o[2] = fmaf(oa[sp].z, w, o[2]);
+        o[3] = fmaf(oa[sp].w, w, o[3]);
+        o[4] = fmaf(ob[sp].x, w, o[4]);
+        o[5] = fmaf(ob[sp].y, w, o[5]);
+        o[6] = fmaf(ob[sp].z, w, o[6]);
+        o[7] = fmaf(ob[sp].w, w, o[7]);
+      }
+    }
+    const float inv = 1.0f / L;
+    xs[i] = u32x4_t{pack_bf2(o[0] * inv, o[1] * inv), pack_bf2(o[2] * inv, o[3] * inv),
+                    pack_bf2(o[4] * inv, o[5] * inv), pack_bf2(o[6] * inv, o[7] * inv)};
+  }
+}
+
+template <int K, int EPI, bool NORM, int WAVES, bool ATTN = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   constexpr int NC = K / 512;                 // 16-byte chunks per lane per row
   constexpr int G = (K == 4096) ? 4 : 7;      // chunks per pipeline step
@@ -142,7 +190,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   }
 
   const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(p.x + (size_t)row * p.x_stride);
-  if constexpr (NORM) {
+  if constexpr (ATTN) {
+    static_assert(K == kQHeads * kHeadDim && !NORM, "attention input: the O projection only");
+    stage_attention<WAVES>(p, xs);
+  } else if constexpr (NORM) {
     float ss = 0.f;
     for (int i = tid; i < K / 8; i += WAVES * 64) {
       const u32x4_t v = x4[i];
@@ -203,6 +254,13 @@ template <int K, int EPI, bool NORM, int WAVES>
 int launch_w(const GemvParams& p, int rows, hipStream_t st) {
   const int waves = (p.n_pairs + p.ppw - 1) / p.ppw;
   dim3 grid((waves + WAVES - 1) / WAVES, rows);
+  if constexpr (K == kQHeads * kHeadDim && EPI == kEpiResid && !NORM) {
+    if (p.attn_part_o) {
+      hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, true>), grid, dim3(WAVES * 64), 0, st, p);
+      IE_CHECK_LAUNCH();
+      return IE_OK;
+    }
+  }
   hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES>), grid, dim3(WAVES * 64), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
@@ -268,6 +326,11 @@ int launch_gemv(int K, int epi, bool norm, GemvParams p, int rows, hipStream_t s
   IE_REQUIRE(p.n_pairs >= 1, "launch_gemv: no rows");
   IE_REQUIRE(rows == 1 || epi == kEpiBf16 || epi == kEpiF32,
              "launch_gemv: epilogue %d supports one row only", epi);
+  IE_REQUIRE(!p.attn_part_o || (K == kQHeads * kHeadDim && epi == kEpiResid && !norm && rows == 1 &&
+                                p.attn_part_ml && p.attn_max_splits >= 1 &&
+                                p.attn_max_splits <= kAttnFusedSplits &&
+                                (p.d_seq_len || (p.pos >= 1 && p.pos <= kMaxCtx))),
+             "launch_gemv: attention-partials input is for the O projection only");
   if (p.ppw <= 0) p.ppw = default_ppw(p.n_pairs);
   if (K == 4096) return launch_k<4096>(epi, norm, p, rows, st);
   if (K == 14336) return launch_k<14336>(epi, norm, p, rows, st);

@@ -342,13 +342,23 @@ def test_attn_prefill_op(hip, ctx, rope):
     assert not got_kv[:, :, S:].any()
 
 
-def test_decoder_layer_decode_config2(hip, ctx, rope):
-    """One full fused decoder layer, token at position 2047."""
-    cos, sin, dcos, dsin = rope
+@pytest.fixture(scope="module")
+def model31():
     from infengine_amd.engine import ModelWeights
-    say("decoder_layer_decode layer 0 pos 2047 (random-init weights)")
-    seed, layer, pos = 31, 0, 2047
-    W = ModelWeights.random_init(seed=seed, std=0.02)
+    W = ModelWeights.random_init(seed=31, std=0.02)
+    yield W
+    W.free()
+
+
+@pytest.mark.parametrize("pos", [100, 2047, 3000, 5000])
+def test_decoder_layer_decode_config2(hip, ctx, rope, model31, pos):
+    """One full fused decoder layer, token at position pos (2047).  Up to
+    4096 rows the O projection merges the attention partials itself (one tile per wave at
+    100, several at 2047 and 3000); 5001 rows take the merge kernel."""
+    cos, sin, dcos, dsin = rope
+    say(f"decoder_layer_decode layer 0 pos {pos} (random-init weights)")
+    seed, layer = 31, 0
+    W = model31
     kv = torch.zeros(hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
     prior = orc.synthetic((2, 8, pos, 128), seed, 700, 0.0, 1.0)
     kv.view(32, 2, 8, 8192, 128)[layer][:, :, :pos] = dev(prior)
@@ -370,7 +380,6 @@ def test_decoder_layer_decode_config2(hip, ctx, rope):
     got_kv = host(kv.view(32, 2, 8, 8192, 128)[layer])
     assert np.array_equal(got_kv[:, :, :pos], prior)
     assert_bf16_close(got_kv[:, :, pos], planes[:, :, pos], what="kv row", outlier_frac=1e-3)
-    W.free()
 
 
 # ---------------------------------------------------------------- sampling (config 3)
