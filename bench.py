@@ -11,6 +11,8 @@ Also reported, on the same run:
                 234,926,080 algorithmic bytes per launch), timed with HIP events
                 on the stream it runs on, rotating over the 32 layers' weights so
                 the 256 MB Infinity Cache cannot serve repeats.
+  batched       config 5's bs=16 leg: 16 independent sequences (staggered contexts
+                from prompt_len+1) per ie_decode_step_batched, tokens/s and GB/s.
   cpu_baseline  the CPU oracle (oracle/, OpenMP) decoding the same model on this
                 host: whole decode steps (32 layers + lm_head + argmax) for about
                 10 s after one untimed step.
@@ -102,6 +104,8 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--batch", type=int, default=16, help="batched-decode sequences (1: skip)")
+    ap.add_argument("--batch-steps", type=int, default=32)
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -165,6 +169,45 @@ def main() -> int:
     kv_bytes = KV_BYTES_PER_POS * sum(p + 1 for p in range(first_pos, last_pos + 1)) / args.steps
     step_gbps = (WEIGHT_BYTES_PER_TOKEN + kv_bytes) / (dt / args.steps) / 1e9
 
+    # ---- batched decode (config 5): 16 independent sequences per step, one KV cache each
+    batched = None
+    if args.batch > 1:
+        B = args.batch
+        log(f"batched decode B={B}")
+        kvs = torch.zeros(B * lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+        toks = torch.randint(0, VOCAB, (B, 8192), dtype=torch.int32, device="cuda")
+        bdata = torch.zeros(B, HIDDEN, dtype=torch.bfloat16, device="cuda")
+        battn = torch.zeros_like(bdata)
+        blogits = torch.zeros(B, VOCAB, dtype=torch.float32, device="cuda")
+        bout = torch.zeros(B, dtype=torch.int32, device="cuda")
+        bws = torch.zeros(lib.ie_batch_workspace_size(B), dtype=torch.uint8, device="cuda")
+        lens = [args.prompt + 1 + b for b in range(B)]     # staggered contexts
+        th = (C.c_int * B)()
+
+        def bstep() -> None:
+            seq = (C.c_int * B)(*lens)
+            check(lib.ie_decode_step_batched(ctx.handle, W.ref(), B, seq, ptr(toks), ptr(bdata),
+                                             ptr(battn), ptr(blogits), ptr(bout), th, ptr(bws),
+                                             ptr(kvs)))
+            for b in range(B):
+                lens[b] += 1
+
+        for _ in range(4):
+            bstep()
+        torch.cuda.synchronize()
+        kv_b = KV_BYTES_PER_POS * sum(lens)
+        t0 = time.perf_counter()
+        for _ in range(args.batch_steps):
+            bstep()
+        torch.cuda.synchronize()
+        bdt = (time.perf_counter() - t0) / args.batch_steps
+        kv_b = (kv_b + KV_BYTES_PER_POS * sum(lens)) / 2          # mean over the timed steps
+        batched = {"batch": B, "steps": args.batch_steps, "tokens_per_s": round(B / bdt, 1),
+                   "ms_per_step": round(bdt * 1e3, 4),
+                   "step_GBps": round((WEIGHT_BYTES_PER_TOKEN + kv_b) / bdt / 1e9, 1),
+                   "contexts": [args.prompt + 5, lens[-1]]}
+        del kvs, toks, bdata, battn, blogits, bout, bws
+
     # ---- dominant kernel, timed live on its own stream with HIP events
     log("gate/up GEMV kernel timing")
     h = torch.empty(FFN, dtype=torch.bfloat16, device="cuda")
@@ -208,6 +251,7 @@ def main() -> int:
         "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "prefill": {"seq_len": args.prompt, "ms": round(prefill_s * 1e3, 2),
                     "tokens_per_s": round(args.prompt / prefill_s, 1)},
+        "batched": batched,
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4096, SwiGLU, RMSNorm> (gate/up)",
                      "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC,

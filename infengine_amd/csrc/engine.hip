@@ -12,6 +12,7 @@
 // then final-norm + lm_head GEMV (fp32 logits) and argmax.  The per-step scalar
 // (seq_len) lives in device memory, so the whole step is captured once into a
 // hipGraph and replayed.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -99,11 +100,12 @@ int qkv_rope_gemv(const ie_layer& L, const ie_rope_weights& rope, const uint16_t
   return launch_gemv(kHidden, kEpiQkvRope, norm_w != nullptr, p, 1, st);
 }
 
-// merge: also write the bf16 attention output to `out` (merge kernel, up to kAttnSplits
-// splits); otherwise only the partials are written, for an O projection that merges them.
+// merge: also write the bf16 attention output to `out` (merge kernel); otherwise only the
+// partials are written, for an O projection that merges them.  max_len: host-known bound on
+// the context lengths; beyond kAttnFusedMaxCtx the splits go up to kAttnSplits (merge only).
 int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs& w,
-                const int* d_seq_len, int seq_len, int batch, long long cache_stride, bool merge,
-                hipStream_t st) {
+                const int* d_seq_len, int seq_len, int max_len, int batch, long long cache_stride,
+                bool merge, hipStream_t st) {
   AttnDecodeParams a{};
   a.q = q;
   a.k_cache = kvl;
@@ -114,7 +116,9 @@ int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs&
   a.part_ml = w.part_ml;
   a.d_seq_len = d_seq_len;
   a.seq_len = seq_len;
-  a.max_splits = merge ? kAttnSplits : kAttnFusedSplits;
+  a.max_splits = max_len <= kAttnFusedMaxCtx ? kAttnFusedSplits : kAttnSplits;
+  IE_REQUIRE(merge || a.max_splits == kAttnFusedSplits,
+             "attn_decode: contexts past %d need the merge kernel", kAttnFusedMaxCtx);
   return launch_attn_decode(a, batch, merge, st);
 }
 
@@ -148,7 +152,7 @@ int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, 
   uint16_t* kvl = kv_layer(kv, layer);
   IE_TRY(qkv_rope_gemv(L, W.rope, x, L.input_layernorm, w.q, kvl, d_seq_len, seq_len - 1, st));
   const bool fused = attn_fused(seq_len);
-  IE_TRY(attn_decode(w.q, kvl, attn_out, w, d_seq_len, seq_len, 1, 0, !fused, st));
+  IE_TRY(attn_decode(w.q, kvl, attn_out, w, d_seq_len, seq_len, seq_len, 1, 0, !fused, st));
   if (fused) {
     // O projection + residual, its input merged from the split partials in its prologue
     GemvParams p{};
@@ -501,7 +505,11 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
                "decode_step_batched: seq_lens[%d]=%d out of [1, %d]", b, seq_lens[b], kMaxCtx);
   const ie_model_weights& W = *weights;
   hipStream_t st = c->stream;
-  for (int b = 0; b < batch; ++b) c->h_params[1 + b] = seq_lens[b];
+  int max_len = 1;
+  for (int b = 0; b < batch; ++b) {
+    c->h_params[1 + b] = seq_lens[b];
+    max_len = std::max(max_len, seq_lens[b]);
+  }
   IE_CHECK_HIP(hipMemcpyAsync(c->d_params + 1, c->h_params + 1, batch * sizeof(int),
                               hipMemcpyHostToDevice, st));
   const int* d_sl = c->d_params + 1;
@@ -527,7 +535,7 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     IE_TRY(launch_gemm(kGemmBf16, g, st));
     IE_TRY(launch_qkv_rope_scatter(batch, 0, w.qkv, W.rope.cos, W.rope.sin, w.q, kvl,
                                    kvl + (size_t)kKVHeads * kKVPlane, d_sl, cstride, st));
-    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, batch, cstride, true, st));
+    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, max_len, batch, cstride, true, st));
     GemmParams o{};
     o.x = attn_buffer;
     o.w0 = L.transformer.w_o;
@@ -891,7 +899,7 @@ int ie_decode_attn(ie_context* c, const float* d_rope_cos, const float* d_rope_s
   L.transformer.w_v = const_cast<ie_bf16*>(d_vproj);
   ie_rope_weights rope{const_cast<float*>(d_rope_cos), const_cast<float*>(d_rope_sin)};
   IE_TRY(qkv_rope_gemv(L, rope, d_input, nullptr, w.q, kvl, nullptr, seq_len - 1, st));
-  IE_TRY(attn_decode(w.q, kvl, w.attn1, w, nullptr, seq_len, 1, 0, true, st));
+  IE_TRY(attn_decode(w.q, kvl, w.attn1, w, nullptr, seq_len, seq_len, 1, 0, true, st));
   return gemv_plain(kHidden, kEpiBf16, w.attn1, nullptr, d_oproj, nullptr, kHidden / 2, d_output,
                     nullptr, 1, kHidden, st);
 }

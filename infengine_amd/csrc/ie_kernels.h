@@ -117,6 +117,9 @@ struct GemmParams {
   int ldy;
 };
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st);
+// M <= 16 streaming variant (batched decode); launch_gemm routes to it when it fits.
+bool gemm_skinny_fits(const GemmParams& p);
+int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st);
 
 // ------------------------------------------------------------ prefill attention
 struct AttnPrefillParams {

@@ -565,6 +565,7 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
                                     (p.n0 + p.n1 >= p.N || (p.n0 + p.n1) % 16 == 0)),
              "gemm: weight split points n0=%d n0+n1=%d inside N=%d must be multiples of 16", p.n0,
              p.n0 + p.n1, p.N);
+  if (gemm_skinny_fits(p)) return launch_gemm_skinny(epi, p, st);
   // Tile shape by a cost model: time = rounds of workgroups over the 256 CUs x the time of one
   // tile at the measured per-CU rate of that shape (256x256: 1085, 256x128: 900,
   // 128x128: 750 TFLOP/s over the chip at full occupancy).  Big tiles win when they fill the

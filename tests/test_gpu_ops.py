@@ -191,11 +191,12 @@ GEMM_EPI = {"bf16": 0, "resid": 1, "f32": 2, "swiglu": 3}
 
 
 @pytest.mark.parametrize("epi", list(GEMM_EPI))
-@pytest.mark.parametrize("m,n", [(300, 1000), (2048, 6144), (2048, 4096)])
+@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (300, 1000), (2048, 6144), (2048, 4096)])
 def test_gemm_epilogues(hip, ctx, epi, m, n):
-    """Every fused epilogue of the MFMA GEMM on each tile shape the launcher picks: a ragged
-    size (128 x 128 tiles), and the prefill sizes that select 256 x 256 tiles (bf16 / resid at
-    n = 6144, SwiGLU at n = 4096) and 256 x 128 tiles (the others); sampled rows at m = 2048."""
+    """Every fused epilogue of the MFMA GEMM on each kernel the launcher picks: the skinny
+    streaming kernel (m <= 16, ragged n), 128 x 128 tiles (m = 300), and the prefill sizes
+    that select 256 x 256 tiles (bf16 / resid at n = 6144, SwiGLU at n = 4096) and 256 x 128
+    tiles (the others); sampled rows at m = 2048."""
     k = 4096
     say(f"gemm_ex {epi} m={m} k={k} n={n}")
     x = orc.synthetic((m, k), 21, m, 0.0, 1.0)
