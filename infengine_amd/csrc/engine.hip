@@ -622,6 +622,60 @@ int ie_fill_synthetic_bf16(ie_bf16* out, size_t n, uint64_t seed, uint64_t tenso
 namespace ie {
 // Tensor ids of the synthetic model (shared with the CPU oracle).
 uint64_t tensor_id_of(int layer, int field) { return 16 + (uint64_t)layer * 16 + field; }
+
+// Layer field f in the order of the synthetic tensor ids: input_layernorm, w_q, w_k, w_v, w_o,
+// post_attention_layernorm, w_gate, w_up, w_down.
+ie_bf16** layer_field(ie_layer& L, int f) {
+  ie_bf16** slots[kLayerFields] = {&L.input_layernorm, &L.transformer.w_q, &L.transformer.w_k,
+                                   &L.transformer.w_v, &L.transformer.w_o,
+                                   &L.post_attention_layernorm, &L.ffn_block.w_gate,
+                                   &L.ffn_block.w_up, &L.ffn_block.w_down};
+  return slots[f];
+}
+
+size_t layer_field_elems(int f) {
+  const size_t mat = (size_t)kHidden * kHidden, kvm = (size_t)kKVDim * kHidden,
+               ffm = (size_t)kFFN * kHidden;
+  const size_t e[kLayerFields] = {(size_t)kHidden, mat, kvm, kvm, mat, (size_t)kHidden, ffm, ffm, ffm};
+  return e[f];
+}
+
+// One arena per model: emb | 32 x 9 layer fields | final_norm | lm_head | rope cos | rope sin,
+// every tensor 256-byte aligned.
+size_t weights_arena_bytes() {
+  const size_t emb = (size_t)kVocab * kHidden;
+  size_t total = align256(emb * 2);
+  for (int l = 0; l < kLayers; ++l)
+    for (int f = 0; f < kLayerFields; ++f) total += align256(layer_field_elems(f) * 2);
+  return total + align256(kHidden * 2) + align256(emb * 2) + 2 * align256((size_t)kMaxCtx * 64 * 4);
+}
+
+void weights_arena_assign(ie_model_weights* w, void* arena) {
+  char* p = static_cast<char*>(arena);
+  auto take = [&](size_t bytes) {
+    void* r = p;
+    p += align256(bytes);
+    return r;
+  };
+  const size_t emb = (size_t)kVocab * kHidden;
+  w->storage = arena;
+  w->emb_lookup = static_cast<ie_bf16*>(take(emb * 2));
+  for (int l = 0; l < kLayers; ++l)
+    for (int f = 0; f < kLayerFields; ++f)
+      *layer_field(w->layers[l], f) = static_cast<ie_bf16*>(take(layer_field_elems(f) * 2));
+  w->final_norm = static_cast<ie_bf16*>(take(kHidden * 2));
+  w->lm_head = static_cast<ie_bf16*>(take(emb * 2));
+  w->rope.cos = static_cast<float*>(take((size_t)kMaxCtx * 64 * 4));
+  w->rope.sin = static_cast<float*>(take((size_t)kMaxCtx * 64 * 4));
+}
+
+int weights_upload_rope(ie_model_weights* w) {
+  std::vector<float> ct, stb;
+  rope_tables_host(ct, stb);
+  IE_CHECK_HIP(hipMemcpy(w->rope.cos, ct.data(), ct.size() * 4, hipMemcpyHostToDevice));
+  IE_CHECK_HIP(hipMemcpy(w->rope.sin, stb.data(), stb.size() * 4, hipMemcpyHostToDevice));
+  return IE_OK;
+}
 }  // namespace ie
 
 extern "C" {
@@ -629,58 +683,25 @@ extern "C" {
 int ie_model_weights_random_init(ie_model_weights* out, uint64_t seed, float std) {
   IE_REQUIRE(out != nullptr, "random_init: null output");
   std::memset(out, 0, sizeof *out);
-  // arena layout: emb | layers | final_norm | lm_head | rope cos | rope sin
-  const size_t mat = (size_t)kHidden * kHidden, kvm = (size_t)kKVDim * kHidden,
-               ffm = (size_t)kFFN * kHidden, emb = (size_t)kVocab * kHidden;
-  const size_t layer_elems[9] = {(size_t)kHidden, mat, kvm, kvm, mat, (size_t)kHidden, ffm, ffm,
-                                 ffm};
-  size_t total = align256(emb * 2);
-  for (int l = 0; l < kLayers; ++l)
-    for (int f = 0; f < 9; ++f) total += align256(layer_elems[f] * 2);
-  total += align256(kHidden * 2) + align256(emb * 2) + 2 * align256((size_t)kMaxCtx * 64 * 4);
   void* arena = nullptr;
-  IE_CHECK_HIP(hipMalloc(&arena, total));
-  char* p = static_cast<char*>(arena);
-  auto take = [&](size_t elems, size_t esize) {
-    void* r = p;
-    p += align256(elems * esize);
-    return r;
-  };
-  out->storage = arena;
-  out->emb_lookup = static_cast<ie_bf16*>(take(emb, 2));
+  IE_CHECK_HIP(hipMalloc(&arena, ie::weights_arena_bytes()));
+  ie::weights_arena_assign(out, arena);
+  const size_t emb = (size_t)kVocab * kHidden;
   int rc = launch_fill_synthetic(out->emb_lookup, emb, seed, 1, 0.f, std, nullptr);
   for (int l = 0; l < kLayers && rc == IE_OK; ++l) {
-    ie_layer& L = out->layers[l];
-    ie_bf16** slots[9] = {&L.input_layernorm, &L.transformer.w_q, &L.transformer.w_k,
-                          &L.transformer.w_v, &L.transformer.w_o, &L.post_attention_layernorm,
-                          &L.ffn_block.w_gate, &L.ffn_block.w_up, &L.ffn_block.w_down};
-    for (int f = 0; f < 9 && rc == IE_OK; ++f) {
-      *slots[f] = static_cast<ie_bf16*>(take(layer_elems[f], 2));
+    for (int f = 0; f < ie::kLayerFields && rc == IE_OK; ++f) {
       const bool norm = (f == 0 || f == 5);
-      rc = launch_fill_synthetic(*slots[f], layer_elems[f], seed, tensor_id_of(l, f),
-                                 norm ? 1.f : 0.f, norm ? 0.02f : std, nullptr);
+      rc = launch_fill_synthetic(*ie::layer_field(out->layers[l], f), ie::layer_field_elems(f),
+                                 seed, tensor_id_of(l, f), norm ? 1.f : 0.f, norm ? 0.02f : std,
+                                 nullptr);
     }
   }
-  if (rc == IE_OK) {
-    out->final_norm = static_cast<ie_bf16*>(take(kHidden, 2));
-    rc = launch_fill_synthetic(out->final_norm, kHidden, seed, 2, 1.f, 0.02f, nullptr);
-  }
-  if (rc == IE_OK) {
-    out->lm_head = static_cast<ie_bf16*>(take(emb, 2));
-    rc = launch_fill_synthetic(out->lm_head, emb, seed, 3, 0.f, std, nullptr);
-  }
-  if (rc == IE_OK) {
-    std::vector<float> ct, stb;
-    rope_tables_host(ct, stb);
-    out->rope.cos = static_cast<float*>(take(ct.size(), 4));
-    out->rope.sin = static_cast<float*>(take(stb.size(), 4));
-    if (hipMemcpy(out->rope.cos, ct.data(), ct.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(out->rope.sin, stb.data(), stb.size() * 4, hipMemcpyHostToDevice) !=
-            hipSuccess ||
-        hipDeviceSynchronize() != hipSuccess) {
-      set_error("random_init: upload failed");
-      rc = IE_ERR_HIP;
-    }
+  if (rc == IE_OK) rc = launch_fill_synthetic(out->final_norm, kHidden, seed, 2, 1.f, 0.02f, nullptr);
+  if (rc == IE_OK) rc = launch_fill_synthetic(out->lm_head, emb, seed, 3, 0.f, std, nullptr);
+  if (rc == IE_OK) rc = ie::weights_upload_rope(out);
+  if (rc == IE_OK && hipDeviceSynchronize() != hipSuccess) {
+    set_error("random_init: fill failed");
+    rc = IE_ERR_HIP;
   }
   if (rc != IE_OK) {
     (void)hipFree(arena);
@@ -984,11 +1005,7 @@ int ie_final_norm_lm_head(ie_context* c, int rows, const ie_bf16* d_x, const ie_
 
 int ie_model_weights_from_safetensors(ie_model_weights* out, const char* const* paths,
                                       int n_paths) {
-  (void)paths;
-  (void)n_paths;
-  IE_REQUIRE(out != nullptr, "from_safetensors: null output");
-  set_error("from_safetensors: not built yet");
-  return IE_ERR_UNSUPPORTED;
+  return ie::load_safetensors(out, paths, n_paths);
 }
 
 }  // extern "C"

@@ -117,6 +117,16 @@ struct GemmParams {
   int ldy;
 };
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st);
+
+// ------------------------------------------------------------ weight arena (engine.hip)
+constexpr int kLayerFields = 9;
+ie_bf16** layer_field(ie_layer& L, int f);
+size_t layer_field_elems(int f);
+size_t weights_arena_bytes();
+void weights_arena_assign(ie_model_weights* w, void* arena);
+int weights_upload_rope(ie_model_weights* w);
+// model_weights.cu:80-154 (weights_io.cpp)
+int load_safetensors(ie_model_weights* out, const char* const* paths, int n_paths);
 // M <= 16 streaming variant (batched decode); launch_gemm routes to it when it fits.
 bool gemm_skinny_fits(const GemmParams& p);
 int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st);

@@ -78,6 +78,16 @@ class ModelWeights:
         check(lib.ie_model_weights_random_init(C.byref(w.s), seed, std))
         return w
 
+    @classmethod
+    def from_safetensors(cls, paths) -> "ModelWeights":
+        """ModelWeights::from_safetensors (model_weights.cu:145-154): HF Llama-3.1-8B BF16
+        checkpoint shards, kept BF16, in one library-owned arena."""
+        w = cls()
+        enc = [str(p).encode() for p in paths]
+        arr = (C.c_char_p * len(enc))(*enc)
+        check(lib.ie_model_weights_from_safetensors(C.byref(w.s), arr, len(enc)))
+        return w
+
     def ref(self):
         return C.byref(self.s)
 
