@@ -293,28 +293,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t x_group(const GemmParams& p, i
 // lambdas: a lambda around the amdgcn builtin inside a kernel template stops the host pass
 // from emitting the kernel's launch stub.)
 template <class C>
-__device__ __forceinline__ void issue_stage(u32x4_t* lds, const __amdgpu_buffer_rsrc_t* rsrc,
-                                            const uint32_t* voff, int wv, int kt, int stage) {
-  const uint32_t soff = (uint32_t)(kt * C::BK * 2);
-#pragma unroll
-  for (int j = 0; j < C::LOADS; ++j) {
-    const bool is_w = j < C::W_LOADS;
-    const int g = wv + C::NW * (is_w ? j : j - C::W_LOADS);
-    u32x4_t* dst = &lds[stage * C::STAGE + (is_w ? 0 : C::W_CHUNKS) + g * 64];
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[j], (lds_void*)dst, 16, voff[j], soff, 0, 0);
-  }
+__device__ __forceinline__ void issue_load(u32x4_t* lds, const __amdgpu_buffer_rsrc_t* rsrc,
+                                           const uint32_t* voff, int wv, int kt, int stage, int j) {
+  const bool is_w = j < C::W_LOADS;
+  const int g = wv + C::NW * (is_w ? j : j - C::W_LOADS);
+  u32x4_t* dst = &lds[stage * C::STAGE + (is_w ? 0 : C::W_CHUNKS) + g * 64];
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[j], (lds_void*)dst, 16, voff[j],
+                                           (uint32_t)(kt * C::BK * 2), 0, 0);
 }
 
-// MFMA operand fragments of k16 sub-step kk: lane l supplies tile row base + l%32,
-// k chunk 2*kk + l/32 (4 W fragments, 2 X fragments).
 template <class C>
-__device__ __forceinline__ void read_frags(const u32x4_t* st, int a_row, int b_row, int kk, int fh,
-                                           int fs, bf16x8_t* af, bf16x8_t* bfr) {
-  const int ch = (2 * kk + fh) ^ fs;
+__device__ __forceinline__ void issue_stage(u32x4_t* lds, const __amdgpu_buffer_rsrc_t* rsrc,
+                                            const uint32_t* voff, int wv, int kt, int stage) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) af[i] = __builtin_bit_cast(bf16x8_t, st[a_row + i * 32 * C::CPR + ch]);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) bfr[j] = __builtin_bit_cast(bf16x8_t, st[b_row + j * 32 * C::CPR + ch]);
+  for (int j = 0; j < C::LOADS; ++j) issue_load<C>(lds, rsrc, voff, wv, kt, stage, j);
+}
+
+// Operand fragment n (0..5) of a k16 sub-step, in the order the sub-step's MFMAs first use
+// them: X0 W0 X1 W1 W2 W3.  Lane l supplies tile row base + l%32 at k chunk ch (2*kk + l/32,
+// swizzled).
+template <class C>
+__device__ __forceinline__ void read_frag(const u32x4_t* src, int a_row, int b_row, int ch, int n,
+                                          bf16x8_t* af, bf16x8_t* bfr) {
+  if (n == 0 || n == 2) {
+    bfr[n / 2] = __builtin_bit_cast(bf16x8_t, src[b_row + (n / 2) * 32 * C::CPR + ch]);
+  } else {
+    const int i = n == 1 ? 0 : n - 2;
+    af[i] = __builtin_bit_cast(bf16x8_t, src[a_row + i * 32 * C::CPR + ch]);
+  }
 }
 
 // 8 bf16 at dst (8-byte aligned; 16-byte aligned when a16)
@@ -327,14 +333,16 @@ __device__ __forceinline__ void store16(uint16_t* dst, uint2 lo, uint2 hi, bool 
   }
 }
 
-// Wait until at most n stages of loads (n * loads per stage) are in flight, then barrier.
+// Wait until at most n stages of loads (n * loads per stage) are in flight and this wave's
+// LDS reads have returned, then barrier: after it the stage is visible to every wave and no
+// wave still reads the ring slot the next loads overwrite.
 template <int LOADS, int N>
 __device__ __forceinline__ void wait_stage_n(int n) {
   if constexpr (N < 0) {
     return;
   } else {
     if (n == N) {
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N * LOADS) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N * LOADS) : "memory");
       return;
     }
     wait_stage_n<LOADS, N - 1>(n);
@@ -357,6 +365,47 @@ __device__ __forceinline__ void tile_of(int b, int nb, int m_tiles, int& mtile, 
     const int t = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
     mtile = t % m_tiles;
     ntile = t / m_tiles;
+  }
+}
+
+// One k-step on ring slot kt % STAGES, as 4 (BK 64) or 2 (BK 32) MFMA sub-steps of k16.  The
+// fragments of the next sub-step are read one after each MFMA of the current one, so that their
+// issue hides under the MFMAs (the scheduling fences keep this order: left alone the scheduler
+// groups the reads and moves each just before its use).  The last sub-step waits for stage
+// kt+1 and reads its first fragments, so no k-step starts on an LDS latency; with ISSUE it also
+// refills slot kt % STAGES with stage kt+STAGES, one or two loads after each MFMA.
+template <class C, bool ISSUE>
+__device__ __forceinline__ void k_step(f32x16_t (&acc)[4][2], bf16x8_t (&af)[2][4],
+                                       bf16x8_t (&bfr)[2][2], u32x4_t* lds,
+                                       const __amdgpu_buffer_rsrc_t* rsrc, const uint32_t* voff,
+                                       int wv, int a_row, int b_row, int fh, int fs, int kt,
+                                       int KT) {
+  const u32x4_t* st = &lds[(kt % C::STAGES) * C::STAGE];
+  const u32x4_t* nst = &lds[((kt + 1) % C::STAGES) * C::STAGE];
+#pragma unroll
+  for (int kk = 0; kk < C::KSUB; ++kk) {
+    const int cur = kk & 1;
+    const bool last = kk + 1 == C::KSUB;
+    const bool rd = !last || ISSUE || kt + 1 < KT;
+    // stage kt+1 must have landed; the younger stages issued so far may stay in flight
+    if (last && rd)
+      wait_stage_n<C::LOADS, C::STAGES - 2>(ISSUE ? C::STAGES - 2 : min(C::STAGES - 2, KT - 2 - kt));
+    const u32x4_t* src = last ? nst : st;
+    const int ch = (2 * (last ? 0 : kk + 1) + fh) ^ fs;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      acc[t / 2][t % 2] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][t / 2], bfr[cur][t % 2], acc[t / 2][t % 2], 0, 0, 0);
+      if (rd && t < 6) read_frag<C>(src, a_row, b_row, ch, t, af[cur ^ 1], bfr[cur ^ 1]);
+      if (ISSUE && last) {
+#pragma unroll
+        for (int j = 0; j < C::LOADS; ++j)
+          if (j * 8 / C::LOADS == t)
+            issue_load<C>(lds, rsrc, voff, wv, kt + C::STAGES, kt % C::STAGES, j);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
@@ -408,29 +457,17 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
 #pragma unroll
   for (int s0 = 0; s0 < STAGES - 1; ++s0)
     if (s0 < KT) issue_stage<C>(lds, rsrc, voff, wv, s0, s0);
-  for (int kt = 0; kt < KT; ++kt) {
-    // stage kt must have landed; the younger stages issued so far may stay in flight
-    wait_stage_n<C::LOADS, STAGES - 2>(min(STAGES - 2, KT - 1 - kt));
-    if (kt + STAGES - 1 < KT)
-      issue_stage<C>(lds, rsrc, voff, wv, kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-    const u32x4_t* st = &lds[(kt % STAGES) * C::STAGE];
-    bf16x8_t af[2][4], bfr[2][2];
-    // fragments of sub-step kk+1 are read while the 8 MFMAs of kk run (the scheduling
-    // fences keep it so: left alone the scheduler reads each fragment just before its use)
-    read_frags<C>(st, a_row, b_row, 0, fh, fs, af[0], bfr[0]);
+  // stage 0 landed; stage STAGES-1 goes to the last ring slot, which no wave reads yet
+  wait_stage_n<C::LOADS, STAGES - 2>(min(STAGES - 2, KT - 1));
+  if (STAGES - 1 < KT) issue_stage<C>(lds, rsrc, voff, wv, STAGES - 1, STAGES - 1);
+  bf16x8_t af[2][4], bfr[2][2];
 #pragma unroll
-    for (int kk = 0; kk < C::KSUB; ++kk) {
-      const int cur = kk & 1;
-      if (kk + 1 < C::KSUB) read_frags<C>(st, a_row, b_row, kk + 1, fh, fs, af[cur ^ 1], bfr[cur ^ 1]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
+  for (int n = 0; n < 6; ++n) read_frag<C>(lds, a_row, b_row, fh ^ fs, n, af[0], bfr[0]);
+  int kt = 0;
+  for (; kt + STAGES < KT; ++kt)
+    k_step<C, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+  for (; kt < KT; ++kt)
+    k_step<C, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
 
   // ---- epilogue: accumulator element 4*g + q of tile (i, j) is
   //      W row wn*128 + 32*i + 8*g + 4*(lane/32) + q,  X row m0 + wm*64 + 32*j + lane%32
