@@ -13,6 +13,11 @@ Also reported, on the same run:
                 the 256 MB Infinity Cache cannot serve repeats.
   batched       config 5's bs=16 leg: 16 independent sequences (staggered contexts
                 from prompt_len+1) per ie_decode_step_batched, tokens/s and GB/s.
+  prefill_2048  config 4: a 2048-token prefill of the full model (mean of 3 after one
+                untimed call), and the four prefill GEMM shapes at M = 2048 (QKV, O with
+                residual, gate/up with SwiGLU, down with residual) timed with HIP events
+                on the engine stream, as TFLOP/s and fraction of the 2.5 PFLOP/s dense bf16
+                MFMA peak.
   cpu_baseline  the CPU oracle (oracle/, OpenMP) decoding the same model on this
                 host: whole decode steps (32 layers + lm_head + argmax) for about
                 10 s after one untimed step.
@@ -35,6 +40,8 @@ WEIGHT_BYTES_PER_TOKEN = 15_009_849_344          # every weight byte read once p
 KV_BYTES_PER_POS = 131_072                       # 32 layers x (K+V) x 8 heads x 128 x 2 B
 GATE_UP_BYTES = 2 * FFN * HIDDEN * 2 + 2 * HIDDEN * 2 + FFN * 2
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0                   # dense bf16 MFMA, MI355X
+LAYER_GEMM_PARAMS = (6144 + 4096 + 2 * FFN) * HIDDEN + HIDDEN * FFN   # QKV, O, gate+up, down
 # HBM bytes per gate/up launch from rocprofv3 FETCH_SIZE (x2.000) + WRITE_SIZE (x1.000), each
 # factor calibrated on a 256 MiB copy; profiles/decode_gemv_hbm_traffic.md.
 GATE_UP_TRAFFIC = 235_190_000
@@ -106,6 +113,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--batch", type=int, default=16, help="batched-decode sequences (1: skip)")
     ap.add_argument("--batch-steps", type=int, default=32)
+    ap.add_argument("--prefill-len", type=int, default=2048,
+                    help="config 4 prefill leg and its GEMM roofline (0: skip)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -208,6 +217,53 @@ def main() -> int:
                    "contexts": [args.prompt + 5, lens[-1]]}
         del kvs, toks, bdata, battn, blogits, bout, bws
 
+    # ---- config 4: 2048-token prefill, and its four GEMM shapes against the MFMA peak
+    prefill2048 = None
+    if args.prefill_len > 0:
+        P = args.prefill_len
+        log(f"prefill {P} tokens")
+        req2 = Request(ctx, W, max_seq_len=P + 8)
+        req2.tokens[:P] = torch.from_numpy(rng.integers(0, VOCAB, P).astype(np.int32)).cuda()
+        req2.prefill(P)                                   # untimed first call
+        torch.cuda.synchronize()
+        reps = 3
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            req2.prefill(P)
+        torch.cuda.synchronize()
+        pdt = (time.perf_counter() - t0) / reps
+        del req2
+        gemms = {}
+        stream = ctx.stream
+        for name, epi, k, n in (("qkv", 0, HIDDEN, 6144), ("o", 1, HIDDEN, HIDDEN),
+                                ("gate_up", 3, HIDDEN, FFN), ("down", 1, FFN, HIDDEN)):
+            gx = (torch.randn(P, k, device="cuda") * 0.5).to(torch.bfloat16)
+            gw0 = (torch.randn(n, k, device="cuda") * 0.02).to(torch.bfloat16)
+            gw1 = (torch.randn(n, k, device="cuda") * 0.02).to(torch.bfloat16) if epi == 3 else gw0
+            gy = torch.zeros(P, n, dtype=torch.bfloat16, device="cuda")
+            torch.cuda.synchronize()
+
+            def run() -> None:
+                check(lib.ie_gemm_ex(ctx.handle, epi, P, k, n, ptr(gx), ptr(gw0), ptr(gw1), ptr(gy)))
+
+            for _ in range(3):
+                run()
+            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            g0.record(stream)
+            for _ in range(10):
+                run()
+            g1.record(stream)
+            g1.synchronize()
+            us = g0.elapsed_time(g1) * 1e3 / 10
+            tf = 2.0 * P * n * k * (2 if epi == 3 else 1) / (us * 1e-6) / 1e12
+            gemms[name] = {"m": P, "n": n, "k": k, "us": round(us, 1), "tflops": round(tf, 1),
+                           "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+            del gx, gw0, gw1, gy
+        flops = 2.0 * P * LAYER_GEMM_PARAMS * LAYERS
+        prefill2048 = {"seq_len": P, "ms": round(pdt * 1e3, 2), "tokens_per_s": round(P / pdt, 1),
+                       "layer_gemm_tflops_per_s": round(flops / pdt / 1e12, 1),
+                       "gemm": gemms, "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS}
+
     # ---- dominant kernel, timed live on its own stream with HIP events
     log("gate/up GEMV kernel timing")
     h = torch.empty(FFN, dtype=torch.bfloat16, device="cuda")
@@ -252,6 +308,7 @@ def main() -> int:
         "prefill": {"seq_len": args.prompt, "ms": round(prefill_s * 1e3, 2),
                     "tokens_per_s": round(args.prompt / prefill_s, 1)},
         "batched": batched,
+        "prefill_2048": prefill2048,
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4096, SwiGLU, RMSNorm> (gate/up)",
                      "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC,

@@ -118,58 +118,98 @@ __device__ __forceinline__ void load_step(const u32x4_t* a, const u32x4_t* b, in
 
 // The decode attention output for the O projection, merged from the split partials straight
 // into the staged input vector: 8 dims of one q head per item, same arithmetic as the merge
-// kernel (weights exp(m_s - max m), o = sum_s w_s o_s / sum_s w_s l_s).
-template <int WAVES>
-__device__ __forceinline__ void stage_attention(const GemvParams& p, u32x4_t* xs) {
-  const int S = p.d_seq_len ? *p.d_seq_len : p.pos;
-  const int ns = attn_decode_splits((S + kAttnTile - 1) / kAttnTile, p.attn_max_splits);
-  for (int i = threadIdx.x; i < kQHeads * kHeadDim / 8; i += WAVES * 64) {
-    const int h = i >> 4, c = i & 15;
-    const size_t slot0 = ((size_t)(h / kGQA) * kAttnSplits) * kGQA + (h % kGQA);
-    float2 ml[kAttnFusedSplits];
-    float4 oa[kAttnFusedSplits], ob[kAttnFusedSplits];
+// kernel (weights exp(m_s - max m), o = sum_s w_s o_s / sum_s w_s l_s).  The loads of an item
+// are issued before the weight stream (attn_load) and merged after it is in flight (attn_merge).
+struct AttnItem {
+  float2 ml[kAttnFusedSplits];
+  float4 oa[kAttnFusedSplits], ob[kAttnFusedSplits];
+};
+
+// Slots sp >= ns re-read slot ns-1 (L1 hits; attn_merge reads only the first ns): the loads
+// stay unconditional, which keeps the compiler's wait counts exact, so the staging does not
+// wait for the weight stream, without fetching slots past ns from L2.
+__device__ __forceinline__ void attn_load(const GemvParams& p, int i, int ns, AttnItem& a) {
+  const int h = i >> 4, c = i & 15;
+  const size_t slot0 = ((size_t)(h / kGQA) * kAttnSplits) * kGQA + (h % kGQA);
 #pragma unroll
-    for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
-      if (sp < ns) {
-        const size_t slot = slot0 + (size_t)sp * kGQA;
-        ml[sp] = *reinterpret_cast<const float2*>(p.attn_part_ml + slot * 2);
-        const float4* po = reinterpret_cast<const float4*>(p.attn_part_o + slot * kHeadDim + c * 8);
-        oa[sp] = po[0];
-        ob[sp] = po[1];
-      }
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int sp = 0; sp < kAttnFusedSplits; ++sp)
-      if (sp < ns) M = fmaxf(M, ml[sp].x);
-    float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
-      if (sp < ns) {
-        const float w = ml[sp].y > 0.f ? __expf(ml[sp].x - M) : 0.f;
-        L = fmaf(ml[sp].y, w, L);
-        o[0] = fmaf(oa[sp].x, w, o[0]);
-        o[1] = fmaf(oa[sp].y, w, o[1]);
-        o[2] = fmaf(oa[sp].z, w, o[2]);
-        o[3] = fmaf(oa[sp].w, w, o[3]);
-        o[4] = fmaf(ob[sp].x, w, o[4]);
-        o[5] = fmaf(ob[sp].y, w, o[5]);
-        o[6] = fmaf(ob[sp].z, w, o[6]);
-        o[7] = fmaf(ob[sp].w, w, o[7]);
-      }
-    }
-    const float inv = 1.0f / L;
-    xs[i] = u32x4_t{pack_bf2(o[0] * inv, o[1] * inv), pack_bf2(o[2] * inv, o[3] * inv),
-                    pack_bf2(o[4] * inv, o[5] * inv), pack_bf2(o[6] * inv, o[7] * inv)};
+  for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
+    const size_t slot = slot0 + (size_t)min(sp, ns - 1) * kGQA;
+    a.ml[sp] = *reinterpret_cast<const float2*>(p.attn_part_ml + slot * 2);
+    const float4* po = reinterpret_cast<const float4*>(p.attn_part_o + slot * kHeadDim + c * 8);
+    a.oa[sp] = po[0];
+    a.ob[sp] = po[1];
   }
 }
 
-template <int K, int EPI, bool NORM, int WAVES, bool ATTN = false>
+__device__ __forceinline__ u32x4_t attn_merge(const AttnItem& a, int ns) {
+  float M = -INFINITY;
+#pragma unroll
+  for (int sp = 0; sp < kAttnFusedSplits; ++sp)
+    if (sp < ns) M = fmaxf(M, a.ml[sp].x);
+  float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
+    if (sp < ns) {
+      const float w = a.ml[sp].y > 0.f ? __expf(a.ml[sp].x - M) : 0.f;
+      L = fmaf(a.ml[sp].y, w, L);
+      o[0] = fmaf(a.oa[sp].x, w, o[0]);
+      o[1] = fmaf(a.oa[sp].y, w, o[1]);
+      o[2] = fmaf(a.oa[sp].z, w, o[2]);
+      o[3] = fmaf(a.oa[sp].w, w, o[3]);
+      o[4] = fmaf(a.ob[sp].x, w, o[4]);
+      o[5] = fmaf(a.ob[sp].y, w, o[5]);
+      o[6] = fmaf(a.ob[sp].z, w, o[6]);
+      o[7] = fmaf(a.ob[sp].w, w, o[7]);
+    }
+  }
+  const float inv = 1.0f / L;
+  return u32x4_t{pack_bf2(o[0] * inv, o[1] * inv), pack_bf2(o[2] * inv, o[3] * inv),
+                 pack_bf2(o[4] * inv, o[5] * inv), pack_bf2(o[6] * inv, o[7] * inv)};
+}
+
+// Loads of step t of this wave's (pair, chunk-group) sequence into (wa, wb).  The pair index
+// is clamped to the last pair, so a wave past the end loads valid rows it never stores.
+template <int K, int EPI, int G, int NG>
+__device__ __forceinline__ void issue_step(const GemvParams& p, int first, int lane, int t,
+                                           u32x4_t (&wa)[G], u32x4_t (&wb)[G]) {
+  const uint16_t *r0, *r1;
+  rows_of_pair<EPI, K>(p, min(first + t / NG, p.n_pairs - 1), r0, r1);
+  load_step<G>(reinterpret_cast<const u32x4_t*>(r0) + lane,
+               reinterpret_cast<const u32x4_t*>(r1) + lane, (t % NG) * G, wa, wb);
+}
+
+// Dot products of step t against the staged input; the row pair's epilogue after its last step.
+template <int EPI, int G, int NG>
+__device__ __forceinline__ void consume_step(const GemvParams& p, const u32x4_t* xs, int first,
+                                             int row, int lane, int t, const u32x4_t (&wa)[G],
+                                             const u32x4_t (&wb)[G], float& acc0, float& acc1) {
+  const int g = t % NG;
+#pragma unroll
+  for (int c = 0; c < G; ++c) {
+    const u32x4_t xv = xs[(g * G + c) * 64 + lane];
+    acc0 = dot8(wa[c], xv, acc0);
+    acc1 = dot8(wb[c], xv, acc1);
+  }
+  if (g == NG - 1) {
+    const float a0 = wave_sum(acc0), a1 = wave_sum(acc1);
+    if (lane == 0 && first + t / NG < p.n_pairs) gemv_epilogue<EPI>(p, first + t / NG, row, a0, a1);
+    acc0 = 0.f;
+    acc1 = 0.f;
+  }
+}
+
+// ONE: one pair per wave (the default), unrolled at compile time so every wait is exact; the
+// general loop for more pairs per wave is a separate instance because its conditional loads
+// more than double the register count.
+template <int K, int EPI, bool NORM, int WAVES, bool ATTN, bool ONE>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
+  constexpr int T = WAVES * 64;
   constexpr int NC = K / 512;                 // 16-byte chunks per lane per row
   constexpr int G = (K == 4096) ? 4 : 7;      // chunks per pipeline step
   constexpr int NG = NC / G;                  // steps per row pair
-  static_assert(NC % G == 0, "K must be a multiple of 512*G");
+  static_assert(NC % G == 0 && NG % 2 == 0, "K must be a multiple of 1024*G");
+  constexpr int XC = (K / 8 + T - 1) / T;     // input chunks staged per thread
+  constexpr int AI = (kQHeads * kHeadDim / 8 + T - 1) / T;  // attention items per thread
   __shared__ u32x4_t xs[K / 8];
   __shared__ float red[WAVES];
 
@@ -179,27 +219,45 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   const int npairs = max(0, min(p.ppw, p.n_pairs - first));
   const int nsteps = npairs * NG;
 
-  // The wave's first weight loads go out before the x staging / RMSNorm
-  // prologue, which then runs under their latency.
-  u32x4_t ca[G], cb[G], na[G], nb[G];
-  const uint16_t *r0 = nullptr, *r1 = nullptr;
-  if (nsteps > 0) {
-    rows_of_pair<EPI, K>(p, first, r0, r1);
-    load_step<G>(reinterpret_cast<const u32x4_t*>(r0) + lane,
-                 reinterpret_cast<const u32x4_t*>(r1) + lane, 0, ca, cb);
-  }
-
+  // Memory operations return in issue order, so the input (activations, norm weight, attention
+  // partials) is loaded first: it lands while the weight stream is still in flight, and the
+  // staging below waits for it alone.  These loads and the first two weight steps are
+  // unconditional (indices clamped): a load under a branch makes the compiler's wait at the
+  // join conservative, which would stall the staging until the weights arrive.
   const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(p.x + (size_t)row * p.x_stride);
+  u32x4_t xin[XC], nwin[XC];
+  AttnItem ai[ATTN ? AI : 1];
+  int ns = 0;
   if constexpr (ATTN) {
     static_assert(K == kQHeads * kHeadDim && !NORM, "attention input: the O projection only");
-    stage_attention<WAVES>(p, xs);
+    const int S = p.d_seq_len ? *p.d_seq_len : p.pos;
+    ns = attn_decode_splits((S + kAttnTile - 1) / kAttnTile, p.attn_max_splits);
+#pragma unroll
+    for (int j = 0; j < AI; ++j)
+      attn_load(p, min(tid + j * T, kQHeads * kHeadDim / 8 - 1), ns, ai[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+      const int i = min(tid + j * T, K / 8 - 1);
+      xin[j] = x4[i];
+      if constexpr (NORM) nwin[j] = reinterpret_cast<const u32x4_t*>(p.norm_w)[i];
+    }
+  }
+
+  // Weight stream: two steps in flight in two register buffers (B0: even steps, B1: odd).
+  u32x4_t a0[G], b0[G], a1[G], b1[G];
+  issue_step<K, EPI, G, NG>(p, first, lane, 0, a0, b0);
+  issue_step<K, EPI, G, NG>(p, first, lane, 1, a1, b1);
+
+  if constexpr (ATTN) {
+#pragma unroll
+    for (int j = 0; j < AI; ++j)
+      if (tid + j * T < kQHeads * kHeadDim / 8) xs[tid + j * T] = attn_merge(ai[j], ns);
   } else if constexpr (NORM) {
     float ss = 0.f;
-    for (int i = tid; i < K / 8; i += WAVES * 64) {
-      const u32x4_t v = x4[i];
-      xs[i] = v;
-      ss += sumsq8(v);
-    }
+#pragma unroll
+    for (int j = 0; j < XC; ++j)
+      if (tid + j * T < K / 8) ss += sumsq8(xin[j]);
     ss = wave_sum(ss);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
@@ -207,68 +265,66 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) tot += red[w];
     const float r = rsqrtf(tot / (float)K + kRmsEps);
-    const u32x4_t* w4 = reinterpret_cast<const u32x4_t*>(p.norm_w);
-    for (int i = tid; i < K / 8; i += WAVES * 64) xs[i] = norm8(xs[i], w4[i], r);
+#pragma unroll
+    for (int j = 0; j < XC; ++j)
+      if (tid + j * T < K / 8) xs[tid + j * T] = norm8(xin[j], nwin[j], r);
   } else {
-    for (int i = tid; i < K / 8; i += WAVES * 64) xs[i] = x4[i];
+#pragma unroll
+    for (int j = 0; j < XC; ++j)
+      if (tid + j * T < K / 8) xs[tid + j * T] = xin[j];
   }
   __syncthreads();
 
-  // Pipeline over (pair, step): the loads of step s+1 (possibly the next
-  // pair's rows) are issued before step s is reduced.
+  // Step t+2 is issued into the buffer step t has just been consumed from.
   float acc0 = 0.f, acc1 = 0.f;
-  for (int s = 0; s < nsteps; ++s) {
-    const int g = s % NG;
-    if (s + 1 < nsteps) {
-      const int s1 = s + 1, g1 = s1 % NG;
-      const uint16_t *q0 = r0, *q1 = r1;
-      if (g1 == 0) rows_of_pair<EPI, K>(p, first + s1 / NG, q0, q1);
-      load_step<G>(reinterpret_cast<const u32x4_t*>(q0) + lane,
-                   reinterpret_cast<const u32x4_t*>(q1) + lane, g1 * G, na, nb);
-      if (g1 == 0) {
-        r0 = q0;
-        r1 = q1;
-      }
-    }
+  if constexpr (ONE) {
 #pragma unroll
-    for (int c = 0; c < G; ++c) {
-      const u32x4_t xv = xs[(g * G + c) * 64 + lane];
-      acc0 = dot8(ca[c], xv, acc0);
-      acc1 = dot8(cb[c], xv, acc1);
+    for (int t = 0; t < NG; t += 2) {
+      consume_step<EPI, G, NG>(p, xs, first, row, lane, t, a0, b0, acc0, acc1);
+      if (t + 2 < NG) issue_step<K, EPI, G, NG>(p, first, lane, t + 2, a0, b0);
+      consume_step<EPI, G, NG>(p, xs, first, row, lane, t + 1, a1, b1, acc0, acc1);
+      if (t + 3 < NG) issue_step<K, EPI, G, NG>(p, first, lane, t + 3, a1, b1);
     }
-    if (g == NG - 1) {
-      const float a0 = wave_sum(acc0), a1 = wave_sum(acc1);
-      if (lane == 0) gemv_epilogue<EPI>(p, first + s / NG, row, a0, a1);
-      acc0 = 0.f;
-      acc1 = 0.f;
-    }
-#pragma unroll
-    for (int c = 0; c < G; ++c) {
-      ca[c] = na[c];
-      cb[c] = nb[c];
+  } else {
+    for (int t = 0; t < nsteps; t += 2) {
+      consume_step<EPI, G, NG>(p, xs, first, row, lane, t, a0, b0, acc0, acc1);
+      if (t + 2 < nsteps) issue_step<K, EPI, G, NG>(p, first, lane, t + 2, a0, b0);
+      consume_step<EPI, G, NG>(p, xs, first, row, lane, t + 1, a1, b1, acc0, acc1);
+      if (t + 3 < nsteps) issue_step<K, EPI, G, NG>(p, first, lane, t + 3, a1, b1);
     }
   }
 }
 
-template <int K, int EPI, bool NORM, int WAVES>
-int launch_w(const GemvParams& p, int rows, hipStream_t st) {
+template <int K, int EPI, bool NORM, int WAVES, bool ONE>
+int launch_o(const GemvParams& p, int rows, hipStream_t st) {
   const int waves = (p.n_pairs + p.ppw - 1) / p.ppw;
   dim3 grid((waves + WAVES - 1) / WAVES, rows);
   if constexpr (K == kQHeads * kHeadDim && EPI == kEpiResid && !NORM) {
     if (p.attn_part_o) {
-      hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, true>), grid, dim3(WAVES * 64), 0, st, p);
+      hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, true, ONE>), grid, dim3(WAVES * 64), 0,
+                         st, p);
       IE_CHECK_LAUNCH();
       return IE_OK;
     }
   }
-  hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES>), grid, dim3(WAVES * 64), 0, st, p);
+  hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, false, ONE>), grid, dim3(WAVES * 64), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
 
+template <int K, int EPI, bool NORM, int WAVES>
+int launch_w(const GemvParams& p, int rows, hipStream_t st) {
+  return p.ppw == 1 ? launch_o<K, EPI, NORM, WAVES, true>(p, rows, st)
+                    : launch_o<K, EPI, NORM, WAVES, false>(p, rows, st);
+}
+
 template <int K, int EPI, bool NORM>
 int launch_t(const GemvParams& p, int rows, hipStream_t st) {
-  switch (gemv_waves(K, EPI, p.n_pairs)) {
+  const int waves = gemv_waves(K, EPI, p.n_pairs);
+  if constexpr (EPI == kEpiQkvRope) {
+    if (waves == 12) return launch_w<K, EPI, NORM, 12>(p, rows, st);
+  }
+  switch (waves) {
     case 8: return launch_w<K, EPI, NORM, 8>(p, rows, st);
     case 16: return launch_w<K, EPI, NORM, 16>(p, rows, st);
     default: return launch_w<K, EPI, NORM, 4>(p, rows, st);
@@ -302,13 +358,14 @@ int g_waves_override = 0;
 
 // Waves per workgroup: each workgroup stages (and for RMSNorm ops normalises) the whole input
 // vector once, so more waves per workgroup means less of that per weight byte, at the price of
-// coarser occupancy.
+// coarser occupancy.  8 by default; the fused QKV GEMV (3072 row pairs) uses 12, which makes
+// its grid exactly one workgroup per CU (measured 1.0 us faster per launch than 384 workgroups
+// of 8 waves, whose 1.5 workgroups per CU finish unevenly).
 int gemv_waves(int K, int epi, int n_pairs) {
   if (g_waves_override > 0) return g_waves_override;
   (void)K;
-  (void)epi;
   (void)n_pairs;
-  return 8;
+  return epi == kEpiQkvRope ? 12 : 8;
 }
 
 int default_ppw(int n_pairs) {
