@@ -63,9 +63,35 @@ __device__ __forceinline__ void rows_of_pair(const GemvParams& p, int pair, cons
   }
 }
 
+// Operands an epilogue reads from memory (the residual, the RoPE position and angle), loaded in
+// the prologue with the inputs when the wave owns a single pair, so that the epilogue does not end
+// the wave on a load latency.  `have` = false: the epilogue loads them itself.
+struct EpiPre {
+  uint32_t old = 0;
+  float c = 0.f, s = 0.f;
+  int pos = 0;
+  bool have = false;
+};
+
+template <int EPI>
+__device__ __forceinline__ EpiPre epi_preload(const GemvParams& p, int pair) {
+  EpiPre e;
+  e.have = true;
+  if constexpr (EPI == kEpiResid) {
+    e.old = *reinterpret_cast<const uint32_t*>(p.out + 2 * pair);
+  } else if constexpr (EPI == kEpiQkvRope) {
+    // V heads take no rotation; their (valid) table entries are loaded and unused
+    const int j = pair & 63;
+    e.pos = p.d_seq_len ? (*p.d_seq_len - 1) : p.pos;
+    e.c = p.rope_cos[e.pos * (kHeadDim / 2) + j];
+    e.s = p.rope_sin[e.pos * (kHeadDim / 2) + j];
+  }
+  return e;
+}
+
 template <int EPI>
 __device__ __forceinline__ void gemv_epilogue(const GemvParams& p, int pair, int row, float a0,
-                                              float a1) {
+                                              float a1, const EpiPre& e) {
   if constexpr (EPI == kEpiBf16) {
     uint16_t* o = p.out + (size_t)row * p.out_stride + 2 * pair;
     *reinterpret_cast<uint32_t*>(o) = pack_bf2(a0, a1);
@@ -74,7 +100,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvParams& p, int pair, int
     *reinterpret_cast<float2*>(o) = make_float2(a0, a1);
   } else if constexpr (EPI == kEpiResid) {
     uint32_t* o = reinterpret_cast<uint32_t*>(p.out + 2 * pair);
-    const uint32_t old = *o;
+    const uint32_t old = e.have ? e.old : *o;
     const float y0 = bf2f(f2bf(a0)), y1 = bf2f(f2bf(a1));
     *o = pack_bf2(bf_lo(old) + y0, bf_hi(old) + y1);
   } else if constexpr (EPI == kEpiSwiglu) {
@@ -82,11 +108,11 @@ __device__ __forceinline__ void gemv_epilogue(const GemvParams& p, int pair, int
     p.out[pair] = f2bf(g * (1.0f / (1.0f + expf(-g))) * u);
   } else {  // kEpiQkvRope
     const int head = pair >> 6, j = pair & 63;
-    const int pos = p.d_seq_len ? (*p.d_seq_len - 1) : p.pos;
+    const int pos = e.have ? e.pos : (p.d_seq_len ? (*p.d_seq_len - 1) : p.pos);
     float y0 = bf2f(f2bf(a0)), y1 = bf2f(f2bf(a1));
     if (head < kQHeads + kKVHeads) {
-      const float c = p.rope_cos[pos * (kHeadDim / 2) + j];
-      const float s = p.rope_sin[pos * (kHeadDim / 2) + j];
+      const float c = e.have ? e.c : p.rope_cos[pos * (kHeadDim / 2) + j];
+      const float s = e.have ? e.s : p.rope_sin[pos * (kHeadDim / 2) + j];
       const float o0 = y0 * c - y1 * s;
       const float o1 = y0 * s + y1 * c;
       y0 = o0;
@@ -182,7 +208,8 @@ __device__ __forceinline__ void issue_step(const GemvParams& p, int first, int l
 template <int EPI, int G, int NG>
 __device__ __forceinline__ void consume_step(const GemvParams& p, const u32x4_t* xs, int first,
                                              int row, int lane, int t, const u32x4_t (&wa)[G],
-                                             const u32x4_t (&wb)[G], float& acc0, float& acc1) {
+                                             const u32x4_t (&wb)[G], float& acc0, float& acc1,
+                                             const EpiPre& e) {
   const int g = t % NG;
 #pragma unroll
   for (int c = 0; c < G; ++c) {
@@ -192,7 +219,8 @@ __device__ __forceinline__ void consume_step(const GemvParams& p, const u32x4_t*
   }
   if (g == NG - 1) {
     const float a0 = wave_sum(acc0), a1 = wave_sum(acc1);
-    if (lane == 0 && first + t / NG < p.n_pairs) gemv_epilogue<EPI>(p, first + t / NG, row, a0, a1);
+    if (lane == 0 && first + t / NG < p.n_pairs)
+      gemv_epilogue<EPI>(p, first + t / NG, row, a0, a1, e);
     acc0 = 0.f;
     acc1 = 0.f;
   }
@@ -244,6 +272,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
     }
   }
 
+  EpiPre epre;
+  if constexpr (ONE) epre = epi_preload<EPI>(p, min(first, p.n_pairs - 1));
+
   // Weight stream: two steps in flight in two register buffers (B0: even steps, B1: odd).
   u32x4_t a0[G], b0[G], a1[G], b1[G];
   issue_step<K, EPI, G, NG>(p, first, lane, 0, a0, b0);
@@ -280,16 +311,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   if constexpr (ONE) {
 #pragma unroll
     for (int t = 0; t < NG; t += 2) {
-      consume_step<EPI, G, NG>(p, xs, first, row, lane, t, a0, b0, acc0, acc1);
+      consume_step<EPI, G, NG>(p, xs, first, row, lane, t, a0, b0, acc0, acc1, epre);
       if (t + 2 < NG) issue_step<K, EPI, G, NG>(p, first, lane, t + 2, a0, b0);
-      consume_step<EPI, G, NG>(p, xs, first, row, lane, t + 1, a1, b1, acc0, acc1);
+      consume_step<EPI, G, NG>(p, xs, first, row, lane, t + 1, a1, b1, acc0, acc1, epre);
       if (t + 3 < NG) issue_step<K, EPI, G, NG>(p, first, lane, t + 3, a1, b1);
     }
   } else {
     for (int t = 0; t < nsteps; t += 2) {
-      consume_step<EPI, G, NG>(p, xs, first, row, lane, t, a0, b0, acc0, acc1);
+      consume_step<EPI, G, NG>(p, xs, first, row, lane, t, a0, b0, acc0, acc1, epre);
       if (t + 2 < nsteps) issue_step<K, EPI, G, NG>(p, first, lane, t + 2, a0, b0);
-      consume_step<EPI, G, NG>(p, xs, first, row, lane, t + 1, a1, b1, acc0, acc1);
+      consume_step<EPI, G, NG>(p, xs, first, row, lane, t + 1, a1, b1, acc0, acc1, epre);
       if (t + 3 < nsteps) issue_step<K, EPI, G, NG>(p, first, lane, t + 3, a1, b1);
     }
   }
