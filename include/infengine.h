@@ -248,6 +248,13 @@ IE_API int ie_gemm_bf16(ie_context* ctx, int m, int k, int n, const ie_bf16* d_x
 #define IE_GEMM_SWIGLU 3
 IE_API int ie_gemm_ex(ie_context* ctx, int epilogue, int m, int k, int n, const ie_bf16* d_x,
                       const ie_bf16* d_w0, const ie_bf16* d_w1, void* d_y);
+/* The causal GQA attention core of prefill on its own (the softmax(QK^T / sqrt(128)) V step of
+ * kernels/attn.cu:309-371, without the projections): d_q [seq_len][32][128] (RoPE applied),
+ * d_k / d_v one layer's K and V planes [8][8192][128] holding key rows 0..start_pos+seq_len-1,
+ * d_out [seq_len][4096] bf16 in the [s][h][d] layout of attn_permute.cu:15-31.  Query row i sits
+ * at position start_pos + i and sees keys 0..start_pos+i. */
+IE_API int ie_attn_prefill_core(ie_context* ctx, int seq_len, int start_pos, const ie_bf16* d_q,
+                                const ie_bf16* d_k, const ie_bf16* d_v, ie_bf16* d_out);
 
 #ifdef __cplusplus
 }

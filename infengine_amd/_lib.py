@@ -102,6 +102,7 @@ SIGNATURES: dict[str, tuple] = {
     "ie_final_norm_lm_head": (_i, [_p, _i, _p, _p, _p, _p]),
     "ie_gemm_bf16": (_i, [_p, _i, _i, _i, _p, _p, _p]),
     "ie_gemm_ex": (_i, [_p, _i, _i, _i, _i, _p, _p, _p, _p]),
+    "ie_attn_prefill_core": (_i, [_p, _i, _i, _p, _p, _p, _p]),
     "ie_tune_gemv_waves": (_i, [_i]),
     "ie_tune_gemv_pairs_per_wave": (_i, [_i]),
 }

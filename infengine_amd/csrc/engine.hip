@@ -793,6 +793,14 @@ int ie_gemm_bf16(ie_context* c, int m, int k, int n, const ie_bf16* d_x, const i
   return launch_gemm(kGemmBf16, g, c->stream);
 }
 
+int ie_attn_prefill_core(ie_context* c, int seq_len, int start_pos, const ie_bf16* d_q,
+                         const ie_bf16* d_k, const ie_bf16* d_v, ie_bf16* d_out) {
+  CTX_OK(c);
+  IE_REQUIRE(d_q && d_k && d_v && d_out, "attn_prefill_core: null pointer");
+  AttnPrefillParams a{d_q, d_k, d_v, d_out, seq_len, start_pos};
+  return launch_attn_prefill(a, c->stream);
+}
+
 int ie_gemm_ex(ie_context* c, int epilogue, int m, int k, int n, const ie_bf16* d_x,
                const ie_bf16* d_w0, const ie_bf16* d_w1, void* d_y) {
   CTX_OK(c);

@@ -5,21 +5,24 @@
 // ([32, S, S] fp16, cublasGemmBatchedEx), runs a causal softmax kernel
 // (softmax.cu:55-107), multiplies by V and permutes [h, s, d] -> [s, h, d].
 //
-// Here one workgroup owns 16 query rows of the 4 q heads of one kv head (GQA:
-// q head h reads kv head h/4, attn.cu:51-53); wave w is q head 4g + w, so every
-// K/V tile staged in LDS feeds 4 heads.  Per 64-key tile and wave:
-//   S^T[key][q] = K . Q^T      16 x v_mfma_f32_16x16x32_bf16 (A = K from LDS,
-//                                B = Q fragments held in registers)
+// Here a workgroup owns 32 query rows of the 4 q heads of one kv head (GQA: q head h reads kv
+// head h/4, attn.cu:51-53); wave w is q head 4g + w, so every K/V tile staged in LDS feeds the
+// 4 heads.  Per 64-key tile and wave, with v_mfma_f32_16x16x32_bf16:
+//   S^T[key][q] = K . Q^T      32 MFMAs (A = K rows from LDS, B = Q fragments in registers;
+//                                the two 16-query column blocks share every K fragment)
 //   online softmax per query column (scale 1/sqrt(128), causal mask key > q)
-//   O^T[d][q] += V^T . P^T      16 MFMAs; B = P^T straight from the S^T
-//                                accumulators: the 32 contraction slots of one
-//                                MFMA are mapped to keys {4G+r, 16+4G+r} of a
-//                                32-key half tile, the same permutation on both
-//                                operands, so P never goes through LDS
-// V is written to LDS transposed ([d][key], 8-byte key quads XOR-swizzled by
-// d & 15) so the A operand of the P.V product is two 8-byte LDS reads.  K rows
-// are 16 chunks of 16 bytes, chunk c of key r stored at c ^ (r & 15).
-// Output rows are [s][h][d] (the attn_permute.cu:15-31 layout), bf16.
+//   O^T[d][q] += V^T . P^T      32 MFMAs; B = P^T straight from the S^T accumulators: the 32
+//                                contraction slots of one MFMA are mapped to keys {4G+r, 16+4G+r}
+//                                of a 32-key half tile, the same permutation on both operands
+// K and V tiles go global -> LDS with direct-to-LDS buffer loads, row-major [key][128] (chunk c
+// of key r at slot c ^ (r & 15)), double-buffered so the next tile loads under this tile's
+// MFMAs.  The A operand of O^T is V^T; gfx950's ds_read_b64_tr_b16 reads it from the row-major
+// tile: in each 16-lane group, output lane j receives element j % 4 of the 8 bytes read by source
+// lanes 4e + j / 4 (e = 0..3), so with source lane s reading V[key0 + s/4][d0 + 4 (s%4) ..+3],
+// lane j gets V[key0 + e][d0 + j], e = 0..3: four consecutive keys of one dim.  Rows past the
+// last key read as zero (buffer bounds), so the masked tail never multiplies garbage.
+// Workgroups are issued longest causal extent first, paired so that the two a CU holds sum to
+// about the mean.  Output rows are [s][h][d] (the attn_permute.cu:15-31 layout), bf16.
 #include "ie_kernels.h"
 
 namespace ie {
@@ -27,150 +30,187 @@ namespace ie {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) short4_t lds_short4;
 
-constexpr int BQ = 16;    // query rows per workgroup
-constexpr int BKEY = 64;  // keys per LDS tile
+constexpr int BQ = 32;                // query rows per workgroup (two 16-row MFMA blocks)
+constexpr int BKEY = 64;              // keys per LDS tile
+constexpr int TC = BKEY * 16;         // 16-byte chunks per K (or V) tile
+constexpr int kRowBytes = kHeadDim * 2;
+constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw 32-bit access)
 
-__device__ __forceinline__ uint32_t pack_bf2_rn(float lo, float hi) { return pack_bf2(lo, hi); }
+__device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r & 15)); }
 
-__global__ __launch_bounds__(256) void flash_prefill_kernel(AttnPrefillParams p) {
-  __shared__ u32x4_t k_lds[BKEY * 16];          // [key][16 chunks], 16 KiB
-  __shared__ u32x2_t vt_lds[kHeadDim * (BKEY / 4)];  // [d][16 key quads], 16 KiB
+// Loads of tile t into ring stage `stage`: this wave's 4 K and 4 V row groups (4 rows each).
+// The tile offset goes into the vector offset, which the buffer range check covers.
+__device__ __forceinline__ void issue_tile(u32x4_t* lds, __amdgpu_buffer_rsrc_t krs,
+                                           __amdgpu_buffer_rsrc_t vrs, const uint32_t* voff,
+                                           int wv, int t, int stage) {
+  const uint32_t toff = (uint32_t)(t * BKEY * kRowBytes);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    u32x4_t* kd = &lds[stage * 2 * TC + (wv + 4 * j) * 64];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)kd, 16, voff[j] + toff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(kd + TC), 16, voff[j] + toff, 0, 0, 0);
+  }
+}
 
-  const int qt = blockIdx.x, g = blockIdx.y;
+__global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams p) {
+  __shared__ u32x4_t lds[2 * 2 * TC];  // [stage][K | V][key][16 chunks], 64 KiB
+
+  const int nqb = (p.S + BQ - 1) / BQ;
+  // workgroup b -> (query block, kv head): the first half of the grid takes the longest causal
+  // extents in descending order, the second half the shortest in ascending order
+  const int i = blockIdx.x / kKVHeads, g = blockIdx.x % kKVHeads;
+  const int half = (nqb + 1) / 2;
+  const int qb = i < half ? nqb - 1 - i : i - half;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int fr = lane & 15, G = lane >> 4;
   const int h = g * kGQA + wave;
-  const int row0 = qt * BQ;                       // first query row of the tile
+  const int row0 = qb * BQ;
   const int rows = min(BQ, p.S - row0);
-  const int q_abs = p.start_pos + row0 + fr;      // this lane's query position
-  const int nkeys = p.start_pos + row0 + rows;    // keys 0 .. nkeys-1 are needed
+  const int nkeys = p.start_pos + row0 + rows;
   const int ntiles = (nkeys + BKEY - 1) / BKEY;
 
-  const uint16_t* Kg = p.k + (size_t)g * kKVPlane;
-  const uint16_t* Vg = p.v + (size_t)g * kKVPlane;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.k + (size_t)g * kKVPlane), 0, nkeys * kRowBytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.v + (size_t)g * kKVPlane), 0, nkeys * kRowBytes, kBufferFlags);
+  // load j of this wave: tile rows 4 (wave + 4j) + lane/16; lane fills LDS slot lane%16 of its
+  // row from global chunk (lane%16) ^ (row & 15)
+  uint32_t voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * (wave + 4 * j) + (lane >> 4);
+    voff[j] = (uint32_t)(r * kRowBytes + (((lane & 15) ^ (r & 15)) * 16));
+  }
 
-  // Q^T fragments: lane holds Q[q = row0 + fr][d = 32 ks + 8 G .. +8]
-  bf16x8_t qf[4];
-  {
-    const int qr = row0 + min(fr, rows - 1);
+  // Q^T fragments: qf[qi][ks] = Q[row0 + 16 qi + fr][h][32 ks + 8 G .. +8]
+  bf16x8_t qf[2][4];
+#pragma unroll
+  for (int qi = 0; qi < 2; ++qi) {
+    const int qr = row0 + min(16 * qi + fr, rows - 1);
     const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(p.q + ((size_t)qr * kQHeads + h) * kHeadDim);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = __builtin_bit_cast(bf16x8_t, qrow[4 * ks + G]);
+    for (int ks = 0; ks < 4; ++ks) qf[qi][ks] = __builtin_bit_cast(bf16x8_t, qrow[4 * ks + G]);
   }
 
-  f32x4_t o[8];
+  f32x4_t o[2][8];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.f;
+  for (int qi = 0; qi < 2; ++qi)
+#pragma unroll
+    for (int db = 0; db < 8; ++db) o[qi][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
   const float scale = 0.08838834764831845f;  // 1/sqrt(128), softmax.cu:79
 
+  issue_tile(lds, krs, vrs, voff, wv, 0, 0);
   for (int t = 0; t < ntiles; ++t) {
+    // tile t has landed (the only loads in flight) and every wave is done with tile t-1
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (t + 1 < ntiles) issue_tile(lds, krs, vrs, voff, wv, t + 1, (t + 1) & 1);
+    const u32x4_t* kt = &lds[(t & 1) * 2 * TC];
+    const u32x4_t* vt = kt + TC;
     const int key0 = t * BKEY;
-    __syncthreads();  // the previous tile is fully consumed
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + i * 256, r = idx >> 4, c = idx & 15;
-      const int key = min(key0 + r, nkeys - 1);
-      const u32x4_t kv = reinterpret_cast<const u32x4_t*>(Kg + (size_t)key * kHeadDim)[c];
-      k_lds[r * 16 + (c ^ (r & 15))] = kv;
-      const u32x4_t vv = reinterpret_cast<const u32x4_t*>(Vg + (size_t)key * kHeadDim)[c];
-      // transpose: 8 dims of one key -> V^T[c*8 + e][key]
-      uint16_t* vt = reinterpret_cast<uint16_t*>(vt_lds);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = c * 8 + e;
-        const uint32_t w = vv[e >> 1];
-        const uint16_t val = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xFFFF);
-        vt[(d * (BKEY / 4) + ((r >> 2) ^ (d & 15))) * 4 + (r & 3)] = val;
-      }
-    }
-    __syncthreads();
 
-    // ---- S^T tiles: s[kt][r] = S[q = fr][key = key0 + 16 kt + 4 G + r]
-    f32x4_t s[4];
+    // ---- S^T blocks: s[qi][kb][r] = S[q = row0 + 16 qi + fr][key = key0 + 16 kb + 4 G + r]
+    f32x4_t s[2][4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      s[kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const int kr = kt * 16 + fr;
+    for (int kb = 0; kb < 4; ++kb) {
+      s[0][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      s[1][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, k_lds[kr * 16 + ((4 * ks + G) ^ fr)]);
-        s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[kt], 0, 0, 0);
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, kt[kv_slot(16 * kb + fr, 4 * ks + G)]);
+        s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][ks], s[0][kb], 0, 0, 0);
+        s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][ks], s[1][kb], 0, 0, 0);
       }
     }
-    // ---- online softmax for query column fr (spread over lanes fr, fr+16, fr+32, fr+48)
-    float mt = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = key0 + kt * 16 + 4 * G + r;
-        const float v = (key <= q_abs && key < nkeys) ? s[kt][r] * scale : -INFINITY;
-        s[kt][r] = v;
-        mt = fmaxf(mt, v);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mn = fmaxf(m, mt);
-    // a query row whose keys in this tile are all masked keeps mn = m (finite
-    // after its first tile, which always holds key 0)
-    const float alpha = __expf(m - mn);
-    float ls = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float e = __expf(s[kt][r] - mn);
-        s[kt][r] = e;
-        ls += e;
-      }
-    ls += __shfl_xor(ls, 16, 64);
-    ls += __shfl_xor(ls, 32, 64);
-    l = l * alpha + ls;
-    m = mn;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
 
-    // ---- P^T fragments (contraction slots 8G+r <-> key 32 ks2 + 4G + r,
-    //      8G+4+r <-> key 32 ks2 + 16 + 4G + r)
-    bf16x8_t pb[2];
+    // ---- online softmax per query column (spread over lanes fr, fr+16, fr+32, fr+48)
+    bf16x8_t pb[2][2];
 #pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
-      const u32x4_t w = {pack_bf2_rn(s[2 * ks2][0], s[2 * ks2][1]),
-                         pack_bf2_rn(s[2 * ks2][2], s[2 * ks2][3]),
-                         pack_bf2_rn(s[2 * ks2 + 1][0], s[2 * ks2 + 1][1]),
-                         pack_bf2_rn(s[2 * ks2 + 1][2], s[2 * ks2 + 1][3])};
-      pb[ks2] = __builtin_bit_cast(bf16x8_t, w);
-    }
-    // ---- O^T[d][q] += V^T[d][keys] . P^T[keys][q]
+    for (int qi = 0; qi < 2; ++qi) {
+      const int q_abs = p.start_pos + row0 + 16 * qi + fr;
+      float mt = -INFINITY;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const int d = dt * 16 + fr;
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = key0 + 16 * kb + 4 * G + r;
+          const float v = (key <= q_abs && key < nkeys) ? s[qi][kb][r] * scale : -INFINITY;
+          s[qi][kb][r] = v;
+          mt = fmaxf(mt, v);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      // a query row whose keys in this tile are all masked keeps mn = m (finite after its
+      // first tile, which always holds key 0)
+      const float mn = fmaxf(m[qi], mt);
+      const float alpha = __expf(m[qi] - mn);
+      float ls = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float e = __expf(s[qi][kb][r] - mn);
+          s[qi][kb][r] = e;
+          ls += e;
+        }
+      ls += __shfl_xor(ls, 16, 64);
+      ls += __shfl_xor(ls, 32, 64);
+      l[qi] = l[qi] * alpha + ls;
+      m[qi] = mn;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) o[qi][db] *= alpha;
+      // P^T fragments: contraction slot 8 G + r <-> key 32 ks2 + 4 G + r,
+      //                slot 8 G + 4 + r <-> key 32 ks2 + 16 + 4 G + r
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
-        const int kq0 = (8 * ks2 + G) ^ (d & 15);          // keys 32 ks2 + 4G .. +3
-        const int kq1 = (8 * ks2 + 4 + G) ^ (d & 15);      // keys 32 ks2 + 16 + 4G .. +3
-        const u32x2_t lo = vt_lds[d * (BKEY / 4) + kq0];
-        const u32x2_t hi = vt_lds[d * (BKEY / 4) + kq1];
-        const u32x4_t av = {lo[0], lo[1], hi[0], hi[1]};
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av), pb[ks2],
-                                                         o[dt], 0, 0, 0);
+        const u32x4_t w = {pack_bf2(s[qi][2 * ks2][0], s[qi][2 * ks2][1]),
+                           pack_bf2(s[qi][2 * ks2][2], s[qi][2 * ks2][3]),
+                           pack_bf2(s[qi][2 * ks2 + 1][0], s[qi][2 * ks2 + 1][1]),
+                           pack_bf2(s[qi][2 * ks2 + 1][2], s[qi][2 * ks2 + 1][3])};
+        pb[qi][ks2] = __builtin_bit_cast(bf16x8_t, w);
+      }
+    }
+
+    // ---- O^T[d][q] += V^T[d][keys] . P^T[keys][q]; the V^T fragment of dims 16 db .. +15 and
+    //      the slot order above is two transposed 8-byte reads per lane
+    const int kr = fr >> 2, dq = fr & 3;  // source-lane role in the transposed read
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const int c = 2 * db + (dq >> 1), hb = (dq & 1) * 8;  // chunk and byte of dims 16db + 4dq
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        const int ka = 32 * ks2 + 4 * G + kr, kb2 = ka + 16;
+        const char* va = reinterpret_cast<const char*>(&vt[kv_slot(ka, c)]) + hb;
+        const char* vb = reinterpret_cast<const char*>(&vt[kv_slot(kb2, c)]) + hb;
+        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)va);
+        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)vb);
+        const short4_t both[2] = {lo, hi};
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, both);
+        o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][ks2], o[0][db], 0, 0, 0);
+        o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][ks2], o[1][db], 0, 0, 0);
       }
     }
   }
 
-  // ---- o[dt][r] = O[q = fr][d = 16 dt + 4 G + r] (unnormalised)
-  if (fr < rows) {
-    const float inv = 1.0f / l;
-    uint16_t* dst = p.out + (size_t)(row0 + fr) * kHidden + h * kHeadDim;
+  // ---- o[qi][db][r] = O[q = row0 + 16 qi + fr][d = 16 db + 4 G + r] (unnormalised)
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const u32x2_t w = {pack_bf2(o[dt][0] * inv, o[dt][1] * inv),
-                         pack_bf2(o[dt][2] * inv, o[dt][3] * inv)};
-      *reinterpret_cast<u32x2_t*>(dst + dt * 16 + 4 * G) = w;
+  for (int qi = 0; qi < 2; ++qi) {
+    if (16 * qi + fr < rows) {
+      const float inv = 1.0f / l[qi];
+      uint16_t* dst = p.out + (size_t)(row0 + 16 * qi + fr) * kHidden + h * kHeadDim;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        const u32x2_t w = {pack_bf2(o[qi][db][0] * inv, o[qi][db][1] * inv),
+                           pack_bf2(o[qi][db][2] * inv, o[qi][db][3] * inv)};
+        *reinterpret_cast<u32x2_t*>(dst + db * 16 + 4 * G) = w;
+      }
     }
   }
 }
@@ -180,8 +220,8 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(AttnPrefillParams p)
 int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t st) {
   IE_REQUIRE(p.S >= 1 && p.start_pos >= 0 && p.start_pos + p.S <= kMaxCtx,
              "attn_prefill: rows [%d, %d) exceed the KV cache", p.start_pos, p.start_pos + p.S);
-  hipLaunchKernelGGL(flash_prefill_kernel, dim3((p.S + BQ - 1) / BQ, kKVHeads), dim3(256), 0, st,
-                     p);
+  const int nqb = (p.S + BQ - 1) / BQ;
+  hipLaunchKernelGGL(flash_prefill_kernel, dim3(nqb * kKVHeads), dim3(256), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
