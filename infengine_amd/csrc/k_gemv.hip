@@ -151,15 +151,17 @@ struct AttnItem {
   float4 oa[kAttnFusedSplits], ob[kAttnFusedSplits];
 };
 
-// Slots sp >= ns re-read slot ns-1 (L1 hits; attn_merge reads only the first ns): the loads
-// stay unconditional, which keeps the compiler's wait counts exact, so the staging does not
-// wait for the weight stream, without fetching slots past ns from L2.
-__device__ __forceinline__ void attn_load(const GemvParams& p, int i, int ns, AttnItem& a) {
+// All kAttnFusedSplits slots are loaded (they lie inside the partials buffer, which holds
+// kAttnSplits per kv head; attn_merge reads only the first ns).  The loads neither branch nor
+// depend on ns (a device value in graph replays): either would let the compiler issue them
+// after the weight stream, or make its wait at the merge conservative, and the staging would
+// then wait for the weights.
+__device__ __forceinline__ void attn_load(const GemvParams& p, int i, AttnItem& a) {
   const int h = i >> 4, c = i & 15;
   const size_t slot0 = ((size_t)(h / kGQA) * kAttnSplits) * kGQA + (h % kGQA);
 #pragma unroll
   for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
-    const size_t slot = slot0 + (size_t)min(sp, ns - 1) * kGQA;
+    const size_t slot = slot0 + (size_t)sp * kGQA;
     a.ml[sp] = *reinterpret_cast<const float2*>(p.attn_part_ml + slot * 2);
     const float4* po = reinterpret_cast<const float4*>(p.attn_part_o + slot * kHeadDim + c * 8);
     a.oa[sp] = po[0];
@@ -258,11 +260,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   int ns = 0;
   if constexpr (ATTN) {
     static_assert(K == kQHeads * kHeadDim && !NORM, "attention input: the O projection only");
+#pragma unroll
+    for (int j = 0; j < AI; ++j) attn_load(p, min(tid + j * T, kQHeads * kHeadDim / 8 - 1), ai[j]);
     const int S = p.d_seq_len ? *p.d_seq_len : p.pos;
     ns = attn_decode_splits((S + kAttnTile - 1) / kAttnTile, p.attn_max_splits);
-#pragma unroll
-    for (int j = 0; j < AI; ++j)
-      attn_load(p, min(tid + j * T, kQHeads * kHeadDim / 8 - 1), ns, ai[j]);
   } else {
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
@@ -274,6 +275,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
 
   EpiPre epre;
   if constexpr (ONE) epre = epi_preload<EPI>(p, min(first, p.n_pairs - 1));
+  __builtin_amdgcn_sched_barrier(0);  // keep every input load ahead of the weight stream
 
   // Weight stream: two steps in flight in two register buffers (B0: even steps, B1: odd).
   u32x4_t a0[G], b0[G], a1[G], b1[G];
