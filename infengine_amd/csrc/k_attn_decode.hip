@@ -87,7 +87,7 @@ __device__ __forceinline__ void attend_slices(const uint16_t* Kh, const uint16_t
     sc[lane] = pr;
 #pragma unroll
     for (int h = 0; h < kGQA; ++h) {
-      const float a = __shfl(alpha, h * kSlice, 64);
+      const float a = readlane_f(alpha, h * kSlice);
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[h][i] *= a;
     }
@@ -112,8 +112,7 @@ __device__ __forceinline__ void attend_slices(const uint16_t* Kh, const uint16_t
   for (int h = 0; h < kGQA; ++h)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      acc[h][i] += __shfl_xor(acc[h][i], 16, 64);
-      acc[h][i] += __shfl_xor(acc[h][i], 32, 64);
+      acc[h][i] = xor32_sum(xor16_sum(acc[h][i]));
     }
 }
 
@@ -169,7 +168,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(Att
   float o0 = 0.f, o1 = 0.f;
 #pragma unroll
   for (int w = 0; w < kSplitWaves; ++w) {
-    const float ww = __shfl(wl, w, 64);
+    const float ww = readlane_f(wl, w);
     o0 = fmaf(xo[w][h][2 * lane], ww, o0);
     o1 = fmaf(xo[w][h][2 * lane + 1], ww, o1);
   }

@@ -145,8 +145,7 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
           s[qi][kb][r] = v;
           mt = fmaxf(mt, v);
         }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      mt = xor32_max(xor16_max(mt));
       // a query row whose keys in this tile are all masked keeps mn = m (finite after its
       // first tile, which always holds key 0)
       const float mn = fmaxf(m[qi], mt);
@@ -160,8 +159,7 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
           s[qi][kb][r] = e;
           ls += e;
         }
-      ls += __shfl_xor(ls, 16, 64);
-      ls += __shfl_xor(ls, 32, 64);
+      ls = xor32_sum(xor16_sum(ls));
       l[qi] = l[qi] * alpha + ls;
       m[qi] = mn;
 #pragma unroll
