@@ -57,14 +57,14 @@ struct AttnDecodeParams {
   int seq_len;              // used when d_seq_len == nullptr (batch must be 1)
   int max_splits;           // splits per kv head cap: kAttnFusedSplits or kAttnSplits
 };
-// Splits per (sequence, kv head) for a context of ntiles 64-row tiles: one tile per wave
-// (two tile groups per split) up to the cap.  Device and host must agree on it.
+// Splits per (sequence, kv head) for a context of ntiles 64-row tiles: four tiles per split
+// (one per wave of the split workgroup) up to the cap.  Device and host must agree on it.
 __host__ __device__ inline int attn_decode_splits(int ntiles, int max_splits) {
-  const int n = (ntiles + 1) / 2;
+  const int n = (ntiles + 3) / 4;
   return n < 1 ? 1 : (n < max_splits ? n : max_splits);
 }
 // The O projection merges the partials itself while the context needs at most this many
-// splits (<= 1024 rows at one tile per wave; longer contexts run several tiles per wave).
+// splits (<= 2048 rows at one tile per wave; longer contexts run several tiles per wave).
 constexpr int kAttnFusedSplits = 8;
 constexpr int kAttnFusedMaxCtx = 4096;  // beyond: merge kernel + up to kAttnSplits splits
 // merge = also launch the merge kernel (bf16 output in p.out)

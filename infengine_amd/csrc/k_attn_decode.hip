@@ -3,21 +3,20 @@
 // Reference: decode_attn (kernels/attn.cu:373-439) runs QK^T and A.V as two
 // cuBLAS batched GEMVs over device pointer arrays plus a separate row softmax
 // (softmax.cu:109-160) with half-precision intermediates.  Here softmax(q.K^T /
-// sqrt(128)) . V for all 32 q heads runs in fp32 as split-context ("flash
-// decoding") attention:
+// sqrt(128)) . V for all 32 q heads runs as split-context ("flash decoding")
+// attention on MFMA:
 //
-//   grid  = (kAttnSplits, 8 kv heads, batch), block = 8 waves
-//   split s of kv head g owns a contiguous run of 64-row tiles of the context
-//   0..S-1; its 8 waves take 16-row slices of that run in turn and each computes
-//   all 4 q heads of the kv head (GQA: q head h reads kv head h/4, attn.cu:51-53)
-//   for its rows, so every K/V byte is fetched once per workgroup and each wave
-//   does 64 (row, head) dot products per slice.  Each wave keeps an online softmax
-//   (running max m, sum l, unnormalised output) per head over its slices; the 8
-//   waves are merged in LDS and the split writes one partial (m, l, o) per q head.
+//   grid  = (max_splits, 8 kv heads, batch), block = 4 waves
+//   split s of kv head g owns a contiguous run of 64-key tiles of the context 0..S-1 (four
+//   tiles per split, one per wave, while the split cap allows); a wave stages its tile's K
+//   and V rows in its own LDS slice with direct-to-LDS loads and computes, with
+//   v_mfma_f32_16x16x32_bf16, S^T = K . Q^T for the 4 GQA q heads of the kv head (GQA: q head h
+//   reads kv head h/4, attn.cu:51-53) as 4 of the 16 MFMA columns, an online softmax per head,
+//   and O^T += V^T . P^T with P^T taken straight from the S^T accumulators and V^T read with
+//   ds_read_b64_tr_b16, as in the prefill kernel.  The 4 waves are merged in LDS and the split
+//   writes one partial (m, l, o) per q head.
 //
-// The number of splits ns = min(max_splits, ceil(tiles / 2)) follows the context
-// length (two tiles, i.e. one slice per wave, per split while that fits).  The
-// partials of the ns splits are merged either by the O projection itself (its
+// The partials of the ns splits are merged either by the O projection itself (its
 // input-staging prologue reads them; decode with max_splits = 8, no extra launch)
 // or by a small merge kernel writing bf16 [h][128] (attn.cu:433-438) for the
 // batched GEMM path and long contexts (max_splits = 32).  A device-scope "last
@@ -29,92 +28,20 @@ namespace ie {
 
 namespace {
 
-constexpr int kSplitWaves = 8;
-constexpr int kSlice = 16;  // rows per wave per step
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) short4_t lds_short4;
 
-// Wave-local ordering of this wave's own LDS slice (waves run different slice counts, so no
-// workgroup barrier may sit inside the slice loop).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-}
+constexpr int kSplitWaves = 4;
+constexpr int kTC = kAttnTile * 16;        // 16-byte chunks of one K (or V) tile
+constexpr int kRowBytes = kHeadDim * 2;
+constexpr int kBufferFlags = 0x00020000;   // buffer descriptor word 3 (raw 32-bit access)
+static_assert(kAttnTile == 64, "tile = 4 x 16-key MFMA blocks");
 
-// Online-softmax attention of the 4 q heads of one kv head over the 16-row slices
-// first, first + stride, ... of rows [row0, row1) (row1 <= S).  Lane (sub = lane/16, dl =
-// lane%16) loads 16 bytes (dims 8dl..8dl+7) of rows 4it + sub, it = 0..3, of a slice.
-// Returns, in the lanes of 16-lane group h, head h's running max and sum (m_me, l_me), and in
-// every lane the unnormalised outputs acc[h][8] of dims 8dl.. summed over its rows.
-__device__ __forceinline__ void attend_slices(const uint16_t* Kh, const uint16_t* Vh,
-                                              const u32x4_t (&qv)[kGQA], int S, int row0,
-                                              int row1, int first, int stride, float* sc,
-                                              float& m_me, float& l_me, float (&acc)[kGQA][8]) {
-  const int lane = threadIdx.x & 63;
-  const int sub = lane >> 4, dl = lane & 15;
-  const float scale = 0.08838834764831845f;  // 1/sqrt(128), softmax.cu:79
-  m_me = -INFINITY;
-  l_me = 0.f;
-#pragma unroll
-  for (int h = 0; h < kGQA; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
-
-  for (int base = row0 + first * kSlice; base < row1; base += stride * kSlice) {
-    u32x4_t kk[kSlice / 4], vv[kSlice / 4];
-#pragma unroll
-    for (int it = 0; it < kSlice / 4; ++it) {
-      const int r = min(base + it * 4 + sub, S - 1);
-      kk[it] = reinterpret_cast<const u32x4_t*>(Kh + (size_t)r * kHeadDim)[dl];
-      vv[it] = reinterpret_cast<const u32x4_t*>(Vh + (size_t)r * kHeadDim)[dl];
-    }
-    // ---- scores: (head h, slice row j) -> sc[16h + j]; rows past row1 get -inf
-#pragma unroll
-    for (int it = 0; it < kSlice / 4; ++it) {
-      const int r = base + it * 4 + sub;
-#pragma unroll
-      for (int h = 0; h < kGQA; ++h) {
-        const float d = row16_sum(dot8(kk[it], qv[h], 0.f));
-        if (dl == 0) sc[h * kSlice + it * 4 + sub] = (r < row1) ? d * scale : -INFINITY;
-      }
-    }
-    wave_lds_sync();
-    // ---- online softmax, lane <-> (head lane/16, row lane%16); row `base` is always < row1
-    const float s = sc[lane];
-    const float mn = fmaxf(m_me, row16_max(s));
-    const float alpha = __expf(m_me - mn);
-    const float pr = __expf(s - mn);
-    l_me = l_me * alpha + row16_sum(pr);
-    m_me = mn;
-    sc[lane] = pr;
-#pragma unroll
-    for (int h = 0; h < kGQA; ++h) {
-      const float a = readlane_f(alpha, h * kSlice);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] *= a;
-    }
-    wave_lds_sync();
-    // ---- P . V: each lane accumulates 8 dims of each head over its 4 rows
-#pragma unroll
-    for (int it = 0; it < kSlice / 4; ++it) {
-#pragma unroll
-      for (int h = 0; h < kGQA; ++h) {
-        const float w = sc[h * kSlice + it * 4 + sub];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acc[h][2 * q] = fmaf(w, bf_lo(vv[it][q]), acc[h][2 * q]);
-          acc[h][2 * q + 1] = fmaf(w, bf_hi(vv[it][q]), acc[h][2 * q + 1]);
-        }
-      }
-    }
-    wave_lds_sync();
-  }
-  // fold the 4 row groups of the wave: lanes dl, dl+16, dl+32, dl+48
-#pragma unroll
-  for (int h = 0; h < kGQA; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      acc[h][i] = xor32_sum(xor16_sum(acc[h][i]));
-    }
-}
+// chunk c of key r of a tile at slot c ^ (r & 15) (LDS bank spread for the fragment reads)
+__device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r & 15)); }
 
 static_assert(kAttnSplits <= 64, "the merge gives each split one lane");
 
@@ -123,42 +50,142 @@ static_assert(kAttnSplits <= 64, "the merge gives each split one lane");
 __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(AttnDecodeParams p) {
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int dl = lane & 15;
+  const int fr = lane & 15, G = lane >> 4;
   const int S = p.d_seq_len ? p.d_seq_len[b] : p.seq_len;
   const int ntiles = (S + kAttnTile - 1) / kAttnTile;
   const int ns = attn_decode_splits(ntiles, p.max_splits);
   if (split >= ns) return;  // whole workgroup: nobody reads a partial past ns
   const int tps = (ntiles + ns - 1) / ns;
-  const int row0 = split * tps * kAttnTile;
-  const int row1 = min(S, row0 + tps * kAttnTile);
+  const int t0 = split * tps, t1 = min(ntiles, t0 + tps);
 
-  __shared__ float sc[kSplitWaves][kGQA * kSlice];
+  __shared__ u32x4_t lds[kSplitWaves][2][kTC];           // per wave: K tile, V tile
   __shared__ float xo[kSplitWaves][kGQA][kHeadDim];
   __shared__ float xml[kSplitWaves][kGQA][2];
   const uint16_t* Kh = p.k_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
   const uint16_t* Vh = p.v_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
-  u32x4_t qv[kGQA];
-#pragma unroll
-  for (int h = 0; h < kGQA; ++h)
-    qv[h] = reinterpret_cast<const u32x4_t*>(p.q + ((size_t)b * kQHeads + g * kGQA + h) * kHeadDim)[dl];
-  float m_me, l_me, acc[kGQA][8];
-  attend_slices(Kh, Vh, qv, S, row0, row1, wave, kSplitWaves, sc[wave], m_me, l_me, acc);
+  // rows past S read as zero (buffer bounds) and are masked below
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Kh, 0, S * kRowBytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Vh, 0, S * kRowBytes, kBufferFlags);
 
-  // merge the 8 waves' partials of each head (a wave without rows has l = 0: weight 0)
-  if (lane < 16) {
+  // Q^T fragments: MFMA column fr is q head 4g + fr for fr < 4 (zero elsewhere); lane supplies
+  // dims 32 ks + 8 G .. +8
+  bf16x8_t qf[4];
+  {
+    const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(
+        p.q + ((size_t)b * kQHeads + g * kGQA + min(fr, kGQA - 1)) * kHeadDim);
 #pragma unroll
-    for (int h = 0; h < kGQA; ++h) {
-      float4* d = reinterpret_cast<float4*>(&xo[wave][h][dl * 8]);
-      d[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-      d[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4_t v = qrow[4 * ks + G];
+      qf[ks] = __builtin_bit_cast(bf16x8_t, fr < kGQA ? v : u32x4_t{0u, 0u, 0u, 0u});
     }
   }
-  if ((lane & 15) == 0) {
-    xml[wave][lane >> 4][0] = m_me;
-    xml[wave][lane >> 4][1] = l_me;
+  const float scale = 0.08838834764831845f;  // 1/sqrt(128), softmax.cu:79
+  float m = -INFINITY, l = 0.f;
+  f32x4_t o[8];
+#pragma unroll
+  for (int db = 0; db < 8; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  u32x4_t* kt = lds[wave][0];
+  const u32x4_t* vt = lds[wave][1];
+
+  for (int t = t0 + wave; t < t1; t += kSplitWaves) {
+    // stage tile t: load j fills rows 4j .. 4j+3; lane fills slot lane%16 of row 4j + lane/16
+    // from global chunk (lane%16) ^ (row & 15).  The wave only reads its own slice, so its own
+    // vmcnt wait is the whole synchronisation.
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = 4 * j + G;
+      const uint32_t off = (uint32_t)((t * kAttnTile + r) * kRowBytes + ((fr ^ (r & 15)) * 16));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)&kt[64 * j], 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)&kt[kTC + 64 * j], 16, off, 0, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int key0 = t * kAttnTile;
+
+    // ---- S^T blocks: s[kb][r] = S[q head 4g + fr][key key0 + 16 kb + 4 G + r]
+    f32x4_t s[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      s[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, kt[kv_slot(16 * kb + fr, 4 * ks + G)]);
+        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[kb], 0, 0, 0);
+      }
+    }
+    // ---- online softmax per q column (spread over lanes fr, fr+16, fr+32, fr+48)
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = key0 + 16 * kb + 4 * G + r;
+        const float v = key < S ? s[kb][r] * scale : -INFINITY;
+        s[kb][r] = v;
+        mt = fmaxf(mt, v);
+      }
+    mt = xor32_max(xor16_max(mt));   // finite: key key0 < S is in every processed tile
+    const float mn = fmaxf(m, mt);
+    const float alpha = __expf(m - mn);
+    float ls = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __expf(s[kb][r] - mn);
+        s[kb][r] = e;
+        ls += e;
+      }
+    l = l * alpha + xor32_sum(xor16_sum(ls));
+    m = mn;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) o[db] *= alpha;
+    // P^T fragments: slot 8 G + r <-> key 32 ks2 + 4 G + r, slot 8 G + 4 + r <-> key
+    // 32 ks2 + 16 + 4 G + r
+    bf16x8_t pb[2];
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      const u32x4_t w = {pack_bf2(s[2 * ks2][0], s[2 * ks2][1]), pack_bf2(s[2 * ks2][2], s[2 * ks2][3]),
+                         pack_bf2(s[2 * ks2 + 1][0], s[2 * ks2 + 1][1]),
+                         pack_bf2(s[2 * ks2 + 1][2], s[2 * ks2 + 1][3])};
+      pb[ks2] = __builtin_bit_cast(bf16x8_t, w);
+    }
+    // ---- O^T[d][q] += V^T[d][keys] . P^T[keys][q]; V^T by transposed LDS reads (source lane
+    //      s of a 16-lane group reads V[key0 + s/4][d0 + 4 (s%4) .. +3])
+    const int kr = fr >> 2, dq = fr & 3;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const int c = 2 * db + (dq >> 1), hb = (dq & 1) * 8;
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        const int ka = 32 * ks2 + 4 * G + kr;
+        const char* va = reinterpret_cast<const char*>(&vt[kv_slot(ka, c)]) + hb;
+        const char* vb = reinterpret_cast<const char*>(&vt[kv_slot(ka + 16, c)]) + hb;
+        const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)va);
+        const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)vb);
+        const short4_t both[2] = {lo, hi};
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, both), pb[ks2],
+                                                        o[db], 0, 0, 0);
+      }
+    }
+    // the next tile's loads overwrite this slice: every read of it has returned
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+
+  // ---- this wave's partial: o[db][r] = O^T[d = 16 db + 4 G + r][head fr] (fr < 4); a wave
+  //      without tiles has l = 0 (weight 0 in the merge)
+  if (fr < kGQA) {
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+      *reinterpret_cast<float4*>(&xo[wave][fr][16 * db + 4 * G]) =
+          make_float4(o[db][0], o[db][1], o[db][2], o[db][3]);
+    if (G == 0) {
+      xml[wave][fr][0] = m;
+      xml[wave][fr][1] = l;
+    }
   }
   __syncthreads();
-  if (wave >= kGQA) return;
   const int h = wave;  // wave h merges q head 4g + h; lane d owns dims 2d, 2d+1
   const float mw = lane < kSplitWaves ? xml[lane][h][0] : -INFINITY;
   const float lw = lane < kSplitWaves ? xml[lane][h][1] : 0.f;
