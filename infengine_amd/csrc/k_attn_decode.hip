@@ -8,8 +8,9 @@
 //
 //   grid  = (max_splits, 8 kv heads, batch), block = 4 waves
 //   split s of kv head g owns a contiguous run of 64-key tiles of the context 0..S-1 (four
-//   tiles per split, one per wave, while the split cap allows); a wave stages its tile's K
-//   and V rows in its own LDS slice with direct-to-LDS loads and computes, with
+//   tiles per split, one per wave, while the split cap allows); a wave stages its tile's V
+//   rows (and at batch 1 its K rows) in its own LDS slice with direct-to-LDS loads, and
+//   computes, with
 //   v_mfma_f32_16x16x32_bf16, S^T = K . Q^T for the 4 GQA q heads of the kv head (GQA: q head h
 //   reads kv head h/4, attn.cu:51-53) as 4 of the 16 MFMA columns, an online softmax per head,
 //   and O^T += V^T . P^T with P^T taken straight from the S^T accumulators and V^T read with
@@ -46,7 +47,11 @@ __device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r &
 static_assert(kAttnSplits <= 64, "the merge gives each split one lane");
 
 // Phase 1: split s of (batch b, kv head g) attends its run of tiles and writes the
-// unnormalised partial (m, l, o) of each of the 4 q heads.
+// unnormalised partial (m, l, o) of each of the 4 q heads.  KREG: K fragments are loaded
+// straight into registers (72 KiB of LDS per workgroup, two workgroups per CU: the batched
+// grid); otherwise K goes through LDS like V (136 KiB, one workgroup per CU; measured 0.7%
+// faster per decode step at batch 1).
+template <bool KREG>
 __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(AttnDecodeParams p) {
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -58,7 +63,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(Att
   const int tps = (ntiles + ns - 1) / ns;
   const int t0 = split * tps, t1 = min(ntiles, t0 + tps);
 
-  __shared__ u32x4_t lds[kSplitWaves][2][kTC];           // per wave: K tile, V tile
+  __shared__ u32x4_t kvlds[kSplitWaves][KREG ? 1 : 2][kTC];  // per wave: (K tile,) V tile
   __shared__ float xo[kSplitWaves][kGQA][kHeadDim];
   __shared__ float xml[kSplitWaves][kGQA][2];
   const uint16_t* Kh = p.k_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
@@ -86,22 +91,40 @@ __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(Att
   f32x4_t o[8];
 #pragma unroll
   for (int db = 0; db < 8; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  u32x4_t* kt = lds[wave][0];
-  const u32x4_t* vt = lds[wave][1];
+  u32x4_t* kt = kvlds[wave][0];
+  u32x4_t* vt = kvlds[wave][KREG ? 0 : 1];
 
   for (int t = t0 + wave; t < t1; t += kSplitWaves) {
-    // stage tile t: load j fills rows 4j .. 4j+3; lane fills slot lane%16 of row 4j + lane/16
+    // K fragments kk[kb][ks] = K[key0 + 16 kb + fr][32 ks + 8 G .. +8], straight from memory
+    // (KREG) or from the LDS tile below
+    const int key0 = t * kAttnTile;
+    u32x4_t kk[4][4];
+    if constexpr (KREG) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          kk[kb][ks] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+              krs, (uint32_t)((key0 + 16 * kb + fr) * kRowBytes + (4 * ks + G) * 16), 0, 0));
+    }
+    // tiles to LDS: load j fills rows 4j .. 4j+3; lane fills slot lane%16 of row 4j + lane/16
     // from global chunk (lane%16) ^ (row & 15).  The wave only reads its own slice, so its own
     // vmcnt wait is the whole synchronisation.
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int r = 4 * j + G;
-      const uint32_t off = (uint32_t)((t * kAttnTile + r) * kRowBytes + ((fr ^ (r & 15)) * 16));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)&kt[64 * j], 16, off, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)&kt[kTC + 64 * j], 16, off, 0, 0, 0);
+      const uint32_t off = (uint32_t)((key0 + r) * kRowBytes + ((fr ^ (r & 15)) * 16));
+      if constexpr (!KREG)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)&kt[64 * j], 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)&vt[64 * j], 16, off, 0, 0, 0);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const int key0 = t * kAttnTile;
+    if constexpr (!KREG) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kk[kb][ks] = kt[kv_slot(16 * kb + fr, 4 * ks + G)];
+    }
 
     // ---- S^T blocks: s[kb][r] = S[q head 4g + fr][key key0 + 16 kb + 4 G + r]
     f32x4_t s[4];
@@ -109,10 +132,9 @@ __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(Att
     for (int kb = 0; kb < 4; ++kb) {
       s[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, kt[kv_slot(16 * kb + fr, 4 * ks + G)]);
-        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[ks], s[kb], 0, 0, 0);
-      }
+      for (int ks = 0; ks < 4; ++ks)
+        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kk[kb][ks]),
+                                                        qf[ks], s[kb], 0, 0, 0);
     }
     // ---- online softmax per q column (spread over lanes fr, fr+16, fr+32, fr+48)
     float mt = -INFINITY;
@@ -153,6 +175,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(Att
     }
     // ---- O^T[d][q] += V^T[d][keys] . P^T[keys][q]; V^T by transposed LDS reads (source lane
     //      s of a 16-lane group reads V[key0 + s/4][d0 + 4 (s%4) .. +3])
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the V tile has landed in LDS
     const int kr = fr >> 2, dq = fr & 3;
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
@@ -259,8 +282,12 @@ int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStre
              p.max_splits);
   // one workgroup per possible split: idle ones would still cost dispatch (at batch 16 and
   // 32 splits, 4096 mostly empty workgroups took 52 us)
-  hipLaunchKernelGGL(attn_decode_split_kernel, dim3(p.max_splits, kKVHeads, batch),
-                     dim3(kSplitWaves * 64), 0, st, p);
+  if (batch > 1)
+    hipLaunchKernelGGL(attn_decode_split_kernel<true>, dim3(p.max_splits, kKVHeads, batch),
+                       dim3(kSplitWaves * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL(attn_decode_split_kernel<false>, dim3(p.max_splits, kKVHeads, batch),
+                       dim3(kSplitWaves * 64), 0, st, p);
   IE_CHECK_LAUNCH();
   if (merge) {
     IE_REQUIRE(p.out, "attn_decode: merge needs an output buffer");
