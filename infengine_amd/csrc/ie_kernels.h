@@ -64,8 +64,10 @@ __host__ __device__ inline int attn_decode_splits(int ntiles, int max_splits) {
   return n < 1 ? 1 : (n < max_splits ? n : max_splits);
 }
 // The O projection merges the partials itself while the context needs at most this many
-// splits (<= 2048 rows at one tile per wave; longer contexts run several tiles per wave).
-constexpr int kAttnFusedSplits = 8;
+// splits (<= 1024 rows at one tile per wave; longer contexts run several tiles per wave).
+// Every O-projection workgroup reads all of them, so the cap is small: 4 measured 0.5% faster
+// per decode step than 8 at p = 600 (and 4% on the bs=16 batched step).
+constexpr int kAttnFusedSplits = 4;
 constexpr int kAttnFusedMaxCtx = 4096;  // beyond: merge kernel + up to kAttnSplits splits
 // merge = also launch the merge kernel (bf16 output in p.out)
 int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStream_t st);
