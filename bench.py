@@ -1,10 +1,11 @@
 """Decode benchmark: random-init Llama-3.1-8B (bf16), batch 1, on one MI355X.
 
-One timed "step" is one ie_decode_step (decode.cuh:6-9 semantics: embed the last
-token, 32 layers, final norm, lm_head, argmax, token read back to the host) plus
-the reference's device-side token write-back (manager.cpp:84).  The KV cache is
-first filled by ie_prefill over a random prompt, so the timed steps run at real
-positions (prompt_len .. prompt_len + warmup + steps).
+One timed "step" is one decode step of ie_generate, the library's Manager loop
+(manager.cpp:60-86): decode.cuh:6-9 semantics (embed the last token, 32 layers,
+final norm, lm_head, argmax, token returned to the host) plus the reference's
+device-side token write-back (manager.cpp:84).  The KV cache is first filled by
+the loop's prefill over a random prompt, so the timed steps run at real positions
+(prompt_len + warmup .. prompt_len + warmup + steps - 1).
 
 Also reported, on the same run:
   roofline      the dominant decode kernel (fused RMSNorm -> gate/up GEMV -> SwiGLU,
@@ -152,27 +153,15 @@ def main() -> int:
     prefill_s = time.perf_counter() - t0
     req.tokens[args.prompt] = tok
 
-    seq = args.prompt + 1
-
-    def step(seq_len: int) -> int:
-        t = req.decode_step(seq_len)
-        req.tokens[seq_len: seq_len + 1].copy_(req.token)     # manager.cpp:84 (D2D write-back)
-        return t
-
-    log(f"decode warmup {args.warmup}")
-    for _ in range(args.warmup):
-        step(seq)
-        seq += 1
-    torch.cuda.synchronize()
-    first_pos = seq - 1
-    log(f"decode timed {args.steps}")
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(seq)
-        seq += 1
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    last_pos = seq - 2
+    # ---- decode: the Manager loop (manager.cpp:60-86) in the library: prefill, then decode
+    # steps, each with its device-side token write-back (manager.cpp:84) and the token returned
+    # to the host; steps 1..warmup are untimed
+    n_new = 1 + args.warmup + args.steps
+    toks, timed_ms = req.generate(ids, n_new, timed_from=1 + args.warmup)
+    assert toks[0] == tok, "ie_generate's prefill token differs from ie_prefill's"
+    first_pos = args.prompt + args.warmup          # position of the first timed step's token
+    last_pos = args.prompt + args.warmup + args.steps - 1
+    dt = timed_ms / 1e3
     ms_per_step = dt * 1e3 / args.steps
     tok_s = args.steps / dt
     kv_bytes = KV_BYTES_PER_POS * sum(p + 1 for p in range(first_pos, last_pos + 1)) / args.steps

@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <chrono>
 #include <cstring>
 #include <mutex>
 #include <numbers>
@@ -177,9 +178,12 @@ int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, 
   return IE_OK;
 }
 
+// wb_buf: when set, the argmax also stores the token at wb_buf[seq_len] (the Manager loop's
+// write-back, manager.cpp:84).  The argmax always advances d_params[0] and hands the token to
+// the host through mapped memory.
 int enqueue_decode(Context* c, hipStream_t st, const ie_model_weights& W, int seq_len,
                    int* tokenid_buff, uint16_t* data, uint16_t* attn, float* logits, int* out_tok,
-                   void* ws, void* kv) {
+                   void* ws, void* kv, int* wb_buf) {
   const int* d_sl = c->d_params;
   const DecodeWs w = decode_ws(ws, 1);
   IE_TRY(launch_emblookup(1, tokenid_buff, W.emb_lookup, data, d_sl, 0, st));
@@ -187,8 +191,12 @@ int enqueue_decode(Context* c, hipStream_t st, const ie_model_weights& W, int se
     IE_TRY(decoder_layer_decode(c, st, W, l, data, attn, w, kv, d_sl, seq_len));
   IE_TRY(gemv_plain(kHidden, kEpiF32, data, W.final_norm, W.lm_head, nullptr, kVocab / 2,
                     nullptr, logits, 1, kVocab, st));
+  ArgmaxTail tail;
+  tail.host_tok = c->h_token_dev;
+  tail.tok_buf = wb_buf;
+  tail.seq = c->d_params;
   IE_TRY(launch_argmax_rows(1, kVocab, logits, out_tok, c->d_slots, c->d_counters + kCntArgmax,
-                            st));
+                            st, tail));
   return IE_OK;
 }
 
@@ -288,8 +296,13 @@ int ie_context_create(ie_context** out, int device, void* stream) {
         hipMalloc(&c->d_slots, kNumSlots * sizeof(unsigned long long)) != hipSuccess ||
         hipMalloc(&c->d_params, 64 * sizeof(int)) != hipSuccess ||
         hipHostMalloc(&c->h_params, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc(&c->h_token, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+        hipHostMalloc(&c->h_token, 64 * sizeof(int), hipHostMallocMapped) != hipSuccess) {
       rc = IE_ERR_OOM;
+      break;
+    }
+    if (hipHostGetDevicePointer(reinterpret_cast<void**>(&c->h_token_dev), c->h_token, 0) !=
+        hipSuccess) {
+      rc = IE_ERR_HIP;
       break;
     }
     if (hipMemset(c->d_counters, 0, kNumCounters * sizeof(unsigned int)) != hipSuccess ||
@@ -351,28 +364,41 @@ size_t ie_batch_workspace_size(int batch) {
 }
 
 // ---------------------------------------------------------------- decode_step
-int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
-                   int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
-                   ie_bf16* attn_buffer, float* output_distr, int* output_token,
-                   void* workspace, void* kv_cache) {
-  (void)aux_buffer;  // normalised activations never leave the GEMV prologues
-  CTX_OK(c);
+}  // extern "C"
+
+namespace ie {
+namespace {
+
+// One decode step (decode.cuh:6-9).  d_params[0] (the position the kernels read) is copied
+// from the host only when it differs from what the previous step's argmax advanced it to; the
+// token reaches the host through mapped memory written by the argmax, so a step costs one
+// graph launch and one stream synchronisation.  wb = true also writes the token back to
+// tokenid_buff[seq_len] on the device (manager.cpp:84).
+int decode_step_impl(Context* c, const ie_model_weights* weights, int seq_len, int* tokenid_buff,
+                     ie_bf16* data_buffer, ie_bf16* attn_buffer, float* output_distr,
+                     int* output_token, void* workspace, void* kv_cache, bool wb) {
   IE_REQUIRE(weights && weights_complete(*weights), "decode_step: incomplete weights");
   IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "decode_step: seq_len %d out of [1, %d]",
              seq_len, kMaxCtx);
+  IE_REQUIRE(!wb || seq_len < kMaxCtx, "decode_step: no slot after position %d", seq_len - 1);
   IE_REQUIRE(tokenid_buff && data_buffer && attn_buffer && output_distr && output_token &&
                  workspace && kv_cache,
              "decode_step: null buffer");
   hipStream_t st = c->stream;
-  c->h_params[0] = seq_len;
-  IE_CHECK_HIP(hipMemcpyAsync(c->d_params, c->h_params, sizeof(int), hipMemcpyHostToDevice, st));
+  const bool copy = seq_len != c->next_seq;
+  c->next_seq = -1;  // unknown until this step is enqueued
+  if (copy) {
+    c->h_params[0] = seq_len;
+    IE_CHECK_HIP(hipMemcpyAsync(c->d_params, c->h_params, sizeof(int), hipMemcpyHostToDevice, st));
+  }
+  int* wb_buf = wb ? tokenid_buff : nullptr;
 
   if (c->use_graph) {
     const void* key[12] = {(const void*)weights, tokenid_buff, data_buffer, attn_buffer,
                            output_distr, output_token, workspace, kv_cache,
                            (const void*)(uintptr_t)hash_bytes(weights, sizeof(*weights)),
                            // the captured attention path depends on the context length
-                           (const void*)(uintptr_t)(attn_fused(seq_len) ? 1 : 2), nullptr,
+                           (const void*)(uintptr_t)(attn_fused(seq_len) ? 1 : 2), wb_buf,
                            nullptr};
     if (!c->graph_exec || std::memcmp(key, c->graph_key, sizeof key) != 0) {
       if (c->graph_exec) {
@@ -384,7 +410,8 @@ int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
       hipGraph_t g = nullptr;
       IE_CHECK_HIP(hipStreamBeginCapture(c->capture, hipStreamCaptureModeThreadLocal));
       const int rc = enqueue_decode(c, c->capture, *weights, seq_len, tokenid_buff, data_buffer,
-                                    attn_buffer, output_distr, output_token, workspace, kv_cache);
+                                    attn_buffer, output_distr, output_token, workspace, kv_cache,
+                                    wb_buf);
       const hipError_t ec = hipStreamEndCapture(c->capture, &g);
       if (rc != IE_OK) {
         if (g) (void)hipGraphDestroy(g);
@@ -399,11 +426,70 @@ int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
     IE_CHECK_HIP(hipGraphLaunch(c->graph_exec, st));
   } else {
     IE_TRY(enqueue_decode(c, st, *weights, seq_len, tokenid_buff, data_buffer, attn_buffer,
-                          output_distr, output_token, workspace, kv_cache));
+                          output_distr, output_token, workspace, kv_cache, wb_buf));
   }
-  IE_CHECK_HIP(hipMemcpyAsync(c->h_token, output_token, sizeof(int), hipMemcpyDeviceToHost, st));
   IE_CHECK_HIP(hipStreamSynchronize(st));
-  return c->h_token[0];
+  c->next_seq = seq_len + 1;
+  return *static_cast<volatile int*>(c->h_token);
+}
+
+}  // namespace
+}  // namespace ie
+
+extern "C" {
+
+int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
+                   int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                   ie_bf16* attn_buffer, float* output_distr, int* output_token,
+                   void* workspace, void* kv_cache) {
+  (void)aux_buffer;  // normalised activations never leave the GEMV prologues
+  CTX_OK(c);
+  return decode_step_impl(c, weights, seq_len, tokenid_buff, data_buffer, attn_buffer,
+                          output_distr, output_token, workspace, kv_cache, false);
+}
+
+// Manager::handle_request's generation loop (manager.cpp:60-86) without the tokenizer: the
+// prompt ids go to the device, one prefill, then decode steps, each token written back to
+// tokenid_buff on the device before the next step reads it.  out_tokens[0] is the prefill's
+// token, out_tokens[i] the i-th decode step's.  timed_ms (optional) receives the host wall time
+// of decode steps timed_from .. max_new_tokens-1 (after a stream synchronisation).
+int ie_generate(ie_context* c, const ie_model_weights* weights, const int* prompt, int prompt_len,
+                int max_new_tokens, int timed_from, int* out_tokens, int* tokenid_buff,
+                ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
+                float* output_distr, int* output_token, void* workspace, void* kv_cache,
+                double* timed_ms) {
+  CTX_OK(c);
+  IE_REQUIRE(prompt && out_tokens, "generate: null prompt / output");
+  IE_REQUIRE(prompt_len >= 1 && max_new_tokens >= 1 && prompt_len + max_new_tokens <= kMaxCtx,
+             "generate: prompt %d + %d new tokens exceed the context %d", prompt_len,
+             max_new_tokens, kMaxCtx);
+  IE_CHECK_HIP(hipMemcpyAsync(tokenid_buff, prompt, prompt_len * sizeof(int),
+                              hipMemcpyHostToDevice, c->stream));
+  const int first = ie_prefill(c, weights, prompt_len, tokenid_buff, data_buffer, aux_buffer,
+                               attn_buffer, output_distr, output_token, workspace, kv_cache);
+  if (first < 0) return first;
+  out_tokens[0] = first;
+  IE_CHECK_HIP(hipMemcpyAsync(tokenid_buff + prompt_len, output_token, sizeof(int),
+                              hipMemcpyDeviceToDevice, c->stream));
+  auto t0 = std::chrono::steady_clock::now();
+  for (int i = 1; i < max_new_tokens; ++i) {
+    if (i == timed_from) {
+      IE_CHECK_HIP(hipStreamSynchronize(c->stream));
+      t0 = std::chrono::steady_clock::now();
+    }
+    const int tok = decode_step_impl(c, weights, prompt_len + i, tokenid_buff, data_buffer,
+                                     attn_buffer, output_distr, output_token, workspace, kv_cache,
+                                     true);
+    if (tok < 0) return tok;
+    out_tokens[i] = tok;
+  }
+  if (timed_ms) {
+    const auto t1 = std::chrono::steady_clock::now();
+    *timed_ms = timed_from < max_new_tokens
+                    ? std::chrono::duration<double, std::milli>(t1 - t0).count()
+                    : 0.0;
+  }
+  return max_new_tokens;
 }
 
 // ---------------------------------------------------------------- prefill

@@ -224,7 +224,9 @@ struct Context {
   unsigned long long* d_slots = nullptr;    // 64-bit reduction slots (argmax)
   int* d_params = nullptr;                  // device copy of per-step scalars
   int* h_params = nullptr;                  // pinned staging for d_params
-  int* h_token = nullptr;                   // pinned token read-back
+  int* h_token = nullptr;                   // pinned, mapped token read-back
+  int* h_token_dev = nullptr;               // device address of h_token (the argmax writes it)
+  int next_seq = -1;                        // d_params[0] as the last decode step left it
   bool use_graph = true;
   // captured decode-step graph and the arguments it was captured with
   hipGraphExec_t graph_exec = nullptr;

@@ -95,8 +95,17 @@ int launch_qkv_rope_scatter(int S, int start_pos, const uint16_t* qkv, const flo
                             hipStream_t st);
 
 // ------------------------------------------------------------ sampling
+// Row 0 extras of the argmax: host_tok (mapped pinned memory) receives the token with a
+// system-scope store, and when seq is set, tok_buf[*seq] = token and *seq += 1 (the decode step's
+// token write-back and position advance).  All optional.
+struct ArgmaxTail {
+  int* host_tok = nullptr;
+  int* tok_buf = nullptr;
+  int* seq = nullptr;
+};
 int launch_argmax_rows(int rows, int vocab, const float* logits, int* out,
-                       unsigned long long* slots, unsigned int* counters, hipStream_t st);
+                       unsigned long long* slots, unsigned int* counters, hipStream_t st,
+                       ArgmaxTail tail = ArgmaxTail{});
 int launch_top_p(int rows, int vocab, const float* logits, float temperature, float top_p,
                  uint64_t seed, uint64_t step, int* out, float* ws, hipStream_t st);
 

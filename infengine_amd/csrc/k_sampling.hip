@@ -50,7 +50,7 @@ constexpr int kArgmaxBlocks = 64;
 
 __global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int vocab, int* out,
                                                      unsigned long long* slots,
-                                                     unsigned int* counters) {
+                                                     unsigned int* counters, ArgmaxTail tail) {
   __shared__ unsigned long long red[4];
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* L = logits + (size_t)row * vocab;
@@ -68,13 +68,25 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int vo
   if (tid == 0) {
     unsigned long long b = red[0];
     for (int w = 1; w < 4; ++w) b = red[w] > b ? red[w] : b;
+    // Device-scope atomics on one address are coherent across the XCDs; waiting for the max
+    // to be performed before counting in orders the two, so the workgroup that counts last
+    // exchanges out the final max.  (No __threadfence: on this part it writes back the L2.)
     atomicMax(&slots[row], b);
-    __threadfence();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (atomicAdd(&counters[row], 1u) == gridDim.x - 1) {
-      __threadfence();
       const unsigned long long fin = atomicExch(&slots[row], 0ull);
-      out[row] = (int)(0xFFFFFFFFu - (unsigned)(fin & 0xFFFFFFFFull));
+      const int tok = (int)(0xFFFFFFFFu - (unsigned)(fin & 0xFFFFFFFFull));
+      out[row] = tok;
       atomicExch(&counters[row], 0u);
+      if (row == 0) {
+        if (tail.host_tok)
+          __hip_atomic_store(tail.host_tok, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (tail.seq) {
+          const int s = *tail.seq;
+          if (tail.tok_buf) tail.tok_buf[s] = tok;
+          *tail.seq = s + 1;
+        }
+      }
     }
   }
 }
@@ -241,14 +253,15 @@ __global__ __launch_bounds__(kTopPThreads) void top_p_kernel(const float* logits
 }  // namespace
 
 int launch_argmax_rows(int rows, int vocab, const float* logits, int* out,
-                       unsigned long long* slots, unsigned int* counters, hipStream_t st) {
+                       unsigned long long* slots, unsigned int* counters, hipStream_t st,
+                       ArgmaxTail tail) {
   IE_REQUIRE(rows >= 1 && rows <= kNumSlots, "argmax: rows=%d out of range [1,%d]", rows,
              kNumSlots);
   IE_REQUIRE(vocab >= 1, "argmax: vocab=%d", vocab);
   int blocks = kArgmaxBlocks;
   if (vocab < blocks * 256) blocks = (vocab + 255) / 256;
   hipLaunchKernelGGL(argmax_kernel, dim3(blocks, rows), dim3(256), 0, st, logits, vocab, out,
-                     slots, counters);
+                     slots, counters, tail);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }

@@ -245,3 +245,40 @@ def test_batched_decode_matches_single(hip, model, noise_floor):
                      what=f"batched row {b}")
         assert list(th)[b] == int(out[b].item()) == int(np.argmax(host(logits[b])))
     c.close()
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_generate_equals_manual_loop(hip, model, graph):
+    """ie_generate (the Manager loop in the library, token write-back fused into the argmax)
+    is bitwise identical to the reference loop driven from the host: ie_prefill, then
+    ie_decode_step with a device-to-device write-back after each token (manager.cpp:70-86).
+    Also covers the skipped position upload (the argmax advances it) and a decode step whose
+    position does not follow the previous one."""
+    from infengine_amd.engine import Context, Request
+    S, N = 24, 6
+    say(f"generate prompt={S} new={N} graph={graph} vs manual decode loop")
+    rng = np.random.default_rng(77)
+    ids = rng.integers(0, 128256, S).astype(np.int32)
+    c = Context(0, graph=graph)
+    a = Request(c, model, max_seq_len=S + N + 8)
+    a.tokens[:S] = torch.from_numpy(ids).cuda()
+    want = [a.prefill(S)]
+    a.tokens[S] = a.token[0]
+    for i in range(1, N):
+        t = a.decode_step(S + i)
+        a.tokens[S + i] = a.token[0]
+        want.append(t)
+    kv_want = host(a.kv.view(torch.int16).view(32, 2, 8, 8192, 128)[:, :, :, :S + N]).copy()
+    logits_want = host(a.logits).copy()
+    b = Request(c, model, max_seq_len=S + N + 8)
+    got, ms = b.generate(ids, N, timed_from=2)
+    assert got == want
+    assert ms is not None and ms > 0
+    assert host(b.tokens[:S + N]).tolist() == ids.tolist() + want[:N]
+    assert np.array_equal(host(b.kv.view(torch.int16).view(32, 2, 8, 8192, 128)[:, :, :, :S + N]),
+                          kv_want)
+    assert np.array_equal(host(b.logits), logits_want)
+    # a step at a position the previous step did not advance to still reads it (re-upload)
+    t_again = b.decode_step(S + N - 1)
+    assert t_again == want[N - 1]
+    c.close()
