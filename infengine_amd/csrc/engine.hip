@@ -376,7 +376,8 @@ namespace {
 // tokenid_buff[seq_len] on the device (manager.cpp:84).
 int decode_step_impl(Context* c, const ie_model_weights* weights, int seq_len, int* tokenid_buff,
                      ie_bf16* data_buffer, ie_bf16* attn_buffer, float* output_distr,
-                     int* output_token, void* workspace, void* kv_cache, bool wb) {
+                     int* output_token, void* workspace, void* kv_cache, bool wb,
+                     bool poll = false) {
   IE_REQUIRE(weights && weights_complete(*weights), "decode_step: incomplete weights");
   IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "decode_step: seq_len %d out of [1, %d]",
              seq_len, kMaxCtx);
@@ -392,6 +393,8 @@ int decode_step_impl(Context* c, const ie_model_weights* weights, int seq_len, i
     IE_CHECK_HIP(hipMemcpyAsync(c->d_params, c->h_params, sizeof(int), hipMemcpyHostToDevice, st));
   }
   int* wb_buf = wb ? tokenid_buff : nullptr;
+  volatile int* htok = static_cast<volatile int*>(c->h_token);
+  *htok = -1;  // token ids are >= 0: -1 = not yet written by this step's argmax
 
   if (c->use_graph) {
     const void* key[12] = {(const void*)weights, tokenid_buff, data_buffer, attn_buffer,
@@ -428,9 +431,22 @@ int decode_step_impl(Context* c, const ie_model_weights* weights, int seq_len, i
     IE_TRY(enqueue_decode(c, st, *weights, seq_len, tokenid_buff, data_buffer, attn_buffer,
                           output_distr, output_token, workspace, kv_cache, wb_buf));
   }
-  IE_CHECK_HIP(hipStreamSynchronize(st));
+  if (poll) {
+    // The argmax stores the token to mapped host memory as the step's last action; the next
+    // step is ordered after this one on the stream, so the caller of this loop only needs the
+    // token.  Bounded: past ~2 s fall back to a stream synchronisation.
+    const auto t0 = std::chrono::steady_clock::now();
+    while (*htok < 0) {
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2)) {
+        IE_CHECK_HIP(hipStreamSynchronize(st));
+        break;
+      }
+    }
+  } else {
+    IE_CHECK_HIP(hipStreamSynchronize(st));
+  }
   c->next_seq = seq_len + 1;
-  return *static_cast<volatile int*>(c->h_token);
+  return *htok;
 }
 
 }  // namespace
@@ -479,10 +495,11 @@ int ie_generate(ie_context* c, const ie_model_weights* weights, const int* promp
     }
     const int tok = decode_step_impl(c, weights, prompt_len + i, tokenid_buff, data_buffer,
                                      attn_buffer, output_distr, output_token, workspace, kv_cache,
-                                     true);
+                                     true, true);
     if (tok < 0) return tok;
     out_tokens[i] = tok;
   }
+  IE_CHECK_HIP(hipStreamSynchronize(c->stream));
   if (timed_ms) {
     const auto t1 = std::chrono::steady_clock::now();
     *timed_ms = timed_from < max_new_tokens
