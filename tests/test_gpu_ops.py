@@ -159,7 +159,8 @@ def test_lm_head_logits(hip, ctx):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 4096, 256), (16, 4096, 1024), (100, 4096, 512),
-                                   (256, 4096, 1024), (64, 14336, 4096), (300, 4096, 132)])
+                                   (256, 4096, 1024), (64, 14336, 4096), (300, 4096, 132),
+                                   (8, 14336, 512), (4, 1536, 200)])
 def test_gemm_mfma(hip, ctx, m, k, n):
     say(f"gemm_bf16 m={m} k={k} n={n}")
     x = orc.synthetic((m, k), 11, m, 0.0, 1.0)
