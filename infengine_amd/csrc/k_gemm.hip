@@ -25,6 +25,8 @@
 // residual_add.cu:17-19), and SwiGLU over a gate/up pair of weights in which the
 // 128 W rows of a tile are [32 gate | 32 up | 32 gate | 32 up] for 64 output
 // columns, so each lane holds gate and up for the same output element.
+#include <algorithm>
+
 #include "ie_kernels.h"
 
 namespace ie {
@@ -213,18 +215,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p, int m_tiles) {
 // step.  No other vector-memory instruction is issued inside the loop.
 namespace wide {
 
-constexpr int BN = 256;  // W rows per tile
-
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw 32-bit access)
 
-// Tile geometry: BN = 256 W rows x BM (128 or 256) X rows x BK (32 or 64) k, in a ring of
-// STAGES LDS stages.  Every wave owns 128 W rows x 64 X rows, so a workgroup has
-// NW = 2 * BM / 64 waves (4 or 8).
-template <int BM_, int BK_, int STAGES_>
+// Tile geometry: BN (256 or 192) W rows x BM (128 or 256) X rows x BK (32 or 64) k, in a
+// ring of STAGES LDS stages.  Every wave owns BN / 2 W rows x 64 X rows (NI = BN / 64 blocks
+// of 32 W rows), so a workgroup has NW = 2 * BM / 64 waves (4 or 8).
+template <int BM_, int BK_, int STAGES_, int BN_ = 256>
 struct Cfg {
+  static constexpr int BN = BN_;
+  static constexpr int WTN = BN / 2;                 // W rows per wave
+  static constexpr int NI = WTN / 32;                // 32-row MFMA blocks per wave
+  static constexpr int NT = 2 * NI;                  // MFMAs per k16 sub-step
   static constexpr int BM = BM_;
   static constexpr int BK = BK_;
   static constexpr int STAGES = STAGES_;
@@ -241,6 +245,7 @@ struct Cfg {
   static constexpr int LOADS = W_LOADS + X_LOADS;
   static constexpr int KSUB = BK / 16;               // MFMA k16 sub-steps per stage
   static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(BN == 256 || BN == 192, "BN");
   static_assert(STAGES * STAGE * 16 <= 160 * 1024, "LDS");
   // Chunk slot s of row r holds global chunk s ^ swz(r): the 16 (or 32) consecutive rows one
   // ds_read_b128 phase touches fall in distinct 16-byte bank groups (64- or 128-bank LDS).
@@ -251,7 +256,7 @@ struct Cfg {
 };
 
 // Buffer descriptor for the `rows` W rows starting at tile-local row r (all in one matrix).
-template <int EPI>
+template <int EPI, int BN>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t w_group(const GemmParams& p, int ntile, int r) {
   const uint16_t* base;
   long long rows;
@@ -309,8 +314,8 @@ __device__ __forceinline__ void issue_stage(u32x4_t* lds, const __amdgpu_buffer_
   for (int j = 0; j < C::LOADS; ++j) issue_load<C>(lds, rsrc, voff, wv, kt, stage, j);
 }
 
-// Operand fragment n (0..5) of a k16 sub-step, in the order the sub-step's MFMAs first use
-// them: X0 W0 X1 W1 W2 W3.  Lane l supplies tile row base + l%32 at k chunk ch (2*kk + l/32,
+// Operand fragment n (0..NI+1) of a k16 sub-step, in the order the sub-step's MFMAs first use
+// them: X0 W0 X1 W1 W2 (W3).  Lane l supplies tile row base + l%32 at k chunk ch (2*kk + l/32,
 // swizzled).
 template <class C>
 __device__ __forceinline__ void read_frag(const u32x4_t* src, int a_row, int b_row, int ch, int n,
@@ -375,7 +380,7 @@ __device__ __forceinline__ void tile_of(int b, int nb, int m_tiles, int& mtile, 
 // kt+1 and reads its first fragments, so no k-step starts on an LDS latency; with ISSUE it also
 // refills slot kt % STAGES with stage kt+STAGES, one or two loads after each MFMA.
 template <class C, bool ISSUE>
-__device__ __forceinline__ void k_step(f32x16_t (&acc)[4][2], bf16x8_t (&af)[2][4],
+__device__ __forceinline__ void k_step(f32x16_t (&acc)[C::NI][2], bf16x8_t (&af)[2][C::NI],
                                        bf16x8_t (&bfr)[2][2], u32x4_t* lds,
                                        const __amdgpu_buffer_rsrc_t* rsrc, const uint32_t* voff,
                                        int wv, int a_row, int b_row, int fh, int fs, int kt,
@@ -394,14 +399,14 @@ __device__ __forceinline__ void k_step(f32x16_t (&acc)[4][2], bf16x8_t (&af)[2][
     const int ch = (2 * (last ? 0 : kk + 1) + fh) ^ fs;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < C::NT; ++t) {
       acc[t / 2][t % 2] =
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][t / 2], bfr[cur][t % 2], acc[t / 2][t % 2], 0, 0, 0);
-      if (rd && t < 6) read_frag<C>(src, a_row, b_row, ch, t, af[cur ^ 1], bfr[cur ^ 1]);
+      if (rd && t < C::NI + 2) read_frag<C>(src, a_row, b_row, ch, t, af[cur ^ 1], bfr[cur ^ 1]);
       if (ISSUE && last) {
 #pragma unroll
         for (int j = 0; j < C::LOADS; ++j)
-          if (j * 8 / C::LOADS == t)
+          if (j * C::NT / C::LOADS == t)
             issue_load<C>(lds, rsrc, voff, wv, kt + C::STAGES, kt % C::STAGES, j);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -409,10 +414,23 @@ __device__ __forceinline__ void k_step(f32x16_t (&acc)[4][2], bf16x8_t (&af)[2][
   }
 }
 
-template <int EPI, int BM, int BK, int STAGES, int MAPG>
+// Output-tile swizzle: 8-byte unit u of row r (of `upr` units) sits at slot swz_out(u, r).  The
+// 32 rows one write instruction touches land in distinct 8-byte bank pairs: within a 32-unit
+// group u ^ (r % 32) is a permutation of the rows; in the 16-unit tail of a 48-unit row the rows'
+// alternating 16-unit offset (48 r mod 32) supplies the fifth bit.
+template <int UPR>
+__device__ __forceinline__ int swz_out(int u, int r) {
+  if constexpr (UPR == 48) {
+    if (u >= 32) return 32 + ((u - 32) ^ ((r & 14) | ((r >> 4) & 1)));
+  }
+  return u ^ (r & 31);
+}
+
+template <int EPI, int BM, int BK, int STAGES, int MAPG, int BN>
 __global__ __launch_bounds__(BM * 2) __attribute__((amdgpu_waves_per_eu(BM / 128, BM / 128)))
 void gemm_wide_kernel(GemmParams p, int m_tiles) {
-  using C = Cfg<BM, BK, STAGES>;
+  using C = Cfg<BM, BK, STAGES, BN>;
+  static_assert(EPI != kGemmSwiglu || BN == 256, "SwiGLU tiles are 256 W rows");
   __shared__ u32x4_t lds[STAGES * C::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -430,13 +448,13 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
   for (int j = 0; j < C::LOADS; ++j) {
     const bool is_w = j < C::W_LOADS;
     const int g = wv + C::NW * (is_w ? j : j - C::W_LOADS);
-    rsrc[j] = is_w ? w_group<EPI>(p, ntile, g * C::RPL) : x_group(p, m0, g * C::RPL);
+    rsrc[j] = is_w ? w_group<EPI, C::BN>(p, ntile, g * C::RPL) : x_group(p, m0, g * C::RPL);
     const int rl = lane / C::CPR, c = (lane % C::CPR) ^ C::swz(g * C::RPL + rl);
     voff[j] = (uint32_t)((rl * p.K + c * 8) * 2);
   }
-  f32x16_t acc[4][2];
+  f32x16_t acc[C::NI][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < C::NI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -444,7 +462,7 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
 
   // fragment addressing: operand lane l supplies tile row base + l%32, k chunk 2*kk + l/32
   const int fr = lane & 31, fh = lane >> 5, fs = C::swz(fr);
-  const int a_row = (wn * 128 + fr) * C::CPR;
+  const int a_row = (wn * C::WTN + fr) * C::CPR;
   const int b_row = C::W_CHUNKS + (wm * 64 + fr) * C::CPR;
 
   // The epilogue's kernel arguments are pulled into SGPRs here: a scalar load still in
@@ -460,9 +478,9 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
   // stage 0 landed; stage STAGES-1 goes to the last ring slot, which no wave reads yet
   wait_stage_n<C::LOADS, STAGES - 2>(min(STAGES - 2, KT - 1));
   if (STAGES - 1 < KT) issue_stage<C>(lds, rsrc, voff, wv, STAGES - 1, STAGES - 1);
-  bf16x8_t af[2][4], bfr[2][2];
+  bf16x8_t af[2][C::NI], bfr[2][2];
 #pragma unroll
-  for (int n = 0; n < 6; ++n) read_frag<C>(lds, a_row, b_row, fh ^ fs, n, af[0], bfr[0]);
+  for (int n = 0; n < C::NI + 2; ++n) read_frag<C>(lds, a_row, b_row, fh ^ fs, n, af[0], bfr[0]);
   int kt = 0;
   for (; kt + STAGES < KT; ++kt)
     k_step<C, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
@@ -470,17 +488,17 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
     k_step<C, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
 
   // ---- epilogue: accumulator element 4*g + q of tile (i, j) is
-  //      W row wn*128 + 32*i + 8*g + 4*(lane/32) + q,  X row m0 + wm*64 + 32*j + lane%32
+  //      W row wn*WTN + 32*i + 8*g + 4*(lane/32) + q,  X row m0 + wm*64 + 32*j + lane%32
   if constexpr (EPI == kGemmF32) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int m = m0 + wm * 64 + j * 32 + fr;
       if (m >= p.M) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < C::NI; ++i)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = ntile * BN + wn * 128 + i * 32 + 8 * g + 4 * fh;
+          const int n = ntile * BN + wn * C::WTN + i * 32 + 8 * g + 4 * fh;
           if (n < p.N)
             *reinterpret_cast<float4*>(yf + (size_t)m * p.ldy + n) =
                 make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
@@ -490,7 +508,7 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
     // bf16 results go through LDS so that the global stores are whole, coalesced row segments
     // (a lane's accumulators are 4 columns of 32 different rows; storing them directly writes
     // every 128-byte line in eight 16-byte pieces).  The tile is [BM][OUTN] bf16 held as
-    // 8-byte units; unit u of row r sits at u ^ (r % 32), which spreads the 32 rows one
+    // 8-byte units; unit u of row r sits at swz_out(u, r), which spreads the 32 rows one
     // write instruction touches over distinct banks without padding.
     constexpr int OUTN = (EPI == kGemmSwiglu) ? 128 : BN;  // output columns per tile
     constexpr int UPR = OUTN / 4;                            // 8-byte units per row
@@ -500,7 +518,6 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = wm * 64 + j * 32 + fr;
-      const int sw = r & 31;
       if constexpr (EPI == kGemmSwiglu) {
 #pragma unroll
         for (int i = 0; i < 4; i += 2)
@@ -519,15 +536,15 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
               o[q] = pack_bf2(v[0], v[1]);
             }
             const int u = (2 * wn + i / 2) * 8 + 2 * g + fh;
-            ot[r * UPR + (u ^ sw)] = make_uint2(o[0], o[1]);
+            ot[r * UPR + swz_out<UPR>(u, r)] = make_uint2(o[0], o[1]);
           }
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < C::NI; ++i)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const int u = wn * 32 + i * 8 + 2 * g + fh;
-            ot[r * UPR + (u ^ sw)] = make_uint2(pack_bf2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+            const int u = wn * (C::WTN / 4) + i * 8 + 2 * g + fh;
+            ot[r * UPR + swz_out<UPR>(u, r)] = make_uint2(pack_bf2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
                                                 pack_bf2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]));
           }
       }
@@ -541,8 +558,7 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
       const int r = P / (UPR / 2), c2 = P % (UPR / 2);
       const int m = m0 + r, n = n_base + 8 * c2;
       if (m >= p.M || n >= p.N) continue;
-      const int sw = r & 31;
-      const uint2 lo = ot[r * UPR + ((2 * c2) ^ sw)], hi = ot[r * UPR + ((2 * c2 + 1) ^ sw)];
+      const uint2 lo = ot[r * UPR + swz_out<UPR>(2 * c2, r)], hi = ot[r * UPR + swz_out<UPR>(2 * c2 + 1, r)];
       uint16_t* dst = y + (size_t)m * p.ldy + n;
       if constexpr (EPI == kGemmResid) {
         // y = bf16(y + bf16(acc)) (residual_add.cu:17-19); the LDS tile holds bf16(acc)
@@ -567,13 +583,13 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
 
 }  // namespace wide
 
-template <int EPI, int BM = 128, int BK = 64, int STAGES = 3, int MAPG = 1>
+template <int EPI, int BM = 128, int BK = 64, int STAGES = 3, int MAPG = 1, int WBN = 256>
 int launch_wide(const GemmParams& p, hipStream_t st) {
   const int m_tiles = (p.M + BM - 1) / BM;
-  const int n_tiles = (EPI == kGemmSwiglu) ? (p.N + 127) / 128 : (p.N + wide::BN - 1) / wide::BN;
+  const int n_tiles = (EPI == kGemmSwiglu) ? (p.N + 127) / 128 : (p.N + WBN - 1) / WBN;
   const long long blocks = (long long)m_tiles * n_tiles;
   IE_REQUIRE(blocks <= 0x7fffffff, "gemm: too many tiles");
-  hipLaunchKernelGGL((wide::gemm_wide_kernel<EPI, BM, BK, STAGES, MAPG>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((wide::gemm_wide_kernel<EPI, BM, BK, STAGES, MAPG, WBN>), dim3((unsigned)blocks),
                      dim3(BM * 2), 0, st, p, m_tiles);
   IE_CHECK_LAUNCH();
   return IE_OK;
@@ -590,6 +606,128 @@ int launch_e(const GemmParams& p, hipStream_t st) {
   return IE_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Tile shape by a cost model: time = rounds of workgroups over the 256 CUs x the time of one
+// tile at the measured per-CU rate of that shape (256x256 and 192x256: 1085, 256x128: 900,
+// 128x128: 750 TFLOP/s over the chip at full occupancy).  Big tiles win when they fill the
+// chip; at small S the 128 x 128 tile keeps more CUs busy.  192 W rows x 256 X rows gives
+// exactly 256 tiles for the QKV projection at S = 2048 (N = 6144).
+enum { kTileSmall, kTileWide, kTileBig, kTileBig192, kTileKinds };
+
+struct TileKind {
+  int tm, tn, tn_swiglu;  // X rows, output columns (plain / SwiGLU) per tile
+  double unit;            // relative time of one tile
+};
+constexpr TileKind kTiles[kTileKinds] = {
+    {128, 128, 64, 128.0 * 128 / 750.0},
+    {128, 256, 128, 256.0 * 128 / 900.0},
+    {256, 256, 128, 256.0 * 256 / 1085.0},
+    {256, 192, 0, 192.0 * 256 / 1085.0},
+};
+
+bool tile_ok(int kind, int epi, const GemmParams& p) {
+  if (kind == kTileSmall) return true;
+  if (p.M < kWideMinRows) return false;
+  if (kind == kTileWide) return true;
+  if (epi == kGemmF32) return false;
+  return kind == kTileBig || epi != kGemmSwiglu;
+}
+
+long long tile_count(int kind, int epi, int M, int N) {
+  const TileKind& t = kTiles[kind];
+  const int tn = epi == kGemmSwiglu ? t.tn_swiglu : t.tn;
+  return (long long)((M + t.tm - 1) / t.tm) * ((N + tn - 1) / tn);
+}
+
+double tile_cost(int kind, int epi, int M, int N) {
+  return (double)((tile_count(kind, epi, M, N) + 255) / 256) * kTiles[kind].unit;
+}
+
+int launch_kind(int kind, int epi, const GemmParams& p, hipStream_t st) {
+  switch (kind * 4 + epi) {
+    case kTileSmall * 4 + kGemmBf16: return launch_e<kGemmBf16>(p, st);
+    case kTileSmall * 4 + kGemmResid: return launch_e<kGemmResid>(p, st);
+    case kTileSmall * 4 + kGemmF32: return launch_e<kGemmF32>(p, st);
+    case kTileSmall * 4 + kGemmSwiglu: return launch_e<kGemmSwiglu>(p, st);
+    case kTileWide * 4 + kGemmBf16: return launch_wide<kGemmBf16>(p, st);
+    case kTileWide * 4 + kGemmResid: return launch_wide<kGemmResid>(p, st);
+    case kTileWide * 4 + kGemmF32: return launch_wide<kGemmF32>(p, st);
+    case kTileWide * 4 + kGemmSwiglu: return launch_wide<kGemmSwiglu>(p, st);
+    case kTileBig * 4 + kGemmBf16: return launch_wide<kGemmBf16, 256, 64, 2>(p, st);
+    case kTileBig * 4 + kGemmResid: return launch_wide<kGemmResid, 256, 64, 2>(p, st);
+    case kTileBig * 4 + kGemmSwiglu: return launch_wide<kGemmSwiglu, 256, 64, 2>(p, st);
+    case kTileBig192 * 4 + kGemmBf16: return launch_wide<kGemmBf16, 256, 64, 2, 1, 192>(p, st);
+    case kTileBig192 * 4 + kGemmResid: return launch_wide<kGemmResid, 256, 64, 2, 1, 192>(p, st);
+  }
+  set_error("gemm: bad epilogue %d", epi);
+  return IE_ERR_INVALID_ARG;
+}
+
+// Output columns [c, N) of p as a GEMM of its own (c a multiple of 64, and of 16 past a
+// weight split point).
+GemmParams column_tail(int epi, const GemmParams& p, int c) {
+  GemmParams q = p;
+  const size_t off = (size_t)c * p.K;
+  q.N = p.N - c;
+  if (p.y) q.y = p.y + c;
+  if (p.yf) q.yf = p.yf + c;
+  if (epi == kGemmSwiglu) {
+    q.w0 = p.w0 + off;
+    q.w1 = p.w1 + off;
+    return q;
+  }
+  const int e0 = std::min(p.n0, p.N), e1 = std::min(p.n0 + p.n1, p.N);
+  if (c < e0) {
+    q.w0 = p.w0 + off;
+    q.n0 = e0 - c;
+  } else if (c < e1) {
+    q.w0 = p.w1 + (size_t)(c - e0) * p.K;
+    q.n0 = e1 - c;
+    q.w1 = p.w2;
+    q.n1 = q.N - q.n0;
+  } else {
+    q.w0 = p.w2 + (size_t)(c - e1) * p.K;
+    q.n0 = q.N;
+    q.n1 = 0;
+  }
+  return q;
+}
+
+// Cheapest tile shape; with `split`, a partial last round of that shape may instead be run as
+// a second launch over the remaining output columns with the shape that fills the chip for
+// them (gate/up at S = 2048: 3 rounds of 256 x 256 tiles, then the last 2048 columns as one
+// round of 256 x 128 tiles, in place of a half-empty fourth round).
+int launch_tiled(int epi, const GemmParams& p, hipStream_t st, bool split) {
+  int best = kTileSmall;
+  double best_cost = tile_cost(kTileSmall, epi, p.M, p.N);
+  for (int k = kTileWide; k < kTileKinds; ++k) {
+    if (!tile_ok(k, epi, p)) continue;
+    const double c = tile_cost(k, epi, p.M, p.N);
+    if (c < best_cost) best = k, best_cost = c;
+  }
+  if (split) {
+    const TileKind& t = kTiles[best];
+    const int tn = epi == kGemmSwiglu ? t.tn_swiglu : t.tn;
+    const int m_tiles = (p.M + t.tm - 1) / t.tm;
+    const long long tiles = tile_count(best, epi, p.M, p.N);
+    if (tiles > 256 && tiles % 256 != 0 && 256 % m_tiles == 0) {
+      const int c = (int)(tiles / 256 * 256 / m_tiles) * tn;  // columns of the full rounds
+      const GemmParams tail = column_tail(epi, p, c);
+      double tail_cost = 1e30;
+      for (int k = kTileSmall; k < kTileKinds; ++k)
+        if (tile_ok(k, epi, tail)) tail_cost = std::min(tail_cost, tile_cost(k, epi, tail.M, tail.N));
+      if ((double)(tiles / 256) * t.unit + tail_cost < best_cost) {
+        GemmParams head = p;
+        head.N = c;
+        const int rc = launch_kind(best, epi, head, st);
+        if (rc != IE_OK) return rc;
+        return launch_tiled(epi, tail, st, false);
+      }
+    }
+  }
+  return launch_kind(best, epi, p, st);
+}
+
 }  // namespace
 
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
@@ -603,42 +741,7 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
              "gemm: weight split points n0=%d n0+n1=%d inside N=%d must be multiples of 16", p.n0,
              p.n0 + p.n1, p.N);
   if (gemm_skinny_fits(p)) return launch_gemm_skinny(epi, p, st);
-  // Tile shape by a cost model: time = rounds of workgroups over the 256 CUs x the time of one
-  // tile at the measured per-CU rate of that shape (256x256: 1085, 256x128: 900,
-  // 128x128: 750 TFLOP/s over the chip at full occupancy).  Big tiles win when they fill the
-  // chip (QKV, gate/up at S = 2048); at small S the 128 x 128 tile keeps more CUs busy.
-  const bool swiglu = epi == kGemmSwiglu;
-  auto cost = [&](int tm, int tn_out, double us_per_tile) {
-    const long long tiles = (long long)((p.M + tm - 1) / tm) * ((p.N + tn_out - 1) / tn_out);
-    return (double)((tiles + 255) / 256) * us_per_tile;
-  };
-  const double c_small = cost(128, swiglu ? 64 : 128, 128.0 * 128 / 750.0);
-  const double c_wide = p.M >= kWideMinRows ? cost(128, swiglu ? 128 : 256, 256.0 * 128 / 900.0) : 1e30;
-  const double c_big = (p.M >= kWideMinRows && epi != kGemmF32)
-                           ? cost(256, swiglu ? 128 : 256, 256.0 * 256 / 1085.0) : 1e30;
-  if (c_big < c_wide && c_big < c_small) {
-    switch (epi) {
-      case kGemmBf16: return launch_wide<kGemmBf16, 256, 64, 2>(p, st);
-      case kGemmResid: return launch_wide<kGemmResid, 256, 64, 2>(p, st);
-      case kGemmSwiglu: return launch_wide<kGemmSwiglu, 256, 64, 2>(p, st);
-    }
-  } else if (c_wide < c_small) {
-    switch (epi) {
-      case kGemmBf16: return launch_wide<kGemmBf16>(p, st);
-      case kGemmResid: return launch_wide<kGemmResid>(p, st);
-      case kGemmF32: return launch_wide<kGemmF32>(p, st);
-      case kGemmSwiglu: return launch_wide<kGemmSwiglu>(p, st);
-    }
-  } else {
-    switch (epi) {
-      case kGemmBf16: return launch_e<kGemmBf16>(p, st);
-      case kGemmResid: return launch_e<kGemmResid>(p, st);
-      case kGemmF32: return launch_e<kGemmF32>(p, st);
-      case kGemmSwiglu: return launch_e<kGemmSwiglu>(p, st);
-    }
-  }
-  set_error("gemm: bad epilogue %d", epi);
-  return IE_ERR_INVALID_ARG;
+  return launch_tiled(epi, p, st, true);
 }
 
 }  // namespace ie

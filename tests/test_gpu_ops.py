@@ -192,12 +192,16 @@ GEMM_EPI = {"bf16": 0, "resid": 1, "f32": 2, "swiglu": 3}
 
 
 @pytest.mark.parametrize("epi", list(GEMM_EPI))
-@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (300, 1000), (2048, 6144), (2048, 4096)])
+@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (300, 1000), (2048, 6144), (2048, 4096),
+                                 (2048, 14336)])
 def test_gemm_epilogues(hip, ctx, epi, m, n):
     """Every fused epilogue of the MFMA GEMM on each kernel the launcher picks: the skinny
-    streaming kernel (m <= 16, ragged n), 128 x 128 tiles (m = 300), and the prefill sizes
-    that select 256 x 256 tiles (bf16 / resid at n = 6144, SwiGLU at n = 4096) and 256 x 128
-    tiles (the others); sampled rows at m = 2048."""
+    streaming kernel (m <= 16, ragged n), 128 x 128 tiles (m = 300), and the prefill sizes:
+    192 x 256 tiles (bf16 / resid at n = 6144), 256 x 256 tiles (SwiGLU at n = 4096), 256 x 128
+    tiles (the others at n = 4096 and 6144), and at n = 14336 a launch split by output columns
+    (full rounds of the big tile, then the remaining columns with another shape: SwiGLU 256 x 256
+    then 256 x 128, bf16 / resid 256 x 256 then 192 x 256, fp32 256 x 128 then 128 x 128);
+    sampled rows at m = 2048."""
     k = 4096
     say(f"gemm_ex {epi} m={m} k={k} n={n}")
     x = orc.synthetic((m, k), 21, m, 0.0, 1.0)
@@ -342,6 +346,39 @@ def test_attn_prefill_op(hip, ctx, rope):
     got_kv = host(kv.view(32, 2, 8, 8192, 128)[layer])
     assert_bf16_close(got_kv[:, :, :S], planes[:, :, :S], what="kv rows", outlier_frac=1e-3)
     assert not got_kv[:, :, S:].any()
+
+
+def test_attn_prefill_op_2048(hip, ctx, rope):
+    """The attention op at S = 2048: the QKV projection runs as one GEMM over the three
+    concatenated weights on 192 x 256 tiles, two of which straddle the Q|K and K|V split points.
+    Every K and V cache row is checked, and the output at sampled query rows."""
+    cos, sin, dcos, dsin = rope
+    S, layer = 2048, 1
+    say(f"attn (prefill) seq_len={S}")
+    w, dw = _attn_weights(17)
+    x = orc.synthetic((S, H), 17, 700, 0.0, 1.0)
+    kv = torch.zeros(hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+    out = bf16_empty(S, H)
+    ws = torch.zeros(hip.lib.ie_attn_workspace_size(S), dtype=torch.uint8, device="cuda")
+    hip.check(hip.lib.ie_attn(ctx.handle, P(dcos), P(dsin), S, P(dev(x)), P(dw["w_q"]),
+                              P(dw["w_k"]), P(dw["w_v"]), P(dw["w_o"]), P(out), P(ws), P(kv),
+                              layer))
+    sync()
+    k = orc.matmul(x, w["w_k"])
+    v = orc.matmul(x, w["w_v"])
+    kh = np.ascontiguousarray(k.reshape(S, 8, 128).transpose(1, 0, 2))    # [head][t][128]
+    planes = np.zeros((2, 8, 8192, 128), np.uint16)
+    planes[0, :, :S] = orc.apply_rope(kh, 0, 8, S, S, cos, sin).reshape(8, S, 128)
+    planes[1, :, :S] = v.reshape(S, 8, 128).transpose(1, 0, 2)
+    got_kv = host(kv.view(32, 2, 8, 8192, 128)[layer])
+    assert_bf16_close(got_kv[:, :, :S], planes[:, :, :S], what="kv rows", outlier_frac=1e-3)
+    assert not got_kv[:, :, S:].any()
+    got = host(out)
+    for t in (0, 1, 767, 1500, 2047):
+        q = orc.apply_rope(orc.matmul(x[t:t + 1], w["w_q"]), t, 32, 1, 1, cos, sin)
+        a = orc.attention(q, planes[0], planes[1], t, 8192)
+        want = orc.matmul(a, w["w_o"])
+        assert_close(orc.bf16_to_f32(got[t:t + 1]), orc.bf16_to_f32(want), what=f"attn row {t}")
 
 
 @pytest.fixture(scope="module")
