@@ -244,6 +244,9 @@ struct Cfg {
   static constexpr int X_LOADS = X_CHUNKS / THREADS;
   static constexpr int LOADS = W_LOADS + X_LOADS;
   static constexpr int KSUB = BK / 16;               // MFMA k16 sub-steps per stage
+  // With a ring of 3 or more stages a stage's loads are spread over four sub-steps (the last of
+  // k-step kt and the first KSUB-1 of k-step kt+1) instead of all issued in one.
+  static constexpr bool SPREAD = STAGES >= 3;
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(BN == 256 || BN == 192, "BN");
   static_assert(STAGES * STAGE * 16 <= 160 * 1024, "LDS");
@@ -377,9 +380,13 @@ __device__ __forceinline__ void tile_of(int b, int nb, int m_tiles, int& mtile, 
 // fragments of the next sub-step are read one after each MFMA of the current one, so that their
 // issue hides under the MFMAs (the scheduling fences keep this order: left alone the scheduler
 // groups the reads and moves each just before its use).  The last sub-step waits for stage
-// kt+1 and reads its first fragments, so no k-step starts on an LDS latency; with ISSUE it also
-// refills slot kt % STAGES with stage kt+STAGES, one or two loads after each MFMA.
-template <class C, bool ISSUE>
+// kt+1 and reads its first fragments, so no k-step starts on an LDS latency.
+// Loads: with NEW the last sub-step refills slot kt % STAGES (free once every wave has passed
+// that sub-step's barrier) with stage kt+STAGES -- all of it, or with SPREAD its first share;
+// with REST (SPREAD) sub-step kk < KSUB-1 issues share kk+1 of stage kt-1+STAGES.  Loads are
+// issued in stage order either way, so the wait for stage kt+1 allows exactly the younger
+// stages issued so far: min(STAGES-2, KT-2-kt) of them.
+template <class C, bool NEW, bool REST>
 __device__ __forceinline__ void k_step(f32x16_t (&acc)[C::NI][2], bf16x8_t (&af)[2][C::NI],
                                        bf16x8_t (&bfr)[2][2], u32x4_t* lds,
                                        const __amdgpu_buffer_rsrc_t* rsrc, const uint32_t* voff,
@@ -391,23 +398,31 @@ __device__ __forceinline__ void k_step(f32x16_t (&acc)[C::NI][2], bf16x8_t (&af)
   for (int kk = 0; kk < C::KSUB; ++kk) {
     const int cur = kk & 1;
     const bool last = kk + 1 == C::KSUB;
-    const bool rd = !last || ISSUE || kt + 1 < KT;
+    const bool rd = !last || kt + 1 < KT;
     // stage kt+1 must have landed; the younger stages issued so far may stay in flight
     if (last && rd)
-      wait_stage_n<C::LOADS, C::STAGES - 2>(ISSUE ? C::STAGES - 2 : min(C::STAGES - 2, KT - 2 - kt));
+      wait_stage_n<C::LOADS, C::STAGES - 2>(NEW ? C::STAGES - 2 : min(C::STAGES - 2, KT - 2 - kt));
     const u32x4_t* src = last ? nst : st;
     const int ch = (2 * (last ? 0 : kk + 1) + fh) ^ fs;
+    // loads of this sub-step: share `sh` of stage `ls` into ring slot `slot`
+    const bool issue = last ? NEW : (C::SPREAD && REST);
+    const int sh = !C::SPREAD ? 0 : last ? 0 : kk + 1;
+    const int ls = last ? kt + C::STAGES : kt - 1 + C::STAGES;
+    const int slot = ls % C::STAGES;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < C::NT; ++t) {
       acc[t / 2][t % 2] =
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][t / 2], bfr[cur][t % 2], acc[t / 2][t % 2], 0, 0, 0);
       if (rd && t < C::NI + 2) read_frag<C>(src, a_row, b_row, ch, t, af[cur ^ 1], bfr[cur ^ 1]);
-      if (ISSUE && last) {
+      if (issue) {
+        constexpr int SHARES = C::SPREAD ? C::KSUB : 1;
+        constexpr int PER = (C::LOADS + SHARES - 1) / SHARES;  // loads per share (last may be short)
 #pragma unroll
-        for (int j = 0; j < C::LOADS; ++j)
-          if (j * C::NT / C::LOADS == t)
-            issue_load<C>(lds, rsrc, voff, wv, kt + C::STAGES, kt % C::STAGES, j);
+        for (int i = 0; i < PER; ++i) {
+          const int j = sh * PER + i;
+          if (j < C::LOADS && i * C::NT / PER == t) issue_load<C>(lds, rsrc, voff, wv, ls, slot, j);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -482,10 +497,19 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
 #pragma unroll
   for (int n = 0; n < C::NI + 2; ++n) read_frag<C>(lds, a_row, b_row, fh ^ fs, n, af[0], bfr[0]);
   int kt = 0;
+  // stage STAGES-1 was issued whole above, so k-step 0 issues no remaining shares
+  if (STAGES < KT) {
+    k_step<C, true, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+    ++kt;
+  }
   for (; kt + STAGES < KT; ++kt)
-    k_step<C, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+    k_step<C, true, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+  if (C::SPREAD && kt >= 1 && kt < KT) {  // the shares of stage KT-1 still to issue
+    k_step<C, false, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+    ++kt;
+  }
   for (; kt < KT; ++kt)
-    k_step<C, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+    k_step<C, false, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
 
   // ---- epilogue: accumulator element 4*g + q of tile (i, j) is
   //      W row wn*WTN + 32*i + 8*g + 4*(lane/32) + q,  X row m0 + wm*64 + 32*j + lane%32
