@@ -192,9 +192,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p, int m_tiles) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide-tile kernel for M >= 128 (prefill): 256 W rows x 128 X rows x 64 k per
-// workgroup of 4 waves; each wave owns 128 W rows x 64 X rows as 4 x 2 tiles of
-// v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators per lane).
+// Wide-tile kernel for M >= 128 (prefill): 256 (or 192) W rows x 128 (or 256) X rows x 64 k
+// per workgroup; each wave owns 128 (96) W rows x 64 X rows as 4 (3) x 2 tiles of
+// v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators per lane).  The 256 x 128 tile runs 8 waves
+// as two k-groups (each takes two of a k-step's four k16 sub-steps for the whole tile, and the
+// groups' sums are added through LDS at the end): two waves per SIMD where one tile's worth
+// of 128 x 64 blocks would leave one.
 //
 // Operands reach LDS by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds:
 // lane i of a wave writes 16 bytes at LDS base + 16 i), through a 3-stage ring
@@ -223,7 +226,7 @@ constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw 32-bi
 // Tile geometry: BN (256 or 192) W rows x BM (128 or 256) X rows x BK (32 or 64) k, in a
 // ring of STAGES LDS stages.  Every wave owns BN / 2 W rows x 64 X rows (NI = BN / 64 blocks
 // of 32 W rows), so a workgroup has NW = 2 * BM / 64 waves (4 or 8).
-template <int BM_, int BK_, int STAGES_, int BN_ = 256>
+template <int BM_, int BK_, int STAGES_, int BN_ = 256, int KG_ = 1>
 struct Cfg {
   static constexpr int BN = BN_;
   static constexpr int WTN = BN / 2;                 // W rows per wave
@@ -233,8 +236,10 @@ struct Cfg {
   static constexpr int BK = BK_;
   static constexpr int STAGES = STAGES_;
   static constexpr int WM = BM / 64;                 // waves along X
-  static constexpr int NW = 2 * WM;                  // waves per workgroup
-  static constexpr int THREADS = 64 * NW;
+  static constexpr int NW = 2 * WM;                  // waves per k-group (one tile's worth)
+  static constexpr int KG = KG_;                     // k-groups: waves splitting each k-step
+  static constexpr int NWT = NW * KG;                // waves per workgroup
+  static constexpr int THREADS = 64 * NWT;
   static constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
   static constexpr int RPL = 64 / CPR;               // tile rows per wave-wide load
   static constexpr int W_CHUNKS = BN * CPR;
@@ -244,11 +249,14 @@ struct Cfg {
   static constexpr int X_LOADS = X_CHUNKS / THREADS;
   static constexpr int LOADS = W_LOADS + X_LOADS;
   static constexpr int KSUB = BK / 16;               // MFMA k16 sub-steps per stage
-  // With a ring of 3 or more stages a stage's loads are spread over four sub-steps (the last of
-  // k-step kt and the first KSUB-1 of k-step kt+1) instead of all issued in one.
+  static constexpr int KSUBW = KSUB / KG;            // sub-steps per wave per k-step
+  // With a ring of 3 or more stages a stage's loads are spread over a wave's KSUBW sub-steps (the
+  // last of k-step kt and the first KSUBW-1 of k-step kt+1) instead of all issued in one.
   static constexpr bool SPREAD = STAGES >= 3;
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(BN == 256 || BN == 192, "BN");
+  static_assert(KSUBW % 2 == 0, "fragment double buffer alternates within a k-step");
+  static_assert(W_CHUNKS % THREADS == 0 && X_CHUNKS % THREADS == 0, "loads per thread");
   static_assert(STAGES * STAGE * 16 <= 160 * 1024, "LDS");
   // Chunk slot s of row r holds global chunk s ^ swz(r): the 16 (or 32) consecutive rows one
   // ds_read_b128 phase touches fall in distinct 16-byte bank groups (64- or 128-bank LDS).
@@ -304,7 +312,7 @@ template <class C>
 __device__ __forceinline__ void issue_load(u32x4_t* lds, const __amdgpu_buffer_rsrc_t* rsrc,
                                            const uint32_t* voff, int wv, int kt, int stage, int j) {
   const bool is_w = j < C::W_LOADS;
-  const int g = wv + C::NW * (is_w ? j : j - C::W_LOADS);
+  const int g = wv + C::NWT * (is_w ? j : j - C::W_LOADS);
   u32x4_t* dst = &lds[stage * C::STAGE + (is_w ? 0 : C::W_CHUNKS) + g * 64];
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[j], (lds_void*)dst, 16, voff[j],
                                            (uint32_t)(kt * C::BK * 2), 0, 0);
@@ -376,34 +384,35 @@ __device__ __forceinline__ void tile_of(int b, int nb, int m_tiles, int& mtile, 
   }
 }
 
-// One k-step on ring slot kt % STAGES, as 4 (BK 64) or 2 (BK 32) MFMA sub-steps of k16.  The
+// One k-step on ring slot kt % STAGES, as 4 (BK 64) or 2 (BK 32) MFMA sub-steps of k16 (with
+// KG = 2 k-groups a wave runs the KSUBW = KSUB / 2 sub-steps from kk0 = its group's half).  The
 // fragments of the next sub-step are read one after each MFMA of the current one, so that their
 // issue hides under the MFMAs (the scheduling fences keep this order: left alone the scheduler
 // groups the reads and moves each just before its use).  The last sub-step waits for stage
 // kt+1 and reads its first fragments, so no k-step starts on an LDS latency.
 // Loads: with NEW the last sub-step refills slot kt % STAGES (free once every wave has passed
 // that sub-step's barrier) with stage kt+STAGES -- all of it, or with SPREAD its first share;
-// with REST (SPREAD) sub-step kk < KSUB-1 issues share kk+1 of stage kt-1+STAGES.  Loads are
+// with REST (SPREAD) sub-step kk < KSUBW-1 issues share kk+1 of stage kt-1+STAGES.  Loads are
 // issued in stage order either way, so the wait for stage kt+1 allows exactly the younger
 // stages issued so far: min(STAGES-2, KT-2-kt) of them.
 template <class C, bool NEW, bool REST>
 __device__ __forceinline__ void k_step(f32x16_t (&acc)[C::NI][2], bf16x8_t (&af)[2][C::NI],
                                        bf16x8_t (&bfr)[2][2], u32x4_t* lds,
                                        const __amdgpu_buffer_rsrc_t* rsrc, const uint32_t* voff,
-                                       int wv, int a_row, int b_row, int fh, int fs, int kt,
-                                       int KT) {
+                                       int wv, int a_row, int b_row, int fh, int fs, int kk0,
+                                       int kt, int KT) {
   const u32x4_t* st = &lds[(kt % C::STAGES) * C::STAGE];
   const u32x4_t* nst = &lds[((kt + 1) % C::STAGES) * C::STAGE];
 #pragma unroll
-  for (int kk = 0; kk < C::KSUB; ++kk) {
+  for (int kk = 0; kk < C::KSUBW; ++kk) {
     const int cur = kk & 1;
-    const bool last = kk + 1 == C::KSUB;
+    const bool last = kk + 1 == C::KSUBW;
     const bool rd = !last || kt + 1 < KT;
     // stage kt+1 must have landed; the younger stages issued so far may stay in flight
     if (last && rd)
       wait_stage_n<C::LOADS, C::STAGES - 2>(NEW ? C::STAGES - 2 : min(C::STAGES - 2, KT - 2 - kt));
     const u32x4_t* src = last ? nst : st;
-    const int ch = (2 * (last ? 0 : kk + 1) + fh) ^ fs;
+    const int ch = (2 * (kk0 + (last ? 0 : kk + 1)) + fh) ^ fs;
     // loads of this sub-step: share `sh` of stage `ls` into ring slot `slot`
     const bool issue = last ? NEW : (C::SPREAD && REST);
     const int sh = !C::SPREAD ? 0 : last ? 0 : kk + 1;
@@ -416,7 +425,7 @@ __device__ __forceinline__ void k_step(f32x16_t (&acc)[C::NI][2], bf16x8_t (&af)
           __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][t / 2], bfr[cur][t % 2], acc[t / 2][t % 2], 0, 0, 0);
       if (rd && t < C::NI + 2) read_frag<C>(src, a_row, b_row, ch, t, af[cur ^ 1], bfr[cur ^ 1]);
       if (issue) {
-        constexpr int SHARES = C::SPREAD ? C::KSUB : 1;
+        constexpr int SHARES = C::SPREAD ? C::KSUBW : 1;
         constexpr int PER = (C::LOADS + SHARES - 1) / SHARES;  // loads per share (last may be short)
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
@@ -441,20 +450,25 @@ __device__ __forceinline__ int swz_out(int u, int r) {
   return u ^ (r & 31);
 }
 
-template <int EPI, int BM, int BK, int STAGES, int MAPG, int BN>
-__global__ __launch_bounds__(BM * 2) __attribute__((amdgpu_waves_per_eu(BM / 128, BM / 128)))
+template <int EPI, int BM, int BK, int STAGES, int MAPG, int BN, int KG>
+__global__ __launch_bounds__(2 * BM * KG) __attribute__((amdgpu_waves_per_eu(BM * KG / 128, BM * KG / 128)))
 void gemm_wide_kernel(GemmParams p, int m_tiles) {
-  using C = Cfg<BM, BK, STAGES, BN>;
+  using C = Cfg<BM, BK, STAGES, BN, KG>;
+  static_assert(C::THREADS == 2 * BM * KG, "launch bounds");
   static_assert(EPI != kGemmSwiglu || BN == 256, "SwiGLU tiles are 256 W rows");
   __shared__ u32x4_t lds[STAGES * C::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave / C::WM, wm = wave % C::WM;
+  // wave = kg * NW + wt: k-group kg runs sub-steps kk0 .. kk0+KSUBW-1 of every k-step for the
+  // 128 x 64 block wt of the tile; with KG = 2 the groups' sums are added at the end
+  const int kg = wave / C::NW, wt = wave % C::NW;
+  const int wn = wt / C::WM, wm = wt % C::WM;
+  const int kk0 = __builtin_amdgcn_readfirstlane(kg * C::KSUBW);
   int mtile, ntile;
   tile_of<MAPG>(blockIdx.x, gridDim.x, m_tiles, mtile, ntile);
   const int m0 = mtile * BM;
 
-  // load j of this wave covers tile rows RPL*g .. RPL*g+RPL-1 with g = wave + NW*j;
+  // load j of this wave covers tile rows RPL*g .. RPL*g+RPL-1 with g = wave + NWT*j;
   // lane i fills LDS slot (row RPL*g + i/CPR, chunk i%CPR) from global chunk (i%CPR) ^ swz(row)
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   __amdgpu_buffer_rsrc_t rsrc[C::LOADS];
@@ -462,7 +476,7 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
 #pragma unroll
   for (int j = 0; j < C::LOADS; ++j) {
     const bool is_w = j < C::W_LOADS;
-    const int g = wv + C::NW * (is_w ? j : j - C::W_LOADS);
+    const int g = wv + C::NWT * (is_w ? j : j - C::W_LOADS);
     rsrc[j] = is_w ? w_group<EPI, C::BN>(p, ntile, g * C::RPL) : x_group(p, m0, g * C::RPL);
     const int rl = lane / C::CPR, c = (lane % C::CPR) ^ C::swz(g * C::RPL + rl);
     voff[j] = (uint32_t)((rl * p.K + c * 8) * 2);
@@ -495,25 +509,51 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
   if (STAGES - 1 < KT) issue_stage<C>(lds, rsrc, voff, wv, STAGES - 1, STAGES - 1);
   bf16x8_t af[2][C::NI], bfr[2][2];
 #pragma unroll
-  for (int n = 0; n < C::NI + 2; ++n) read_frag<C>(lds, a_row, b_row, fh ^ fs, n, af[0], bfr[0]);
+  for (int n = 0; n < C::NI + 2; ++n) read_frag<C>(lds, a_row, b_row, (2 * kk0 + fh) ^ fs, n, af[0], bfr[0]);
   int kt = 0;
   // stage STAGES-1 was issued whole above, so k-step 0 issues no remaining shares
   if (STAGES < KT) {
-    k_step<C, true, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+    k_step<C, true, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kk0, kt, KT);
     ++kt;
   }
   for (; kt + STAGES < KT; ++kt)
-    k_step<C, true, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+    k_step<C, true, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kk0, kt, KT);
   if (C::SPREAD && kt >= 1 && kt < KT) {  // the shares of stage KT-1 still to issue
-    k_step<C, false, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+    k_step<C, false, true>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kk0, kt, KT);
     ++kt;
   }
   for (; kt < KT; ++kt)
-    k_step<C, false, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kt, KT);
+    k_step<C, false, false>(acc, af, bfr, lds, rsrc, voff, wv, a_row, b_row, fh, fs, kk0, kt, KT);
+
+  if constexpr (C::KG == 2) {
+    // k-group 1 hands its sums to k-group 0 through the ring: block wt's 128 fp32 per lane,
+    // lane-contiguous (conflict-free)
+    static_assert(C::NW * C::NI * 2 * 16 * 64 * 4 <= STAGES * C::STAGE * 16, "reduction fits the ring");
+    float* red = reinterpret_cast<float*>(lds) + (size_t)wt * (C::NI * 2 * 16 * 64) + lane;
+    __syncthreads();  // every wave is done reading the ring
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) red[((i * 2 + j) * 16 + e) * 64] = acc[i][j][e];
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((i * 2 + j) * 16 + e) * 64];
+    }
+  }
 
   // ---- epilogue: accumulator element 4*g + q of tile (i, j) is
   //      W row wn*WTN + 32*i + 8*g + 4*(lane/32) + q,  X row m0 + wm*64 + 32*j + lane%32
   if constexpr (EPI == kGemmF32) {
+    if (kg != 0) return;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int m = m0 + wm * 64 + j * 32 + fr;
@@ -541,6 +581,7 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
     __syncthreads();  // every wave is done reading the ring
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
+      if (kg != 0) break;
       const int r = wm * 64 + j * 32 + fr;
       if constexpr (EPI == kGemmSwiglu) {
 #pragma unroll
@@ -607,14 +648,14 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
 
 }  // namespace wide
 
-template <int EPI, int BM = 128, int BK = 64, int STAGES = 3, int MAPG = 1, int WBN = 256>
+template <int EPI, int BM = 128, int BK = 64, int STAGES = 3, int MAPG = 1, int WBN = 256, int KG = 1>
 int launch_wide(const GemmParams& p, hipStream_t st) {
   const int m_tiles = (p.M + BM - 1) / BM;
   const int n_tiles = (EPI == kGemmSwiglu) ? (p.N + 127) / 128 : (p.N + WBN - 1) / WBN;
   const long long blocks = (long long)m_tiles * n_tiles;
   IE_REQUIRE(blocks <= 0x7fffffff, "gemm: too many tiles");
-  hipLaunchKernelGGL((wide::gemm_wide_kernel<EPI, BM, BK, STAGES, MAPG, WBN>), dim3((unsigned)blocks),
-                     dim3(BM * 2), 0, st, p, m_tiles);
+  hipLaunchKernelGGL((wide::gemm_wide_kernel<EPI, BM, BK, STAGES, MAPG, WBN, KG>), dim3((unsigned)blocks),
+                     dim3(wide::Cfg<BM, BK, STAGES, WBN, KG>::THREADS), 0, st, p, m_tiles);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
@@ -673,10 +714,10 @@ int launch_kind(int kind, int epi, const GemmParams& p, hipStream_t st) {
     case kTileSmall * 4 + kGemmResid: return launch_e<kGemmResid>(p, st);
     case kTileSmall * 4 + kGemmF32: return launch_e<kGemmF32>(p, st);
     case kTileSmall * 4 + kGemmSwiglu: return launch_e<kGemmSwiglu>(p, st);
-    case kTileWide * 4 + kGemmBf16: return launch_wide<kGemmBf16>(p, st);
-    case kTileWide * 4 + kGemmResid: return launch_wide<kGemmResid>(p, st);
-    case kTileWide * 4 + kGemmF32: return launch_wide<kGemmF32>(p, st);
-    case kTileWide * 4 + kGemmSwiglu: return launch_wide<kGemmSwiglu>(p, st);
+    case kTileWide * 4 + kGemmBf16: return launch_wide<kGemmBf16, 128, 64, 3, 1, 256, 2>(p, st);
+    case kTileWide * 4 + kGemmResid: return launch_wide<kGemmResid, 128, 64, 3, 1, 256, 2>(p, st);
+    case kTileWide * 4 + kGemmF32: return launch_wide<kGemmF32, 128, 64, 3, 1, 256, 2>(p, st);
+    case kTileWide * 4 + kGemmSwiglu: return launch_wide<kGemmSwiglu, 128, 64, 3, 1, 256, 2>(p, st);
     case kTileBig * 4 + kGemmBf16: return launch_wide<kGemmBf16, 256, 64, 2>(p, st);
     case kTileBig * 4 + kGemmResid: return launch_wide<kGemmResid, 256, 64, 2>(p, st);
     case kTileBig * 4 + kGemmSwiglu: return launch_wide<kGemmSwiglu, 256, 64, 2>(p, st);
