@@ -8,11 +8,15 @@
 // as B, and the quarters are summed through LDS.  Grid = N / 16 workgroups (256 for N = 4096,
 // 8016 for the lm_head), enough to fill the chip where a 128-row tile GEMM had 32.
 //
-// Load pattern: a step covers 128 k as 4 MFMA k-chunks of 32; for chunk c lane l (row l % 16,
-// group q = l / 16) loads the 16 bytes at k = 32c + 8q of its W row and of its X row (the
-// MFMA operand layout), so each load instruction reads 64 contiguous bytes of 16 rows and a
-// step streams 256 contiguous bytes of every weight row.  D = W . X^T: lane l holds output
-// row m = l % 16 and 4 consecutive output columns n = 4 (l / 16) + i.
+// Load pattern: a step covers 128 k (256 bytes of each of the tile's 16 weight rows) as 4 MFMA
+// k-chunks of 32.  The MFMA operand layout (lane l: row l % 16, 8 k at 8 (l / 16)) would make
+// each load instruction read 64 bytes of 16 rows -- half a cache line per row, which measured
+// 25-35% slower than whole rows -- so W is loaded as 4 rows x 256 contiguous bytes per
+// instruction and transposed through a wave-private LDS tile (one 16-byte write and one
+// 16-byte read per lane per instruction; the slot of row R's 16-byte chunk c is R*16 + (c ^ R),
+// conflict-free both ways).  LDS operations of one wave run in order, so the tile needs no
+// barrier.  X (L2-resident) is loaded in the operand layout directly.  D = W . X^T: lane l holds
+// output row m = l % 16 and 4 consecutive output columns n = 4 (l / 16) + i.
 //
 // Epilogues as the MFMA GEMM: bf16, residual add, fp32, and SwiGLU (gate and up rows of the
 // same 16 columns in one workgroup, lane-local silu(bf16(g)) * bf16(u)).
@@ -37,60 +41,90 @@ __device__ __forceinline__ const uint16_t* skinny_w_row(const GemmParams& p, int
   return p.w2 + (size_t)(R - e1) * p.K;
 }
 
-// the 4 chunks of one step: 16 bytes every 64 bytes from src (= row + k0 + 8q)
-__device__ __forceinline__ void load_step(const uint16_t* src, u32x4_t (&v)[4]) {
+// Loads of one step (k offset ks from each row start): W as 4 rows x 256 bytes per instruction
+// (lane (r, q): row 4j + q of tile t, 16-byte chunk r), X in the MFMA operand layout (lane
+// (r, q): X row r, the 16 bytes at k = 32c + 8q).
+template <int NT>
+__device__ __forceinline__ void sk_load(const uint16_t* const (&wp)[NT][4], const uint16_t* xr,
+                                        int ks, int r, int q, u32x4_t (&w)[NT][4],
+                                        u32x4_t (&xv)[4]) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c) v[c] = *reinterpret_cast<const u32x4_t*>(src + 32 * c);
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[t][j] = *reinterpret_cast<const u32x4_t*>(wp[t][j] + ks + 8 * r);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) xv[c] = *reinterpret_cast<const u32x4_t*>(xr + ks + 32 * c + 8 * q);
 }
 
-template <int EPI>
+// One step: the W rows through the wave's LDS tile into the operand layout, then 4 MFMA k-chunks
+// per tile (the MFMA's 32-k contraction of chunk c is k = 32c .. 32c+31 of the step for both
+// operands: W chunk 4c + q of row r, X the same).
+template <int NT>
+__device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const u32x4_t (&w)[NT][4],
+                                        const u32x4_t (&xv)[4], int r, int q, f32x4_t (&acc)[NT]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int R = 4 * j + q;
+      tr[t][R * 16 + (r ^ R)] = w[t][j];
+    }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const bf16x8_t xb = __builtin_bit_cast(bf16x8_t, xv[c]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8_t, tr[t][r * 16 + ((4 * c + q) ^ r)]), xb, acc[t], 0, 0, 0);
+  }
+}
+
+// KC: K fixed at compile time (4096 or 14336; the step loop then unrolls fully), 0: at run time.
+template <int EPI, int KC>
 __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p) {
   constexpr bool SW = EPI == kGemmSwiglu;
+  constexpr int NT = SW ? 2 : 1;  // 16-row W tiles: the weight rows, or gate and up rows
+  __shared__ u32x4_t tr[kSkSplit][NT][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int n0 = blockIdx.x * kSkRows;
+  const int K = KC > 0 ? KC : p.K;
 
-  const uint16_t *wa, *wb = nullptr;
-  if constexpr (SW) {
-    const int col = min(n0 + r, p.N - 1);
-    wa = p.w0 + (size_t)col * p.K;  // gate
-    wb = p.w1 + (size_t)col * p.K;  // up
-  } else {
-    wa = skinny_w_row(p, n0 + r);
+  // row 4j + q of each tile (rows past N repeat the last row; their outputs are not stored)
+  const uint16_t* wp[NT][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (SW) {
+      const int col = min(n0 + 4 * j + q, p.N - 1);
+      wp[0][j] = p.w0 + (size_t)col * K;  // gate
+      wp[NT - 1][j] = p.w1 + (size_t)col * K;  // up
+    } else {
+      wp[0][j] = skinny_w_row(p, n0 + 4 * j + q);
+    }
   }
-  const uint16_t* xr = p.x + (size_t)min(r, p.M - 1) * p.K;
-  const int kq = p.K / kSkSplit;
-  const int kbase = wave * kq + 8 * q;
+  const uint16_t* xr = p.x + (size_t)min(r, p.M - 1) * K;
+  const int kq = K / kSkSplit;
+  const int kbase = wave * kq;
   const int steps = kq / kSkStep;
 
-  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  u32x4_t ca[4], cb[4], cx[4], na[4], nb[4], nx[4];
-  load_step(wa + kbase, ca);
-  if constexpr (SW) load_step(wb + kbase, cb);
-  load_step(xr + kbase, cx);
-  for (int s = 0; s < steps; ++s) {
-    if (s + 1 < steps) {
-      const int k = kbase + (s + 1) * kSkStep;
-      load_step(wa + k, na);
-      if constexpr (SW) load_step(wb + k, nb);
-      load_step(xr + k, nx);
-    }
+  f32x4_t acc[NT];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8_t xb = __builtin_bit_cast(bf16x8_t, cx[c]);
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ca[c]), xb, acc0,
-                                                     0, 0, 0);
-      if constexpr (SW)
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cb[c]), xb,
-                                                       acc1, 0, 0, 0);
-    }
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // two register buffers: step s is multiplied while step s+1 is in flight, then buffer s % 2
+  // is refilled with step s+2
+  u32x4_t w0[NT][4], x0[4], w1[NT][4], x1[4];
+  sk_load<NT>(wp, xr, kbase, r, q, w0, x0);
+  if (steps > 1) sk_load<NT>(wp, xr, kbase + kSkStep, r, q, w1, x1);
+  int s = 0;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      ca[c] = na[c];
-      cx[c] = nx[c];
-      if constexpr (SW) cb[c] = nb[c];
-    }
+  for (; s + 1 < (KC > 0 ? KC / kSkSplit / kSkStep : steps); s += 2) {
+    sk_step<NT>(tr[wave], w0, x0, r, q, acc);
+    if (s + 2 < steps) sk_load<NT>(wp, xr, kbase + (s + 2) * kSkStep, r, q, w0, x0);
+    sk_step<NT>(tr[wave], w1, x1, r, q, acc);
+    if (s + 3 < steps) sk_load<NT>(wp, xr, kbase + (s + 3) * kSkStep, r, q, w1, x1);
   }
+  if (s < steps) sk_step<NT>(tr[wave], w0, x0, r, q, acc);
+  f32x4_t acc0 = acc[0], acc1 = acc[NT - 1];
 
   // sum the K quarters: waves 1..3 hand their tiles to wave 0
   __shared__ f32x4_t red[kSkSplit][SW ? 2 : 1][64];
@@ -133,7 +167,12 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
 template <int EPI>
 int launch_s(const GemmParams& p, hipStream_t st) {
   const int blocks = (p.N + kSkRows - 1) / kSkRows;
-  hipLaunchKernelGGL((gemm_skinny_kernel<EPI>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+  if (p.K == 4096)
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4096>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+  else if (p.K == 14336)
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 14336>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 0>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
