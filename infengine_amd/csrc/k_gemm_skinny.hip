@@ -15,7 +15,7 @@
 // instruction and transposed through a wave-private LDS tile (one 16-byte write and one
 // 16-byte read per lane per instruction; the slot of row R's 16-byte chunk c is R*16 + (c ^ R),
 // conflict-free both ways).  LDS operations of one wave run in order, so the tile needs no
-// barrier.  X (L2-resident) is loaded in the operand layout directly.  D = W . X^T: lane l holds
+// barrier.  X (L2-resident) takes the same path as one more 16-row tile.  D = W . X^T: lane l holds
 // output row m = l % 16 and 4 consecutive output columns n = 4 (l / 16) + i.
 //
 // Epilogues as the MFMA GEMM: bf16, residual add, fp32, and SwiGLU (gate and up rows of the
@@ -41,37 +41,36 @@ __device__ __forceinline__ const uint16_t* skinny_w_row(const GemmParams& p, int
   return p.w2 + (size_t)(R - e1) * p.K;
 }
 
-// Loads of one step (k offset ks from each row start): W as 4 rows x 256 bytes per instruction
-// (lane (r, q): row 4j + q of tile t, 16-byte chunk r), X in the MFMA operand layout (lane
-// (r, q): X row r, the 16 bytes at k = 32c + 8q).
+// Loads of one step (k offset ks from each row start), 4 rows x 256 bytes per instruction: lane
+// (r, q) loads 16-byte chunk r of row 4j + q of each W tile and of the X rows.
 template <int NT>
-__device__ __forceinline__ void sk_load(const uint16_t* const (&wp)[NT][4], const uint16_t* xr,
-                                        int ks, int r, int q, u32x4_t (&w)[NT][4],
-                                        u32x4_t (&xv)[4]) {
+__device__ __forceinline__ void sk_load(const uint16_t* const (&wp)[NT][4],
+                                        const uint16_t* const (&xp)[4], int ks, int r,
+                                        u32x4_t (&w)[NT][4], u32x4_t (&xv)[4]) {
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int j = 0; j < 4; ++j) w[t][j] = *reinterpret_cast<const u32x4_t*>(wp[t][j] + ks + 8 * r);
 #pragma unroll
-  for (int c = 0; c < 4; ++c) xv[c] = *reinterpret_cast<const u32x4_t*>(xr + ks + 32 * c + 8 * q);
+  for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4_t*>(xp[j] + ks + 8 * r);
 }
 
-// One step: the W rows through the wave's LDS tile into the operand layout, then 4 MFMA k-chunks
-// per tile (the MFMA's 32-k contraction of chunk c is k = 32c .. 32c+31 of the step for both
-// operands: W chunk 4c + q of row r, X the same).
+// One step: the W and X rows through the wave's LDS tiles into the operand layout, then 4 MFMA
+// k-chunks per W tile (the MFMA's 32-k contraction of chunk c is k = 32c .. 32c+31 of the step
+// for both operands: chunk 4c + q of W row r and of X row r).
 template <int NT>
 __device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const u32x4_t (&w)[NT][4],
                                         const u32x4_t (&xv)[4], int r, int q, f32x4_t (&acc)[NT]) {
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int j = 0; j < 4; ++j) {
+    const int R = 4 * j + q;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int R = 4 * j + q;
-      tr[t][R * 16 + (r ^ R)] = w[t][j];
-    }
+    for (int t = 0; t < NT; ++t) tr[t][R * 16 + (r ^ R)] = w[t][j];
+    tr[NT][R * 16 + (r ^ R)] = xv[j];
+  }
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const bf16x8_t xb = __builtin_bit_cast(bf16x8_t, xv[c]);
+    const bf16x8_t xb = __builtin_bit_cast(bf16x8_t, tr[NT][r * 16 + ((4 * c + q) ^ r)]);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -84,7 +83,7 @@ template <int EPI, int KC>
 __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p) {
   constexpr bool SW = EPI == kGemmSwiglu;
   constexpr int NT = SW ? 2 : 1;  // 16-row W tiles: the weight rows, or gate and up rows
-  __shared__ u32x4_t tr[kSkSplit][NT][256];
+  __shared__ u32x4_t tr[kSkSplit][NT + 1][256];  // per wave: the W tiles and the X rows
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int n0 = blockIdx.x * kSkRows;
@@ -102,7 +101,10 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
       wp[0][j] = skinny_w_row(p, n0 + 4 * j + q);
     }
   }
-  const uint16_t* xr = p.x + (size_t)min(r, p.M - 1) * K;
+  // X row 4j + q (rows past M repeat the last row; their outputs are not stored)
+  const uint16_t* xp[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) xp[j] = p.x + (size_t)min(4 * j + q, p.M - 1) * K;
   const int kq = K / kSkSplit;
   const int kbase = wave * kq;
   const int steps = kq / kSkStep;
@@ -113,15 +115,15 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
   // two register buffers: step s is multiplied while step s+1 is in flight, then buffer s % 2
   // is refilled with step s+2
   u32x4_t w0[NT][4], x0[4], w1[NT][4], x1[4];
-  sk_load<NT>(wp, xr, kbase, r, q, w0, x0);
-  if (steps > 1) sk_load<NT>(wp, xr, kbase + kSkStep, r, q, w1, x1);
+  sk_load<NT>(wp, xp, kbase, r, w0, x0);
+  if (steps > 1) sk_load<NT>(wp, xp, kbase + kSkStep, r, w1, x1);
   int s = 0;
 #pragma unroll
   for (; s + 1 < (KC > 0 ? KC / kSkSplit / kSkStep : steps); s += 2) {
     sk_step<NT>(tr[wave], w0, x0, r, q, acc);
-    if (s + 2 < steps) sk_load<NT>(wp, xr, kbase + (s + 2) * kSkStep, r, q, w0, x0);
+    if (s + 2 < steps) sk_load<NT>(wp, xp, kbase + (s + 2) * kSkStep, r, w0, x0);
     sk_step<NT>(tr[wave], w1, x1, r, q, acc);
-    if (s + 3 < steps) sk_load<NT>(wp, xr, kbase + (s + 3) * kSkStep, r, q, w1, x1);
+    if (s + 3 < steps) sk_load<NT>(wp, xp, kbase + (s + 3) * kSkStep, r, w1, x1);
   }
   if (s < steps) sk_step<NT>(tr[wave], w0, x0, r, q, acc);
   f32x4_t acc0 = acc[0], acc1 = acc[NT - 1];
