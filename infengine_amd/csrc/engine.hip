@@ -33,7 +33,7 @@ thread_local char g_err[1024] = "";
 
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// ---- decode workspace: [q | h | attn1 | partials]
+// ---- decode workspace: [q | h | attn1 | partials | xn]
 struct DecodeWs {
   uint16_t* q;      // [batch][4096]   rotated q
   uint16_t* h;      // [batch][14336]  SwiGLU output
@@ -41,13 +41,12 @@ struct DecodeWs {
   float* part_o;
   float* part_ml;
   uint16_t* xn;     // [batch][4096]   normalised rows (batched path)
-  uint16_t* qkv;    // [batch][6144]   projection (batched path)
 };
 
 size_t decode_ws_bytes(int batch) {
   return align256((size_t)batch * kHidden * 2) + align256((size_t)batch * kFFN * 2) +
          align256((size_t)batch * kHidden * 2) + align256(attn_decode_partials_bytes(batch)) +
-         align256((size_t)batch * kHidden * 2) + align256((size_t)batch * kQKVDim * 2);
+         align256((size_t)batch * kHidden * 2);
 }
 
 DecodeWs decode_ws(void* ws, int batch) {
@@ -64,8 +63,6 @@ DecodeWs decode_ws(void* ws, int batch) {
   d.part_ml = d.part_o + slots * kHeadDim;
   p += align256(attn_decode_partials_bytes(batch));
   d.xn = reinterpret_cast<uint16_t*>(p);
-  p += align256((size_t)batch * kHidden * 2);
-  d.qkv = reinterpret_cast<uint16_t*>(p);
   return d;
 }
 
@@ -630,14 +627,18 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     g.w2 = L.transformer.w_v;
     g.n0 = kHidden;
     g.n1 = kKVDim;
-    g.y = w.qkv;
+    g.y = w.q;  // q rotated; k rotated and v into each sequence's cache row
     g.M = batch;
     g.N = kQKVDim;
     g.K = kHidden;
     g.ldy = kQKVDim;
-    IE_TRY(launch_gemm(kGemmBf16, g, st));
-    IE_TRY(launch_qkv_rope_scatter(batch, 0, w.qkv, W.rope.cos, W.rope.sin, w.q, kvl,
-                                   kvl + (size_t)kKVHeads * kKVPlane, d_sl, cstride, st));
+    g.rope_cos = W.rope.cos;
+    g.rope_sin = W.rope.sin;
+    g.k_cache = kvl;
+    g.v_cache = kvl + (size_t)kKVHeads * kKVPlane;
+    g.cache_stride = cstride;
+    g.d_seq_len = d_sl;
+    IE_TRY(launch_gemm(kGemmQkvRope, g, st));
     IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, max_len, batch, cstride, true, st));
     GemmParams o{};
     o.x = attn_buffer;

@@ -115,6 +115,10 @@ enum GemmEpi : int {
   kGemmResid = 1,   // Y = bf16(Y + bf16(acc))
   kGemmF32 = 2,     // Yf = acc
   kGemmSwiglu = 3,  // Y[:, j] = bf16(silu(bf16(acc_gate)) * bf16(acc_up)) (two weights)
+  // Batched-decode QKV projection (skinny GEMM only, M <= 16, the [q|k|v] weights as w0/w1/w2):
+  // bf16(acc), RoPE on q and k at position d_seq_len[m] - 1, q to q_out [M][32][128], k and v to
+  // sequence m's cache row (rope.cu:53-64, attn.cu:345-352).
+  kGemmQkvRope = 4,
 };
 struct GemmParams {
   const uint16_t* x;   // [M][K]
@@ -126,6 +130,13 @@ struct GemmParams {
   float* yf;           // [M][ldy]
   int M, N, K;
   int ldy;
+  // kGemmQkvRope only
+  const float* rope_cos;   // [kMaxCtx][64]
+  const float* rope_sin;
+  uint16_t* k_cache;       // sequence 0's K plane base of this layer [8][kMaxCtx][128]
+  uint16_t* v_cache;
+  long long cache_stride;  // elements between sequences' caches
+  const int* d_seq_len;    // [M]
 };
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st);
 

@@ -806,6 +806,7 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
              "gemm: weight split points n0=%d n0+n1=%d inside N=%d must be multiples of 16", p.n0,
              p.n0 + p.n1, p.N);
   if (gemm_skinny_fits(p)) return launch_gemm_skinny(epi, p, st);
+  IE_REQUIRE(epi >= kGemmBf16 && epi <= kGemmSwiglu, "gemm: epilogue %d needs M <= 16", epi);
   return launch_tiled(epi, p, st, true);
 }
 

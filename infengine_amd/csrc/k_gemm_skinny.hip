@@ -19,7 +19,10 @@
 // output row m = l % 16 and 4 consecutive output columns n = 4 (l / 16) + i.
 //
 // Epilogues as the MFMA GEMM: bf16, residual add, fp32, and SwiGLU (gate and up rows of the
-// same 16 columns in one workgroup, lane-local silu(bf16(g)) * bf16(u)).
+// same 16 columns in one workgroup, lane-local silu(bf16(g)) * bf16(u)); and QKV + RoPE for
+// batched decode: workgroup b owns RoPE pairs 8 (b % 8) .. +7 of head b / 8 (its 16 weight rows
+// are those pairs' first halves, then their second halves), so lane l and lane l ^ 32 hold the
+// two halves of the same 4 pairs and one cross-lane swap gives each both.
 #include "ie_kernels.h"
 
 namespace ie {
@@ -78,6 +81,19 @@ __device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const u32x4_t (&w)[N
   }
 }
 
+// Steps s and s+1 from the two register buffers, each refilled with the step two ahead.
+template <int NT>
+__device__ __forceinline__ void sk_pair(u32x4_t (*tr)[256], const uint16_t* const (&wp)[NT][4],
+                                        const uint16_t* const (&xp)[4], int kbase, int s,
+                                        int steps, int r, int q, u32x4_t (&w0)[NT][4],
+                                        u32x4_t (&x0)[4], u32x4_t (&w1)[NT][4], u32x4_t (&x1)[4],
+                                        f32x4_t (&acc)[NT]) {
+  sk_step<NT>(tr, w0, x0, r, q, acc);
+  if (s + 2 < steps) sk_load<NT>(wp, xp, kbase + (s + 2) * kSkStep, r, w0, x0);
+  sk_step<NT>(tr, w1, x1, r, q, acc);
+  if (s + 3 < steps) sk_load<NT>(wp, xp, kbase + (s + 3) * kSkStep, r, w1, x1);
+}
+
 // KC: K fixed at compile time (4096 or 14336; the step loop then unrolls fully), 0: at run time.
 template <int EPI, int KC>
 __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p) {
@@ -93,7 +109,10 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
   const uint16_t* wp[NT][4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if constexpr (SW) {
+    if constexpr (EPI == kGemmQkvRope) {
+      const int R = 4 * j + q;
+      wp[0][j] = skinny_w_row(p, (blockIdx.x >> 3) * kHeadDim + (blockIdx.x & 7) * 8 + (R & 7) + 64 * (R >> 3));
+    } else if constexpr (SW) {
       const int col = min(n0 + 4 * j + q, p.N - 1);
       wp[0][j] = p.w0 + (size_t)col * K;  // gate
       wp[NT - 1][j] = p.w1 + (size_t)col * K;  // up
@@ -118,12 +137,13 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
   sk_load<NT>(wp, xp, kbase, r, w0, x0);
   if (steps > 1) sk_load<NT>(wp, xp, kbase + kSkStep, r, w1, x1);
   int s = 0;
+  if constexpr (KC > 0) {
 #pragma unroll
-  for (; s + 1 < (KC > 0 ? KC / kSkSplit / kSkStep : steps); s += 2) {
-    sk_step<NT>(tr[wave], w0, x0, r, q, acc);
-    if (s + 2 < steps) sk_load<NT>(wp, xp, kbase + (s + 2) * kSkStep, r, w0, x0);
-    sk_step<NT>(tr[wave], w1, x1, r, q, acc);
-    if (s + 3 < steps) sk_load<NT>(wp, xp, kbase + (s + 3) * kSkStep, r, w1, x1);
+    for (; s + 1 < KC / kSkSplit / kSkStep; s += 2)
+      sk_pair<NT>(tr[wave], wp, xp, kbase, s, steps, r, q, w0, x0, w1, x1, acc);
+  } else {
+    for (; s + 1 < steps; s += 2)
+      sk_pair<NT>(tr[wave], wp, xp, kbase, s, steps, r, q, w0, x0, w1, x1, acc);
   }
   if (s < steps) sk_step<NT>(tr[wave], w0, x0, r, q, acc);
   f32x4_t acc0 = acc[0], acc1 = acc[NT - 1];
@@ -141,6 +161,42 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
   }
 
   const int m = r, n = n0 + 4 * q;
+  if constexpr (EPI == kGemmQkvRope) {
+    // lanes q < 2 hold the first halves of pairs jp .. jp+3, lanes q + 2 (= lane ^ 32) the second
+    float a[4], b[4];
+    const bool hi = q >= 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float mine = bf2f(f2bf(acc0[i]));
+      const float other = __shfl_xor(mine, 32);
+      a[i] = hi ? other : mine;
+      b[i] = hi ? mine : other;
+    }
+    if (m >= p.M) return;
+    const int head = blockIdx.x >> 3, jp = (blockIdx.x & 7) * 8 + 4 * (q & 1);
+    const int pos = p.d_seq_len[m] - 1;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (head < kQHeads + kKVHeads) {
+        const float c = p.rope_cos[pos * 64 + jp + i], sn = p.rope_sin[pos * 64 + jp + i];
+        v[i] = hi ? a[i] * sn + b[i] * c : a[i] * c - b[i] * sn;
+      } else {
+        v[i] = hi ? b[i] : a[i];
+      }
+    }
+    uint16_t* dst;
+    if (head < kQHeads)
+      dst = p.y + ((size_t)m * kQHeads + head) * kHeadDim;
+    else if (head < kQHeads + kKVHeads)
+      dst = p.k_cache + (size_t)m * p.cache_stride + ((size_t)(head - kQHeads) * kMaxCtx + pos) * kHeadDim;
+    else
+      dst = p.v_cache + (size_t)m * p.cache_stride +
+            ((size_t)(head - kQHeads - kKVHeads) * kMaxCtx + pos) * kHeadDim;
+    *reinterpret_cast<uint2*>(dst + jp + (hi ? 64 : 0)) =
+        make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+    return;
+  }
   if (m >= p.M || n >= p.N) return;
   if constexpr (EPI == kGemmF32) {
     *reinterpret_cast<float4*>(p.yf + (size_t)m * p.ldy + n) =
@@ -169,6 +225,14 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
 template <int EPI>
 int launch_s(const GemmParams& p, hipStream_t st) {
   const int blocks = (p.N + kSkRows - 1) / kSkRows;
+  if constexpr (EPI == kGemmQkvRope) {
+    IE_REQUIRE(p.K == kHidden && p.N == kQKVDim && p.n0 == kHidden && p.n1 == kKVDim && p.y &&
+                   p.k_cache && p.v_cache && p.d_seq_len && p.rope_cos && p.rope_sin,
+               "gemm_skinny: the QKV + RoPE epilogue is for the [q|k|v] projection");
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4096>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+    IE_CHECK_LAUNCH();
+    return IE_OK;
+  }
   if (p.K == 4096)
     hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4096>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
   else if (p.K == 14336)
@@ -193,6 +257,7 @@ int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {
     case kGemmResid: return launch_s<kGemmResid>(p, st);
     case kGemmF32: return launch_s<kGemmF32>(p, st);
     case kGemmSwiglu: return launch_s<kGemmSwiglu>(p, st);
+    case kGemmQkvRope: return launch_s<kGemmQkvRope>(p, st);
   }
   set_error("gemm_skinny: bad epilogue %d", epi);
   return IE_ERR_INVALID_ARG;

@@ -227,7 +227,9 @@ def test_batched_decode_matches_single(hip, model, noise_floor):
         req.kv_view()[:, :, :, :lens[b] - 1] = dev(prior).view(torch.bfloat16)
         req.tokens[lens[b] - 1] = 1000 * (b + 1)
         t = req.decode_step(lens[b])
-        singles.append((t, host(req.logits).copy()))
+        # the new token's K (rotated) and V rows of every layer
+        kv_row = host(req.kv_view()[:, :, :, lens[b] - 1].contiguous().view(torch.int16)).copy()
+        singles.append((t, host(req.logits).copy(), kv_row))
         del req
     data = torch.zeros(B, 4096, dtype=torch.bfloat16, device="cuda")
     attn = torch.zeros_like(data)
@@ -244,6 +246,14 @@ def test_batched_decode_matches_single(hip, model, noise_floor):
         assert_close(host(logits[b]), singles[b][1], tol=e2e_tol(noise_floor),
                      what=f"batched row {b}")
         assert list(th)[b] == int(out[b].item()) == int(np.argmax(host(logits[b])))
+        # the projection + RoPE + cache write fused into the batched QKV GEMM writes the same
+        # rows as the single-sequence path: bf16-close at layer 0 (only the summation order
+        # differs), within the end-to-end tolerance through all 32 layers
+        got_row = host(kvs.view(B, 32, 2, 8, 8192, 128)[b, :, :, :, lens[b] - 1].contiguous())
+        assert_bf16_close(got_row[0], singles[b][2][0], ulps=2, what=f"batched kv row {b} layer 0",
+                          outlier_frac=1e-3)
+        assert_close(orc.bf16_to_f32(got_row), orc.bf16_to_f32(singles[b][2]),
+                     tol=e2e_tol(noise_floor), what=f"batched kv row {b}")
     c.close()
 
 
