@@ -33,20 +33,24 @@ thread_local char g_err[1024] = "";
 
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// ---- decode workspace: [q | h | attn1 | partials | xn]
+// ---- decode workspace: [q | h | attn1 | partials | xn | ss]
 struct DecodeWs {
   uint16_t* q;      // [batch][4096]   rotated q
   uint16_t* h;      // [batch][14336]  SwiGLU output
   uint16_t* attn1;  // [batch][4096]   attention output (op-level decode_attn only)
   float* part_o;
   float* part_ml;
-  uint16_t* xn;     // [batch][4096]   normalised rows (batched path)
+  uint16_t* xn;     // [batch][4096]   rows times the next norm weight (batched path)
+  float* ss;        // [256][16]       partial sums of squares of those rows (batched path)
 };
+
+// Producer workgroups of a 4096-column skinny GEMM: the partial sums of squares per row.
+constexpr int kNormParts = kHidden / 16;
 
 size_t decode_ws_bytes(int batch) {
   return align256((size_t)batch * kHidden * 2) + align256((size_t)batch * kFFN * 2) +
          align256((size_t)batch * kHidden * 2) + align256(attn_decode_partials_bytes(batch)) +
-         align256((size_t)batch * kHidden * 2);
+         align256((size_t)batch * kHidden * 2) + align256((size_t)kNormParts * 16 * sizeof(float));
 }
 
 DecodeWs decode_ws(void* ws, int batch) {
@@ -63,6 +67,8 @@ DecodeWs decode_ws(void* ws, int batch) {
   d.part_ml = d.part_o + slots * kHeadDim;
   p += align256(attn_decode_partials_bytes(batch));
   d.xn = reinterpret_cast<uint16_t*>(p);
+  p += align256((size_t)batch * kHidden * 2);
+  d.ss = reinterpret_cast<float*>(p);
   return d;
 }
 
@@ -616,10 +622,14 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
   const DecodeWs w = decode_ws(workspace, batch);
   const long long cstride = (long long)kLayers * kKVLayer;
   IE_TRY(launch_emblookup(batch, tokenid_buffs, W.emb_lookup, data_buffer, d_sl, kMaxCtx, st));
+  // RMSNorm folded into the projections: each norm's input rows arrive as bf16(x * norm weight)
+  // with partial sums of squares (layer 0: from this prep kernel, 4 per row; later:
+  // from the residual epilogue of the O / down projection, kNormParts partials per row), and the
+  // projection scales its accumulators by rsqrt(mean + eps)
+  IE_TRY(launch_rmsnorm_prep(batch, data_buffer, W.layers[0].input_layernorm, w.xn, w.ss, st));
   for (int l = 0; l < kLayers; ++l) {
     const ie_layer& L = W.layers[l];
     uint16_t* kvl = kv_layer(kv_caches, l);
-    IE_TRY(launch_rmsnorm(batch, data_buffer, L.input_layernorm, w.xn, st));
     GemmParams g{};
     g.x = w.xn;
     g.w0 = L.transformer.w_q;
@@ -638,6 +648,8 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     g.v_cache = kvl + (size_t)kKVHeads * kKVPlane;
     g.cache_stride = cstride;
     g.d_seq_len = d_sl;
+    g.ss_in = w.ss;
+    g.ss_parts = l == 0 ? 4 : kNormParts;
     IE_TRY(launch_gemm(kGemmQkvRope, g, st));
     IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, max_len, batch, cstride, true, st));
     GemmParams o{};
@@ -649,8 +661,10 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     o.N = kHidden;
     o.K = kHidden;
     o.ldy = kHidden;
+    o.xw_out = w.xn;
+    o.xw_norm = L.post_attention_layernorm;
+    o.ss_out = w.ss;
     IE_TRY(launch_gemm(kGemmResid, o, st));
-    IE_TRY(launch_rmsnorm(batch, data_buffer, L.post_attention_layernorm, w.xn, st));
     GemmParams gu{};
     gu.x = w.xn;
     gu.w0 = L.ffn_block.w_gate;
@@ -660,6 +674,8 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     gu.N = kFFN;
     gu.K = kHidden;
     gu.ldy = kFFN;
+    gu.ss_in = w.ss;
+    gu.ss_parts = kNormParts;
     IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
     GemmParams dn{};
     dn.x = w.h;
@@ -670,9 +686,11 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     dn.N = kHidden;
     dn.K = kFFN;
     dn.ldy = kHidden;
+    dn.xw_out = w.xn;
+    dn.xw_norm = l + 1 < kLayers ? W.layers[l + 1].input_layernorm : W.final_norm;
+    dn.ss_out = w.ss;
     IE_TRY(launch_gemm(kGemmResid, dn, st));
   }
-  IE_TRY(launch_rmsnorm(batch, data_buffer, W.final_norm, w.xn, st));
   GemmParams lm{};
   lm.x = w.xn;
   lm.w0 = W.lm_head;
@@ -682,6 +700,8 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
   lm.N = kVocab;
   lm.K = kHidden;
   lm.ldy = kVocab;
+  lm.ss_in = w.ss;
+  lm.ss_parts = kNormParts;
   IE_TRY(launch_gemm(kGemmF32, lm, st));
   IE_TRY(launch_argmax_rows(batch, kVocab, output_distr, output_tokens, c->d_slots,
                             c->d_counters + kCntArgmax, st));

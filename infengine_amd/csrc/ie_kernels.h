@@ -76,6 +76,10 @@ size_t attn_decode_partials_bytes(int batch);
 // ------------------------------------------------------------ elementwise
 int launch_emblookup(int rows, const int* ids, const uint16_t* table, uint16_t* out,
                      const int* d_seq_len, int ids_stride, hipStream_t st);
+// For a skinny GEMM with the norm folded in: xw = bf16(x * w) and the sums of squares of rows
+// 0..15 as 4 partials per row (ss[m][4]: the row's sum, then zeros; rows >= `rows` all zero).
+int launch_rmsnorm_prep(int rows, const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ss,
+                        hipStream_t st);
 int launch_rmsnorm(int rows, const uint16_t* x, const uint16_t* w, uint16_t* out,
                    hipStream_t st);
 int launch_residual_add(size_t n, uint16_t* x, const uint16_t* d, hipStream_t st);
@@ -137,6 +141,16 @@ struct GemmParams {
   uint16_t* v_cache;
   long long cache_stride;  // elements between sequences' caches
   const int* d_seq_len;    // [M]
+  // Skinny GEMM (M <= 16) only: RMSNorm folded into the projection.
+  // Consumer: x holds bf16(x_row * norm_w) and ss_in [16][ss_parts] partial sums of squares of the
+  // 16 rows (rows past M zero); the accumulators are scaled by rsqrt(sum / K + eps).
+  const float* ss_in;
+  int ss_parts;
+  // Producer (kGemmResid): also writes xw_out = bf16(y_new * xw_norm) (stride ldy) and this
+  // workgroup's sums of squares of the 16 new rows to ss_out[row][blockIdx] (N / 16 per row).
+  uint16_t* xw_out;
+  const uint16_t* xw_norm;
+  float* ss_out;
 };
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st);
 

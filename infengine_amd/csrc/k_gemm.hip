@@ -807,6 +807,7 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
              p.n0 + p.n1, p.N);
   if (gemm_skinny_fits(p)) return launch_gemm_skinny(epi, p, st);
   IE_REQUIRE(epi >= kGemmBf16 && epi <= kGemmSwiglu, "gemm: epilogue %d needs M <= 16", epi);
+  IE_REQUIRE(!p.ss_in && !p.ss_out, "gemm: the folded RMSNorm needs M <= 16");
   return launch_tiled(epi, p, st, true);
 }
 

@@ -35,6 +35,9 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kSkRows = 16;   // weight rows (output columns) per workgroup
 constexpr int kSkSplit = 4;   // waves per workgroup = K quarters
 constexpr int kSkStep = 128;  // k per step
+// Folded RMSNorm: each of a row's 16 summing threads takes up to kSsLoads float4 partials, so up
+// to 16 * 4 * kSsLoads = 256 producer workgroups.
+constexpr int kSsLoads = 4;
 
 __device__ __forceinline__ const uint16_t* skinny_w_row(const GemmParams& p, int R) {
   if (R >= p.N) R = p.N - 1;
@@ -134,8 +137,33 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
   // two register buffers: step s is multiplied while step s+1 is in flight, then buffer s % 2
   // is refilled with step s+2
   u32x4_t w0[NT][4], x0[4], w1[NT][4], x1[4];
+  // folded RMSNorm: the rows' sums of squares from the producer's partials, [16][ss_parts] (a
+  // multiple of 4).  Loaded before the first weight loads and summed after them: loads return in
+  // issue order, so waiting for these does not wait for the weights.
+  __shared__ float ssr[16];
+  float4 ssv[kSsLoads];
+  const bool norm = p.ss_in != nullptr;
+  const int ss_row = threadIdx.x >> 4, ss_lane = threadIdx.x & 15;
+  if (norm) {
+#pragma unroll
+    for (int i = 0; i < kSsLoads; ++i) {
+      const int b = 4 * (ss_lane + 16 * i);
+      ssv[i] = b < p.ss_parts ? *reinterpret_cast<const float4*>(p.ss_in + ss_row * p.ss_parts + b)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   sk_load<NT>(wp, xp, kbase, r, w0, x0);
   if (steps > 1) sk_load<NT>(wp, xp, kbase + kSkStep, r, w1, x1);
+  __builtin_amdgcn_sched_barrier(0);
+  if (norm) {
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSsLoads; ++i) sum += (ssv[i].x + ssv[i].y) + (ssv[i].z + ssv[i].w);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 16);
+    if (ss_lane == 0) ssr[ss_row] = sum;
+  }
   int s = 0;
   if constexpr (KC > 0) {
 #pragma unroll
@@ -161,6 +189,36 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
   }
 
   const int m = r, n = n0 + 4 * q;
+  if (norm) {
+    const float inv = rsqrtf(ssr[m] / (float)K + kRmsEps);
+    acc0 *= inv;
+    if constexpr (SW) acc1 *= inv;
+  }
+  if constexpr (EPI == kGemmResid) {
+    if (p.ss_out) {
+      // the new residual rows, bf16(y * norm weight) for the next projection, and this
+      // workgroup's share of each row's sum of squares (lanes q = 0..3 hold 4 columns each)
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      if (m < p.M && n < p.N) {
+        uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n);
+        const uint2 old = *dst;
+        v[0] = bf2f(f2bf(bf_lo(old.x) + bf2f(f2bf(acc0[0]))));
+        v[1] = bf2f(f2bf(bf_hi(old.x) + bf2f(f2bf(acc0[1]))));
+        v[2] = bf2f(f2bf(bf_lo(old.y) + bf2f(f2bf(acc0[2]))));
+        v[3] = bf2f(f2bf(bf_hi(old.y) + bf2f(f2bf(acc0[3]))));
+        *dst = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+        const uint2 wv = *reinterpret_cast<const uint2*>(p.xw_norm + n);
+        *reinterpret_cast<uint2*>(p.xw_out + (size_t)m * p.ldy + n) =
+            make_uint2(pack_bf2(v[0] * bf_lo(wv.x), v[1] * bf_hi(wv.x)),
+                       pack_bf2(v[2] * bf_lo(wv.y), v[3] * bf_hi(wv.y)));
+      }
+      float sq = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], v[3] * v[3])));
+      sq += __shfl_xor(sq, 16);
+      sq += __shfl_xor(sq, 32);
+      if (q == 0) p.ss_out[m * gridDim.x + blockIdx.x] = sq;
+      return;
+    }
+  }
   if constexpr (EPI == kGemmQkvRope) {
     // lanes q < 2 hold the first halves of pairs jp .. jp+3, lanes q + 2 (= lane ^ 32) the second
     float a[4], b[4];
@@ -252,6 +310,12 @@ bool gemm_skinny_fits(const GemmParams& p) {
 int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {
   IE_REQUIRE(gemm_skinny_fits(p), "gemm_skinny: needs M <= %d and K %% %d == 0 (M=%d K=%d)",
              kSkRows, kSkSplit * kSkStep, p.M, p.K);
+  IE_REQUIRE(!p.ss_in || (p.ss_parts >= 4 && p.ss_parts % 4 == 0 && p.ss_parts <= 64 * kSsLoads &&
+                          epi != kGemmResid),
+             "gemm_skinny: folded RMSNorm input needs 4..%d partial sums per row (a multiple of 4)",
+             64 * kSsLoads);
+  IE_REQUIRE(!p.ss_out || (epi == kGemmResid && p.xw_out && p.xw_norm && p.N % 16 == 0),
+             "gemm_skinny: the norm-preparing output is a residual-epilogue option");
   switch (epi) {
     case kGemmBf16: return launch_s<kGemmBf16>(p, st);
     case kGemmResid: return launch_s<kGemmResid>(p, st);

@@ -247,11 +247,15 @@ def test_batched_decode_matches_single(hip, model, noise_floor):
                      what=f"batched row {b}")
         assert list(th)[b] == int(out[b].item()) == int(np.argmax(host(logits[b])))
         # the projection + RoPE + cache write fused into the batched QKV GEMM writes the same
-        # rows as the single-sequence path: bf16-close at layer 0 (only the summation order
-        # differs), within the end-to-end tolerance through all 32 layers
+        # rows as the single-sequence path: bf16-close at layer 0, within the end-to-end
+        # tolerance through all 32 layers.  The batched path folds RMSNorm into the projection
+        # -- it multiplies bf16(x * w) and scales the fp32 sums by rsqrt(mean + eps), where the
+        # reference (rmsnorm.cu) rounds bf16(bf16(x * rsqrt) * w) before the product -- so about
+        # 1-2% of the layer-0 elements land more than 2 bf16 steps away (each within 1e-2 of
+        # the scale, which assert_bf16_close enforces)
         got_row = host(kvs.view(B, 32, 2, 8, 8192, 128)[b, :, :, :, lens[b] - 1].contiguous())
         assert_bf16_close(got_row[0], singles[b][2][0], ulps=2, what=f"batched kv row {b} layer 0",
-                          outlier_frac=1e-3)
+                          outlier_frac=5e-2)
         assert_close(orc.bf16_to_f32(got_row), orc.bf16_to_f32(singles[b][2]),
                      tol=e2e_tol(noise_floor), what=f"batched kv row {b}")
     c.close()
