@@ -18,7 +18,8 @@ Also reported, on the same run:
                 untimed calls), and the four prefill GEMM shapes at M = 2048 (QKV, O with
                 residual, gate/up with SwiGLU, down with residual) timed with HIP events
                 on the engine stream after 150 ms of warm-up (median of 3 runs of 10
-                launches), as TFLOP/s and fraction of the 2.5 PFLOP/s dense bf16 MFMA peak.
+                launches), as TFLOP/s and fraction of the 2.5 PFLOP/s dense bf16 MFMA peak,
+                with torch.matmul (hipBLASLt) on the same shapes and protocol beside them.
   cpu_baseline  the CPU oracle (oracle/, OpenMP) decoding the same model on this
                 host: whole decode steps (32 layers + lm_head + argmax) for about
                 10 s after one untimed step.
@@ -244,20 +245,35 @@ def main() -> int:
                 for _ in range(8):
                     run()
                 torch.cuda.synchronize()
-            runs = []
-            for _ in range(3):
-                g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                g0.record(stream)
-                for _ in range(10):
-                    run()
-                g1.record(stream)
-                g1.synchronize()
-                runs.append(g0.elapsed_time(g1) * 1e3 / 10)
-            us = sorted(runs)[1]
-            tf = 2.0 * P * n * k * (2 if epi == 3 else 1) / (us * 1e-6) / 1e12
+            def timed(fn) -> float:
+                runs = []
+                for _ in range(3):
+                    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    g0.record(stream)
+                    for _ in range(10):
+                        fn()
+                    g1.record(stream)
+                    g1.synchronize()
+                    runs.append(g0.elapsed_time(g1) * 1e3 / 10)
+                return sorted(runs)[1]
+
+            us = timed(run)
+            flop = 2.0 * P * n * k * (2 if epi == 3 else 1)
+            tf = flop / (us * 1e-6) / 1e12
+            # the same product through torch.matmul (hipBLASLt), same protocol: gate and up as
+            # one [2 * 14336, 4096] weight, no fused epilogue
+            gw = torch.cat([gw0, gw1]) if epi == 3 else gw0
+            t_end = time.perf_counter() + 0.15
+            while time.perf_counter() < t_end:
+                for _ in range(8):
+                    torch.matmul(gx, gw.t())
+                torch.cuda.synchronize()
+            ref_us = timed(lambda: torch.matmul(gx, gw.t()))
             gemms[name] = {"m": P, "n": n, "k": k, "us": round(us, 1), "tflops": round(tf, 1),
-                           "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
-            del gx, gw0, gw1, gy
+                           "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                           "torch_matmul_us": round(ref_us, 1),
+                           "torch_matmul_tflops": round(flop / (ref_us * 1e-6) / 1e12, 1)}
+            del gx, gw0, gw1, gy, gw
         flops = 2.0 * P * LAYER_GEMM_PARAMS * LAYERS
         prefill2048 = {"seq_len": P, "ms": round(pdt * 1e3, 2), "tokens_per_s": round(P / pdt, 1),
                        "layer_gemm_tflops_per_s": round(flops / pdt / 1e12, 1),
