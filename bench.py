@@ -104,6 +104,65 @@ def calibration_copy(nbytes: int = 256 << 20) -> None:
     torch.cuda.synchronize()
 
 
+def prefill_gemms(ctx, P: int) -> dict:
+    """The four prefill GEMM shapes at M = P (QKV, O with residual, gate/up with SwiGLU, down with
+    residual) through ie_gemm_ex, and the same products through torch.matmul (hipBLASLt), each
+    timed with HIP events on the engine stream after 150 ms of warm-up (median of 3 runs of 10
+    launches)."""
+    import torch
+
+    from infengine_amd import check, lib
+    from infengine_amd.engine import ptr
+
+    stream = ctx.stream
+
+    def timed(fn) -> float:
+        # The clocks settle over the first ~0.1 s of sustained MFMA load (a cold launch runs
+        # 10-15 % slow), as they do inside a prefill's 32 back-to-back layers: warm up for
+        # 150 ms, then take the median of three timed runs of 10 launches.
+        t_end = time.perf_counter() + 0.15
+        while time.perf_counter() < t_end:
+            for _ in range(8):
+                fn()
+            torch.cuda.synchronize()
+        runs = []
+        for _ in range(3):
+            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            g0.record(stream)
+            for _ in range(10):
+                fn()
+            g1.record(stream)
+            g1.synchronize()
+            runs.append(g0.elapsed_time(g1) * 1e3 / 10)
+        return sorted(runs)[1]
+
+    gemms = {}
+    for name, epi, k, n in (("qkv", 0, HIDDEN, 6144), ("o", 1, HIDDEN, HIDDEN),
+                            ("gate_up", 3, HIDDEN, FFN), ("down", 1, FFN, HIDDEN)):
+        gx = (torch.randn(P, k, device="cuda") * 0.5).to(torch.bfloat16)
+        gw0 = (torch.randn(n, k, device="cuda") * 0.02).to(torch.bfloat16)
+        gw1 = (torch.randn(n, k, device="cuda") * 0.02).to(torch.bfloat16) if epi == 3 else gw0
+        gy = torch.zeros(P, n, dtype=torch.bfloat16, device="cuda")
+        torch.cuda.synchronize()
+
+        def run() -> None:
+            check(lib.ie_gemm_ex(ctx.handle, epi, P, k, n, ptr(gx), ptr(gw0), ptr(gw1), ptr(gy)))
+
+        us = timed(run)
+        flop = 2.0 * P * n * k * (2 if epi == 3 else 1)
+        tf = flop / (us * 1e-6) / 1e12
+        # the same product through torch.matmul (hipBLASLt), same protocol: gate and up as
+        # one [2 * 14336, 4096] weight, no fused epilogue
+        gw = torch.cat([gw0, gw1]) if epi == 3 else gw0
+        ref_us = timed(lambda: torch.matmul(gx, gw.t()))
+        gemms[name] = {"m": P, "n": n, "k": k, "us": round(us, 1), "tflops": round(tf, 1),
+                       "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                       "torch_matmul_us": round(ref_us, 1),
+                       "torch_matmul_tflops": round(flop / (ref_us * 1e-6) / 1e12, 1)}
+        del gx, gw0, gw1, gy, gw
+    return gemms
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -117,6 +176,9 @@ def main() -> int:
     ap.add_argument("--batch-steps", type=int, default=32)
     ap.add_argument("--prefill-len", type=int, default=2048,
                     help="config 4 prefill leg and its GEMM roofline (0: skip)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the prefill GEMM shapes at M = --prefill-len, ours and torch.matmul "
+                         "(for profiling them); prints their JSON")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -139,6 +201,10 @@ def main() -> int:
     if args.calibration_copy:
         calibration_copy()
     ctx = Context(0, graph=not args.no_graph)
+    if args.gemm_only:
+        print(json.dumps({"prefill_gemm": prefill_gemms(ctx, args.prefill_len or 2048)}), flush=True)
+        ctx.close()
+        return 0
     log("random-init weights (16.06 GB)")
     W = ModelWeights.random_init(seed=0, std=0.02)
     total = args.prompt + args.warmup + args.steps + 1
@@ -224,56 +290,7 @@ def main() -> int:
         torch.cuda.synchronize()
         pdt = (time.perf_counter() - t0) / reps
         del req2
-        gemms = {}
-        stream = ctx.stream
-        for name, epi, k, n in (("qkv", 0, HIDDEN, 6144), ("o", 1, HIDDEN, HIDDEN),
-                                ("gate_up", 3, HIDDEN, FFN), ("down", 1, FFN, HIDDEN)):
-            gx = (torch.randn(P, k, device="cuda") * 0.5).to(torch.bfloat16)
-            gw0 = (torch.randn(n, k, device="cuda") * 0.02).to(torch.bfloat16)
-            gw1 = (torch.randn(n, k, device="cuda") * 0.02).to(torch.bfloat16) if epi == 3 else gw0
-            gy = torch.zeros(P, n, dtype=torch.bfloat16, device="cuda")
-            torch.cuda.synchronize()
-
-            def run() -> None:
-                check(lib.ie_gemm_ex(ctx.handle, epi, P, k, n, ptr(gx), ptr(gw0), ptr(gw1), ptr(gy)))
-
-            # The clocks settle over the first ~0.1 s of sustained MFMA load (a cold launch runs
-            # 10-15 % slow), as they do inside a prefill's 32 back-to-back layers: warm up for
-            # 150 ms, then take the median of three timed runs of 10 launches.
-            t_end = time.perf_counter() + 0.15
-            while time.perf_counter() < t_end:
-                for _ in range(8):
-                    run()
-                torch.cuda.synchronize()
-            def timed(fn) -> float:
-                runs = []
-                for _ in range(3):
-                    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    g0.record(stream)
-                    for _ in range(10):
-                        fn()
-                    g1.record(stream)
-                    g1.synchronize()
-                    runs.append(g0.elapsed_time(g1) * 1e3 / 10)
-                return sorted(runs)[1]
-
-            us = timed(run)
-            flop = 2.0 * P * n * k * (2 if epi == 3 else 1)
-            tf = flop / (us * 1e-6) / 1e12
-            # the same product through torch.matmul (hipBLASLt), same protocol: gate and up as
-            # one [2 * 14336, 4096] weight, no fused epilogue
-            gw = torch.cat([gw0, gw1]) if epi == 3 else gw0
-            t_end = time.perf_counter() + 0.15
-            while time.perf_counter() < t_end:
-                for _ in range(8):
-                    torch.matmul(gx, gw.t())
-                torch.cuda.synchronize()
-            ref_us = timed(lambda: torch.matmul(gx, gw.t()))
-            gemms[name] = {"m": P, "n": n, "k": k, "us": round(us, 1), "tflops": round(tf, 1),
-                           "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                           "torch_matmul_us": round(ref_us, 1),
-                           "torch_matmul_tflops": round(flop / (ref_us * 1e-6) / 1e12, 1)}
-            del gx, gw0, gw1, gy, gw
+        gemms = prefill_gemms(ctx, P)
         flops = 2.0 * P * LAYER_GEMM_PARAMS * LAYERS
         prefill2048 = {"seq_len": P, "ms": round(pdt * 1e3, 2), "tokens_per_s": round(P / pdt, 1),
                        "layer_gemm_tflops_per_s": round(flops / pdt / 1e12, 1),
