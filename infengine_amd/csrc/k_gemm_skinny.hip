@@ -39,94 +39,152 @@ constexpr int kSkStep = 128;  // k per step
 // to 16 * 4 * kSsLoads = 256 producer workgroups.
 constexpr int kSsLoads = 4;
 
-__device__ __forceinline__ const uint16_t* skinny_w_row(const GemmParams& p, int R) {
-  if (R >= p.N) R = p.N - 1;
-  const int e0 = min(p.n0, p.N), e1 = min(p.n0 + p.n1, p.N);
-  if (R < e0) return p.w0 + (size_t)R * p.K;
-  if (R < e1) return p.w1 + (size_t)(R - e0) * p.K;
-  return p.w2 + (size_t)(R - e1) * p.K;
+constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw 32-bit access)
+
+// Operand sources of one workgroup: buffer resources whose byte ranges end at the last row the
+// tile may read (rows past a matrix end or past M read as zero; their outputs are not stored),
+// and per-lane 32-bit byte offsets of row 4j + q, 16-byte chunk r, of each source.
+struct SkSrc {
+  __amdgpu_buffer_rsrc_t w[2];  // the W tiles: the weight rows, or gate and up rows
+  __amdgpu_buffer_rsrc_t x;
+  uint32_t wo[4], xo[4];
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const uint16_t* base, int rows, int K) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, rows * K * 2, kBufferFlags);
 }
 
 // Loads of one step (k offset ks from each row start), 4 rows x 256 bytes per instruction: lane
-// (r, q) loads 16-byte chunk r of row 4j + q of each W tile and of the X rows.
+// (r, q) loads 16-byte chunk r of row 4j + q of each W tile, or of the X rows.
 template <int NT>
-__device__ __forceinline__ void sk_load(const uint16_t* const (&wp)[NT][4],
-                                        const uint16_t* const (&xp)[4], int ks, int r,
-                                        u32x4_t (&w)[NT][4], u32x4_t (&xv)[4]) {
+__device__ __forceinline__ void sk_load_w(const SkSrc& src, int ks, u32x4_t (&w)[NT][4]) {
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[t][j] = *reinterpret_cast<const u32x4_t*>(wp[t][j] + ks + 8 * r);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const u32x4_t*>(xp[j] + ks + 8 * r);
+    for (int j = 0; j < 4; ++j)
+      w[t][j] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src.w[t], src.wo[j], 2 * ks, 0));
 }
 
-// One step: the W and X rows through the wave's LDS tiles into the operand layout, then 4 MFMA
-// k-chunks per W tile (the MFMA's 32-k contraction of chunk c is k = 32c .. 32c+31 of the step
-// for both operands: chunk 4c + q of W row r and of X row r).
-template <int NT>
-__device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const u32x4_t (&w)[NT][4],
-                                        const u32x4_t (&xv)[4], int r, int q, f32x4_t (&acc)[NT]) {
+__device__ __forceinline__ void sk_load_x(const SkSrc& src, int ks, u32x4_t (&xv)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    xv[j] = __builtin_bit_cast(
+        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src.x, src.xo[j], 2 * ks, 0));
+}
+
+// One 16-row tile into a wave's LDS tile: row R's 16-byte chunk c goes to slot R*16 + (c ^ R).
+__device__ __forceinline__ void sk_put(u32x4_t* t, const u32x4_t (&v)[4], int r, int q) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int R = 4 * j + q;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) tr[t][R * 16 + (r ^ R)] = w[t][j];
-    tr[NT][R * 16 + (r ^ R)] = xv[j];
-  }
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const bf16x8_t xb = __builtin_bit_cast(bf16x8_t, tr[NT][r * 16 + ((4 * c + q) ^ r)]);
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          __builtin_bit_cast(bf16x8_t, tr[t][r * 16 + ((4 * c + q) ^ r)]), xb, acc[t], 0, 0, 0);
+    t[R * 16 + (r ^ R)] = v[j];
   }
 }
 
-// Steps s and s+1 from the two register buffers, each refilled with the step two ahead.
+// One step: the X rows (tr[1]) and each W tile in turn (tr[0]; the second W tile overwrites the
+// first once its fragments are read -- one wave's LDS operations run in order) through the
+// wave's LDS tiles into the operand layout, 4 MFMA k-chunks per W tile (the MFMA's 32-k
+// contraction of chunk c is k = 32c .. 32c+31 of the step for both operands: chunk 4c + q of W
+// row r and of X row r).  The X registers are refilled with step kx as soon as they are in LDS
+// (X is L2-resident: one step of lookahead hides it), the W registers with step kw once the last
+// W tile is in LDS.
 template <int NT>
-__device__ __forceinline__ void sk_pair(u32x4_t (*tr)[256], const uint16_t* const (&wp)[NT][4],
-                                        const uint16_t* const (&xp)[4], int kbase, int s,
+__device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const SkSrc& src, u32x4_t (&w)[NT][4],
+                                        u32x4_t (&xv)[4], int r, int q, f32x4_t (&acc)[NT],
+                                        bool lx, int kx, bool lw, int kw) {
+  sk_put(tr[0], w[0], r, q);
+  sk_put(tr[1], xv, r, q);
+  if (lx) sk_load_x(src, kx, xv);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (t > 0) sk_put(tr[0], w[t], r, q);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8_t, tr[0][r * 16 + ((4 * c + q) ^ r)]),
+          __builtin_bit_cast(bf16x8_t, tr[1][r * 16 + ((4 * c + q) ^ r)]), acc[t], 0, 0, 0);
+  }
+  if (lw) sk_load_w<NT>(src, kw, w);
+}
+
+// Steps s and s+1 from the two W register buffers, each refilled with the step two ahead; X
+// one step ahead.
+template <int NT>
+__device__ __forceinline__ void sk_pair(u32x4_t (*tr)[256], const SkSrc& src, int kbase, int s,
                                         int steps, int r, int q, u32x4_t (&w0)[NT][4],
-                                        u32x4_t (&x0)[4], u32x4_t (&w1)[NT][4], u32x4_t (&x1)[4],
+                                        u32x4_t (&w1)[NT][4], u32x4_t (&xv)[4],
                                         f32x4_t (&acc)[NT]) {
-  sk_step<NT>(tr, w0, x0, r, q, acc);
-  if (s + 2 < steps) sk_load<NT>(wp, xp, kbase + (s + 2) * kSkStep, r, w0, x0);
-  sk_step<NT>(tr, w1, x1, r, q, acc);
-  if (s + 3 < steps) sk_load<NT>(wp, xp, kbase + (s + 3) * kSkStep, r, w1, x1);
+  const int k1 = kbase + (s + 1) * kSkStep;
+  sk_step<NT>(tr, src, w0, xv, r, q, acc, s + 1 < steps, k1, s + 2 < steps, k1 + kSkStep);
+  __builtin_amdgcn_sched_barrier(0);
+  sk_step<NT>(tr, src, w1, xv, r, q, acc, s + 2 < steps, k1 + kSkStep, s + 3 < steps,
+              k1 + 2 * kSkStep);
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // KC: K fixed at compile time (4096 or 14336; the step loop then unrolls fully), 0: at run time.
+// At most 128 VGPRs (fixed K) and 32 KiB of LDS: 4 workgroups per CU, so the 896 workgroups of
+// the gate/up projection are all resident at once (the same speed, measured, as 2 per CU).
 template <int EPI, int KC>
-__global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p) {
+__global__ __launch_bounds__(kSkSplit * 64) __attribute__((amdgpu_waves_per_eu(KC > 0 ? 4 : 1)))
+void gemm_skinny_kernel(GemmParams p) {
   constexpr bool SW = EPI == kGemmSwiglu;
   constexpr int NT = SW ? 2 : 1;  // 16-row W tiles: the weight rows, or gate and up rows
-  __shared__ u32x4_t tr[kSkSplit][NT + 1][256];  // per wave: the W tiles and the X rows
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ u32x4_t tr[kSkSplit][2][256];  // per wave: a W tile and the X rows
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int n0 = blockIdx.x * kSkRows;
   const int K = KC > 0 ? KC : p.K;
 
-  // row 4j + q of each tile (rows past N repeat the last row; their outputs are not stored)
-  const uint16_t* wp[NT][4];
+  SkSrc src;
+  // row offset of tile row 4j + q within the W source
+  int wrow[4];
+  if constexpr (EPI == kGemmQkvRope) {
+    // head b / 8 of the [q|k|v] rows; the tile's rows are pairs 8 (b % 8) .. +7, first halves
+    // (rows 0..7) then second halves (rows 8..15, 64 rows further on)
+    const int head = blockIdx.x >> 3, pr = (blockIdx.x & 7) * 8;
+    const uint16_t* base = head < kQHeads ? p.w0 + (size_t)head * kHeadDim * K
+                           : head < kQHeads + kKVHeads
+                               ? p.w1 + (size_t)(head - kQHeads) * kHeadDim * K
+                               : p.w2 + (size_t)(head - kQHeads - kKVHeads) * kHeadDim * K;
+    src.w[0] = sk_rsrc(base, kHeadDim, K);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int R = 4 * j + q;
+      wrow[j] = pr + (R & 7) + 64 * (R >> 3);
+    }
+  } else {
+    if constexpr (SW) {
+      const int rows = min(kSkRows, p.N - n0);
+      src.w[0] = sk_rsrc(p.w0 + (size_t)n0 * K, rows, K);  // gate
+      src.w[1] = sk_rsrc(p.w1 + (size_t)n0 * K, rows, K);  // up
+    } else {
+      // the weight matrix holding the tile (the launch keeps tiles inside one matrix)
+      const int e0 = min(p.n0, p.N), e1 = min(p.n0 + p.n1, p.N);
+      const uint16_t* base;
+      int end;
+      if (n0 < e0) base = p.w0 + (size_t)n0 * K, end = e0;
+      else if (n0 < e1) base = p.w1 + (size_t)(n0 - e0) * K, end = e1;
+      else base = p.w2 + (size_t)(n0 - e1) * K, end = p.N;
+      src.w[0] = sk_rsrc(base, min(kSkRows, end - n0), K);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wrow[j] = 4 * j + q;
+  }
+  src.x = sk_rsrc(p.x, p.M, K);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if constexpr (EPI == kGemmQkvRope) {
-      const int R = 4 * j + q;
-      wp[0][j] = skinny_w_row(p, (blockIdx.x >> 3) * kHeadDim + (blockIdx.x & 7) * 8 + (R & 7) + 64 * (R >> 3));
-    } else if constexpr (SW) {
-      const int col = min(n0 + 4 * j + q, p.N - 1);
-      wp[0][j] = p.w0 + (size_t)col * K;  // gate
-      wp[NT - 1][j] = p.w1 + (size_t)col * K;  // up
-    } else {
-      wp[0][j] = skinny_w_row(p, n0 + 4 * j + q);
-    }
+    src.wo[j] = (uint32_t)(wrow[j] * K + 8 * r) * 2u;
+    src.xo[j] = (uint32_t)((4 * j + q) * K + 8 * r) * 2u;
   }
-  // X row 4j + q (rows past M repeat the last row; their outputs are not stored)
-  const uint16_t* xp[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) xp[j] = p.x + (size_t)min(4 * j + q, p.M - 1) * K;
+  // kept as per-lane values: folding a row's uniform part into the scalar offset would take it
+  // out of the buffer range check on the rows past the matrix end
+  asm volatile("" : "+v"(src.wo[0]), "+v"(src.wo[1]), "+v"(src.wo[2]), "+v"(src.wo[3]));
+  asm volatile("" : "+v"(src.xo[0]), "+v"(src.xo[1]), "+v"(src.xo[2]), "+v"(src.xo[3]));
+  // wave w takes K quarter w (interleaving the waves' steps, so that the 4 waves read 1 KiB runs
+  // of each row together, measured 4-6% slower)
   const int kq = K / kSkSplit;
   const int kbase = wave * kq;
   const int steps = kq / kSkStep;
@@ -134,9 +192,10 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
   f32x4_t acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // two register buffers: step s is multiplied while step s+1 is in flight, then buffer s % 2
-  // is refilled with step s+2
-  u32x4_t w0[NT][4], x0[4], w1[NT][4], x1[4];
+  // two W register buffers: step s is multiplied while step s+1 is in flight, then buffer s % 2
+  // is refilled with step s+2; the X rows of step s+1 are loaded during step s, ahead of the W
+  // rows of step s+2 (loads return in issue order)
+  u32x4_t w0[NT][4], w1[NT][4], xv[4];
   // folded RMSNorm: the rows' sums of squares from the producer's partials, [16][ss_parts] (a
   // multiple of 4).  Loaded before the first weight loads and summed after them: loads return in
   // issue order, so waiting for these does not wait for the weights.
@@ -153,8 +212,9 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  sk_load<NT>(wp, xp, kbase, r, w0, x0);
-  if (steps > 1) sk_load<NT>(wp, xp, kbase + kSkStep, r, w1, x1);
+  sk_load_w<NT>(src, kbase, w0);
+  sk_load_x(src, kbase, xv);
+  if (steps > 1) sk_load_w<NT>(src, kbase + kSkStep, w1);
   __builtin_amdgcn_sched_barrier(0);
   if (norm) {
     float sum = 0.f;
@@ -168,24 +228,24 @@ __global__ __launch_bounds__(kSkSplit * 64) void gemm_skinny_kernel(GemmParams p
   if constexpr (KC > 0) {
 #pragma unroll
     for (; s + 1 < KC / kSkSplit / kSkStep; s += 2)
-      sk_pair<NT>(tr[wave], wp, xp, kbase, s, steps, r, q, w0, x0, w1, x1, acc);
+      sk_pair<NT>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc);
   } else {
     for (; s + 1 < steps; s += 2)
-      sk_pair<NT>(tr[wave], wp, xp, kbase, s, steps, r, q, w0, x0, w1, x1, acc);
+      sk_pair<NT>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc);
   }
-  if (s < steps) sk_step<NT>(tr[wave], w0, x0, r, q, acc);
+  if (s < steps) sk_step<NT>(tr[wave], src, w0, xv, r, q, acc, false, 0, false, 0);
   f32x4_t acc0 = acc[0], acc1 = acc[NT - 1];
 
-  // sum the K quarters: waves 1..3 hand their tiles to wave 0
-  __shared__ f32x4_t red[kSkSplit][SW ? 2 : 1][64];
-  red[wave][0][lane] = acc0;
-  if constexpr (SW) red[wave][SW ? 1 : 0][lane] = acc1;
+  // sum the K quarters: waves 1..3 hand their tiles to wave 0 through their own W tile slots
+  // (each wave's last reads of its slot precede these writes)
+  tr[wave][0][lane] = __builtin_bit_cast(u32x4_t, acc0);
+  if constexpr (SW) tr[wave][0][64 + lane] = __builtin_bit_cast(u32x4_t, acc1);
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int w = 1; w < kSkSplit; ++w) {
-    acc0 += red[w][0][lane];
-    if constexpr (SW) acc1 += red[w][SW ? 1 : 0][lane];
+    acc0 += __builtin_bit_cast(f32x4_t, tr[w][0][lane]);
+    if constexpr (SW) acc1 += __builtin_bit_cast(f32x4_t, tr[w][0][64 + lane]);
   }
 
   const int m = r, n = n0 + 4 * q;
@@ -301,6 +361,7 @@ int launch_s(const GemmParams& p, hipStream_t st) {
   return IE_OK;
 }
 
+
 }  // namespace
 
 bool gemm_skinny_fits(const GemmParams& p) {
@@ -317,14 +378,23 @@ int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {
   IE_REQUIRE(!p.ss_out || (epi == kGemmResid && p.xw_out && p.xw_norm && p.N % 16 == 0),
              "gemm_skinny: the norm-preparing output is a residual-epilogue option");
   switch (epi) {
-    case kGemmBf16: return launch_s<kGemmBf16>(p, st);
-    case kGemmResid: return launch_s<kGemmResid>(p, st);
-    case kGemmF32: return launch_s<kGemmF32>(p, st);
     case kGemmSwiglu: return launch_s<kGemmSwiglu>(p, st);
     case kGemmQkvRope: return launch_s<kGemmQkvRope>(p, st);
+    case kGemmBf16:
+    case kGemmResid:
+    case kGemmF32: break;
+    default:
+      set_error("gemm_skinny: bad epilogue %d", epi);
+      return IE_ERR_INVALID_ARG;
   }
-  set_error("gemm_skinny: bad epilogue %d", epi);
-  return IE_ERR_INVALID_ARG;
+  // a workgroup's 16 rows are read from one weight matrix
+  const int e0 = std::min(p.n0, p.N), e1 = std::min(p.n0 + p.n1, p.N);
+  IE_REQUIRE((e0 == p.N || e0 % kSkRows == 0) && (e1 == p.N || e1 % kSkRows == 0),
+             "gemm_skinny: weight matrix boundaries must fall on multiples of %d rows (n0=%d n1=%d)",
+             kSkRows, p.n0, p.n1);
+  if (epi == kGemmResid) return launch_s<kGemmResid>(p, st);
+  if (epi == kGemmF32) return launch_s<kGemmF32>(p, st);
+  return launch_s<kGemmBf16>(p, st);
 }
 
 }  // namespace ie
