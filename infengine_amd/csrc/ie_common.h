@@ -87,11 +87,14 @@ __host__ __device__ __forceinline__ uint16_t f2bf(float f) {
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-}
-
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to bf16 in one gfx950 v_cvt_pk_bf16_f32 (round to nearest even, as f2bf; NaN becomes
+// a quiet NaN).
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
 
 // acc + a.lo*b.lo + a.hi*b.hi on the gfx950 dot2 unit (bf16 inputs, fp32 accumulate)
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {

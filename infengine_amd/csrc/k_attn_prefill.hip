@@ -58,6 +58,63 @@ __device__ __forceinline__ void issue_tile(u32x4_t* lds, __amdgpu_buffer_rsrc_t 
   }
 }
 
+// Online softmax of one tile's scores for the wave's 32 query columns (each spread over lanes fr,
+// fr+16, fr+32, fr+48): s[qi][kb][r] = S[q = q0 + 16 qi][key = key0 + 16 kb + 4 G + r] (raw,
+// unscaled).  p = exp((s - m) / sqrt(128)) as one fma and one exp2 per score (the measured
+// alternative, rescaling o only when some lane's max grew by 2^8, was 8% slower: the wave-uniform
+// branch costs more than the 64 multiplies it skips); MASK applies the causal and end-of-keys
+// mask (key <= q, key < nkeys).  Rescales l and o by the max's change and
+// packs P^T as the P.V MFMA's B operand: contraction slot 8 G + r <-> key 32 ks2 + 4 G + r, slot
+// 8 G + 4 + r <-> key 32 ks2 + 16 + 4 G + r.
+template <bool MASK>
+__device__ __forceinline__ void softmax_tile(f32x4_t (&s)[2][4], float (&m)[2], float (&l)[2],
+                                             f32x4_t (&o)[2][8], bf16x8_t (&pb)[2][2], int key0,
+                                             int q0, int nkeys, int G) {
+  constexpr float c = 0.08838834764831845f * 1.4426950408889634f;  // 1/sqrt(128) (softmax.cu:79) * log2(e)
+#pragma unroll
+  for (int qi = 0; qi < 2; ++qi) {
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (MASK) {
+          const int key = key0 + 16 * kb + 4 * G + r;
+          if (!(key <= q0 + 16 * qi && key < nkeys)) s[qi][kb][r] = -INFINITY;
+        }
+        mt = fmaxf(mt, s[qi][kb][r]);
+      }
+    mt = xor32_max(xor16_max(mt));
+    // a query row whose keys in this tile are all masked keeps mn = m (finite after its first
+    // tile, which always holds key 0)
+    const float mn = fmaxf(m[qi], mt);
+    const float nb = -mn * c;
+    const float alpha = __builtin_amdgcn_exp2f(fmaf(m[qi], c, nb));  // m = -inf: 0
+    float ls = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(s[qi][kb][r], c, nb));
+        s[qi][kb][r] = e;
+        ls += e;
+      }
+    ls = xor32_sum(xor16_sum(ls));
+    l[qi] = l[qi] * alpha + ls;
+    m[qi] = mn;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) o[qi][db] *= alpha;
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      const u32x4_t w = {pack_bf2(s[qi][2 * ks2][0], s[qi][2 * ks2][1]),
+                         pack_bf2(s[qi][2 * ks2][2], s[qi][2 * ks2][3]),
+                         pack_bf2(s[qi][2 * ks2 + 1][0], s[qi][2 * ks2 + 1][1]),
+                         pack_bf2(s[qi][2 * ks2 + 1][2], s[qi][2 * ks2 + 1][3])};
+      pb[qi][ks2] = __builtin_bit_cast(bf16x8_t, w);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams p) {
   __shared__ u32x4_t lds[2 * 2 * TC];  // [stage][K | V][key][16 chunks], 64 KiB
 
@@ -104,8 +161,8 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
   for (int qi = 0; qi < 2; ++qi)
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[qi][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // m: running max of the raw scores (the scale is applied inside the exponent)
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  const float scale = 0.08838834764831845f;  // 1/sqrt(128), softmax.cu:79
 
   issue_tile(lds, krs, vrs, voff, wv, 0, 0);
   for (int t = 0; t < ntiles; ++t) {
@@ -130,51 +187,12 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
       }
     }
 
-    // ---- online softmax per query column (spread over lanes fr, fr+16, fr+32, fr+48)
+    // ---- online softmax; causal masking only on the tiles that reach past the block's first query
     bf16x8_t pb[2][2];
-#pragma unroll
-    for (int qi = 0; qi < 2; ++qi) {
-      const int q_abs = p.start_pos + row0 + 16 * qi + fr;
-      float mt = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = key0 + 16 * kb + 4 * G + r;
-          const float v = (key <= q_abs && key < nkeys) ? s[qi][kb][r] * scale : -INFINITY;
-          s[qi][kb][r] = v;
-          mt = fmaxf(mt, v);
-        }
-      mt = xor32_max(xor16_max(mt));
-      // a query row whose keys in this tile are all masked keeps mn = m (finite after its
-      // first tile, which always holds key 0)
-      const float mn = fmaxf(m[qi], mt);
-      const float alpha = __expf(m[qi] - mn);
-      float ls = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float e = __expf(s[qi][kb][r] - mn);
-          s[qi][kb][r] = e;
-          ls += e;
-        }
-      ls = xor32_sum(xor16_sum(ls));
-      l[qi] = l[qi] * alpha + ls;
-      m[qi] = mn;
-#pragma unroll
-      for (int db = 0; db < 8; ++db) o[qi][db] *= alpha;
-      // P^T fragments: contraction slot 8 G + r <-> key 32 ks2 + 4 G + r,
-      //                slot 8 G + 4 + r <-> key 32 ks2 + 16 + 4 G + r
-#pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2) {
-        const u32x4_t w = {pack_bf2(s[qi][2 * ks2][0], s[qi][2 * ks2][1]),
-                           pack_bf2(s[qi][2 * ks2][2], s[qi][2 * ks2][3]),
-                           pack_bf2(s[qi][2 * ks2 + 1][0], s[qi][2 * ks2 + 1][1]),
-                           pack_bf2(s[qi][2 * ks2 + 1][2], s[qi][2 * ks2 + 1][3])};
-        pb[qi][ks2] = __builtin_bit_cast(bf16x8_t, w);
-      }
-    }
+    if (key0 + BKEY - 1 <= p.start_pos + row0)
+      softmax_tile<false>(s, m, l, o, pb, key0, p.start_pos + row0 + fr, nkeys, G);
+    else
+      softmax_tile<true>(s, m, l, o, pb, key0, p.start_pos + row0 + fr, nkeys, G);
 
     // ---- O^T[d][q] += V^T[d][keys] . P^T[keys][q]; the V^T fragment of dims 16 db .. +15 and
     //      the slot order above is two transposed 8-byte reads per lane
