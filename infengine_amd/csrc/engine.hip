@@ -120,7 +120,11 @@ int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs&
   a.part_ml = w.part_ml;
   a.d_seq_len = d_seq_len;
   a.seq_len = seq_len;
-  a.max_splits = max_len <= kAttnFusedMaxCtx ? kAttnFusedSplits : kAttnSplits;
+  // batched: 16 x 8 (sequence, kv head) workgroups already fill the chip, so up to
+  // kAttnDirectMaxCtx one split per pair writes the output (no merge launch)
+  a.max_splits = (batch > 1 && merge && max_len <= kAttnDirectMaxCtx) ? 1
+                 : max_len <= kAttnFusedMaxCtx                        ? kAttnFusedSplits
+                                                                     : kAttnSplits;
   IE_REQUIRE(merge || a.max_splits == kAttnFusedSplits,
              "attn_decode: contexts past %d need the merge kernel", kAttnFusedMaxCtx);
   return launch_attn_decode(a, batch, merge, st);

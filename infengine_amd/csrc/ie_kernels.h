@@ -55,7 +55,8 @@ struct AttnDecodeParams {
   float* part_ml;           // [batch][8][splits][4][2]
   const int* d_seq_len;     // [batch] device seq lens, or nullptr
   int seq_len;              // used when d_seq_len == nullptr (batch must be 1)
-  int max_splits;           // splits per kv head cap: kAttnFusedSplits or kAttnSplits
+  int max_splits;           // splits per kv head cap: kAttnFusedSplits or kAttnSplits (1: the
+                            // kernel writes the normalised bf16 output itself)
 };
 // Splits per (sequence, kv head) for a context of ntiles 64-row tiles: four tiles per split
 // (one per wave of the split workgroup) up to the cap.  Device and host must agree on it.
@@ -69,6 +70,7 @@ __host__ __device__ inline int attn_decode_splits(int ntiles, int max_splits) {
 // per decode step than 8 at p = 600 (and 4% on the bs=16 batched step).
 constexpr int kAttnFusedSplits = 4;
 constexpr int kAttnFusedMaxCtx = 4096;  // beyond: merge kernel + up to kAttnSplits splits
+constexpr int kAttnDirectMaxCtx = 2048; // batched contexts up to this: one split, output written directly
 // merge = also launch the merge kernel (bf16 output in p.out)
 int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStream_t st);
 size_t attn_decode_partials_bytes(int batch);

@@ -46,13 +46,14 @@ __device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r &
 
 static_assert(kAttnSplits <= 64, "the merge gives each split one lane");
 
-// Phase 1: split s of (batch b, kv head g) attends its run of tiles and writes the
-// unnormalised partial (m, l, o) of each of the 4 q heads.  KREG: K fragments are loaded
-// straight into registers (72 KiB of LDS per workgroup, two workgroups per CU: the batched
-// grid); otherwise K goes through LDS like V (136 KiB, one workgroup per CU; measured 0.7%
-// faster per decode step at batch 1).
-template <bool KREG>
-__global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(AttnDecodeParams p) {
+// Phase 1: split s of (batch b, kv head g) attends its run of tiles (its NW waves take every
+// NW-th tile) and writes the unnormalised partial (m, l, o) of each of the 4 q heads; with one
+// split (max_splits = 1, batched, NW = 8) it writes the normalised bf16 output instead.  KREG: K
+// fragments are loaded straight into registers (72 KiB of LDS per 4-wave workgroup, two
+// workgroups per CU: the batched grid); otherwise K goes through LDS like V (136 KiB, one
+// workgroup per CU; measured 0.7% faster per decode step at batch 1).
+template <bool KREG, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodeParams p) {
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int fr = lane & 15, G = lane >> 4;
@@ -63,9 +64,9 @@ __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(Att
   const int tps = (ntiles + ns - 1) / ns;
   const int t0 = split * tps, t1 = min(ntiles, t0 + tps);
 
-  __shared__ u32x4_t kvlds[kSplitWaves][KREG ? 1 : 2][kTC];  // per wave: (K tile,) V tile
-  __shared__ float xo[kSplitWaves][kGQA][kHeadDim];
-  __shared__ float xml[kSplitWaves][kGQA][2];
+  __shared__ u32x4_t kvlds[NW][KREG ? 1 : 2][kTC];  // per wave: (K tile,) V tile
+  __shared__ float xo[NW][kGQA][kHeadDim];
+  __shared__ float xml[NW][kGQA][2];
   const uint16_t* Kh = p.k_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
   const uint16_t* Vh = p.v_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
   // rows past S read as zero (buffer bounds) and are masked below
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(Att
   u32x4_t* kt = kvlds[wave][0];
   u32x4_t* vt = kvlds[wave][KREG ? 0 : 1];
 
-  for (int t = t0 + wave; t < t1; t += kSplitWaves) {
+  for (int t = t0 + wave; t < t1; t += NW) {
     // K fragments kk[kb][ks] = K[key0 + 16 kb + fr][32 ks + 8 G .. +8], straight from memory
     // (KREG) or from the LDS tile below
     const int key0 = t * kAttnTile;
@@ -209,18 +210,26 @@ __global__ __launch_bounds__(kSplitWaves * 64) void attn_decode_split_kernel(Att
     }
   }
   __syncthreads();
+  if (wave >= kGQA) return;  // (NW = 8) waves past the 4 q heads only contribute partials
   const int h = wave;  // wave h merges q head 4g + h; lane d owns dims 2d, 2d+1
-  const float mw = lane < kSplitWaves ? xml[lane][h][0] : -INFINITY;
-  const float lw = lane < kSplitWaves ? xml[lane][h][1] : 0.f;
+  const float mw = lane < NW ? xml[lane][h][0] : -INFINITY;
+  const float lw = lane < NW ? xml[lane][h][1] : 0.f;
   const float M = wave_max(mw);
   const float wl = lw > 0.f ? __expf(mw - M) : 0.f;
   const float L = wave_sum(lw * wl);
   float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-  for (int w = 0; w < kSplitWaves; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const float ww = readlane_f(wl, w);
     o0 = fmaf(xo[w][h][2 * lane], ww, o0);
     o1 = fmaf(xo[w][h][2 * lane + 1], ww, o1);
+  }
+  if (p.max_splits == 1) {
+    // one split: the merged result is final (attn.cu:433-438), no partials
+    const float inv = 1.0f / L;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(p.out + ((size_t)b * kQHeads + g * kGQA + h) * kHeadDim);
+    dst[lane] = pack_bf2(o0 * inv, o1 * inv);
+    return;
   }
   const size_t slot = (((size_t)b * kKVHeads + g) * kAttnSplits + split) * kGQA + h;
   *reinterpret_cast<float2*>(p.part_o + slot * kHeadDim + 2 * lane) = make_float2(o0, o1);
@@ -280,16 +289,20 @@ int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStre
              "attn_decode: seq_len %d out of range [1,%d]", p.seq_len, kMaxCtx);
   IE_REQUIRE(p.max_splits >= 1 && p.max_splits <= kAttnSplits, "attn_decode: max_splits %d",
              p.max_splits);
+  IE_REQUIRE(p.max_splits > 1 || (merge && p.out), "attn_decode: one split writes the output");
   // one workgroup per possible split: idle ones would still cost dispatch (at batch 16 and
   // 32 splits, 4096 mostly empty workgroups took 52 us)
-  if (batch > 1)
-    hipLaunchKernelGGL(attn_decode_split_kernel<true>, dim3(p.max_splits, kKVHeads, batch),
-                       dim3(kSplitWaves * 64), 0, st, p);
+  if (batch > 1 && p.max_splits == 1)  // one workgroup per (sequence, kv head): 8 waves share its tiles
+    hipLaunchKernelGGL((attn_decode_split_kernel<true, 8>), dim3(1, kKVHeads, batch), dim3(8 * 64), 0,
+                       st, p);
+  else if (batch > 1)
+    hipLaunchKernelGGL((attn_decode_split_kernel<true, kSplitWaves>),
+                       dim3(p.max_splits, kKVHeads, batch), dim3(kSplitWaves * 64), 0, st, p);
   else
-    hipLaunchKernelGGL(attn_decode_split_kernel<false>, dim3(p.max_splits, kKVHeads, batch),
-                       dim3(kSplitWaves * 64), 0, st, p);
+    hipLaunchKernelGGL((attn_decode_split_kernel<false, kSplitWaves>),
+                       dim3(p.max_splits, kKVHeads, batch), dim3(kSplitWaves * 64), 0, st, p);
   IE_CHECK_LAUNCH();
-  if (merge) {
+  if (merge && p.max_splits > 1) {
     IE_REQUIRE(p.out, "attn_decode: merge needs an output buffer");
     hipLaunchKernelGGL(attn_decode_merge_kernel, dim3(kKVHeads, batch), dim3(256), 0, st, p);
     IE_CHECK_LAUNCH();
