@@ -209,10 +209,12 @@ def test_prefill_then_decode_vs_oracle(hip, model, oracle_model, noise_floor):
     assert_close(got3, got2, tol=tol, what="prefill(S+1) vs prefill(S)+decode")
 
 
-def test_batched_decode_matches_single(hip, model, noise_floor):
+# contexts up to 2048 take the one-workgroup-per-(sequence, kv head) attention; a longer one
+# takes split + merge
+@pytest.mark.parametrize("lens", [[101, 257, 64], [2100, 257, 64]])
+def test_batched_decode_matches_single(hip, model, noise_floor, lens):
     from infengine_amd.engine import Context, Request, ptr
-    B = 3
-    lens = [101, 257, 64]
+    B = len(lens)
     say(f"decode_step_batched B={B} lens={lens}")
     c = Context(0, graph=False)
     kvsz = hip.lib.ie_kv_cache_size()
