@@ -14,6 +14,8 @@ Also reported, on the same run:
                 the 256 MB Infinity Cache cannot serve repeats.
   batched       config 5's bs=16 leg: 16 independent sequences (staggered contexts
                 from prompt_len+1) per ie_decode_step_batched, tokens/s and GB/s.
+  batched_paged the same leg over a paged KV pool (ie_decode_step_batched_paged, each
+                sequence's 64-position blocks on shuffled pages).
   prefill_2048  config 4: a 2048-token prefill of the full model (mean of 3 after three
                 untimed calls), and the four prefill GEMM shapes at M = 2048 (QKV, O with
                 residual, gate/up with SwiGLU, down with residual) timed with HIP events
@@ -235,7 +237,7 @@ def main() -> int:
     step_gbps = (WEIGHT_BYTES_PER_TOKEN + kv_bytes) / (dt / args.steps) / 1e9
 
     # ---- batched decode (config 5): 16 independent sequences per step, one KV cache each
-    batched = None
+    batched = batched_paged = None
     if args.batch > 1:
         B = args.batch
         log(f"batched decode B={B}")
@@ -246,31 +248,51 @@ def main() -> int:
         blogits = torch.zeros(B, VOCAB, dtype=torch.float32, device="cuda")
         bout = torch.zeros(B, dtype=torch.int32, device="cuda")
         bws = torch.zeros(lib.ie_batch_workspace_size(B), dtype=torch.uint8, device="cuda")
-        lens = [args.prompt + 1 + b for b in range(B)]     # staggered contexts
         th = (C.c_int * B)()
+        # the same leg on a paged KV pool: each sequence's 64-position blocks on pages in a
+        # shuffled order (ie_decode_step_batched_paged)
+        last = args.prompt + B + 4 + args.batch_steps
+        nblk = (last + 63) // 64
+        pool = torch.zeros(B * nblk * lib.ie_kv_page_size() // 2, dtype=torch.int16, device="cuda")
+        table = torch.from_numpy(np.random.default_rng(7).permutation(B * nblk).astype(np.int32)
+                                 .reshape(B, nblk)).cuda()
 
-        def bstep() -> None:
-            seq = (C.c_int * B)(*lens)
-            check(lib.ie_decode_step_batched(ctx.handle, W.ref(), B, seq, ptr(toks), ptr(bdata),
-                                             ptr(battn), ptr(blogits), ptr(bout), th, ptr(bws),
-                                             ptr(kvs)))
-            for b in range(B):
-                lens[b] += 1
+        def run_leg(paged: bool) -> dict:
+            lens = [args.prompt + 1 + b for b in range(B)]     # staggered contexts
 
-        for _ in range(4):
-            bstep()
-        torch.cuda.synchronize()
-        kv_b = KV_BYTES_PER_POS * sum(lens)
-        t0 = time.perf_counter()
-        for _ in range(args.batch_steps):
-            bstep()
-        torch.cuda.synchronize()
-        bdt = (time.perf_counter() - t0) / args.batch_steps
-        kv_b = (kv_b + KV_BYTES_PER_POS * sum(lens)) / 2          # mean over the timed steps
-        batched = {"batch": B, "steps": args.batch_steps, "tokens_per_s": round(B / bdt, 1),
-                   "ms_per_step": round(bdt * 1e3, 4),
-                   "step_GBps": round((WEIGHT_BYTES_PER_TOKEN + kv_b) / bdt / 1e9, 1),
-                   "contexts": [args.prompt + 5, lens[-1]]}
+            def bstep() -> None:
+                seq = (C.c_int * B)(*lens)
+                if paged:
+                    check(lib.ie_decode_step_batched_paged(
+                        ctx.handle, W.ref(), B, seq, ptr(toks), ptr(bdata), ptr(battn),
+                        ptr(blogits), ptr(bout), th, ptr(bws), ptr(pool), B * nblk, ptr(table),
+                        nblk))
+                else:
+                    check(lib.ie_decode_step_batched(ctx.handle, W.ref(), B, seq, ptr(toks),
+                                                     ptr(bdata), ptr(battn), ptr(blogits),
+                                                     ptr(bout), th, ptr(bws), ptr(kvs)))
+                for b in range(B):
+                    lens[b] += 1
+
+            for _ in range(4):
+                bstep()
+            torch.cuda.synchronize()
+            kv_b = KV_BYTES_PER_POS * sum(lens)
+            t0 = time.perf_counter()
+            for _ in range(args.batch_steps):
+                bstep()
+            torch.cuda.synchronize()
+            bdt = (time.perf_counter() - t0) / args.batch_steps
+            kv_b = (kv_b + KV_BYTES_PER_POS * sum(lens)) / 2          # mean over the timed steps
+            return {"batch": B, "steps": args.batch_steps, "tokens_per_s": round(B / bdt, 1),
+                    "ms_per_step": round(bdt * 1e3, 4),
+                    "step_GBps": round((WEIGHT_BYTES_PER_TOKEN + kv_b) / bdt / 1e9, 1),
+                    "contexts": [args.prompt + 5, lens[-1]]}
+
+        batched = run_leg(False)
+        log(f"batched decode B={B}, paged KV")
+        batched_paged = run_leg(True)
+        del pool, table
         del kvs, toks, bdata, battn, blogits, bout, bws
 
     # ---- config 4: 2048-token prefill, and its four GEMM shapes against the MFMA peak
@@ -340,6 +362,7 @@ def main() -> int:
         "prefill": {"seq_len": args.prompt, "ms": round(prefill_s * 1e3, 2),
                     "tokens_per_s": round(args.prompt / prefill_s, 1)},
         "batched": batched,
+        "batched_paged": batched_paged,
         "prefill_2048": prefill2048,
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4096, SwiGLU, RMSNorm> (gate/up)",
                      "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

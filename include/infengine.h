@@ -147,6 +147,23 @@ IE_API int ie_decode_step_batched(ie_context* ctx, const ie_model_weights* weigh
                                   float* output_distr, int* output_tokens, int* tokens_out,
                                   void* workspace, void* kv_caches);
 
+/* Paged KV cache for the batched step (no reference counterpart; the step toward a
+ * paged cache that manager.h:19-24's per-request RequestContext leads to).  A page
+ * holds 64 positions of every layer, [32 layers][K|V][8 kv heads][64][128] bf16
+ * (ie_kv_page_size() = 8 MiB); kv_pages is a pool of n_pages pages.  block_tables
+ * is a DEVICE int array [batch][table_stride]: entry i of row b is the page that
+ * holds positions 64*i .. 64*i+63 of sequence b; entries 0 .. (seq_lens[b]-1)/64
+ * must be set (the step writes the new K/V row at position seq_lens[b]-1).  Page
+ * ids outside [0, n_pages) read as zero and are not written.  Results are
+ * bit-identical to ie_decode_step_batched on the same rows. */
+IE_API size_t ie_kv_page_size(void);
+IE_API int ie_decode_step_batched_paged(ie_context* ctx, const ie_model_weights* weights,
+                                        int batch, const int* seq_lens, int* tokenid_buffs,
+                                        ie_bf16* data_buffer, ie_bf16* attn_buffer,
+                                        float* output_distr, int* output_tokens, int* tokens_out,
+                                        void* workspace, void* kv_pages, int n_pages,
+                                        const int* block_tables, int table_stride);
+
 /* ---- weights (model_weights.cu:142-172) ---- */
 /* Random-init Llama-3.1-8B: matrices ~N(0,std), norms ~1+N(0,0.02), rope tables. */
 IE_API int ie_model_weights_random_init(ie_model_weights* out, uint64_t seed, float std);

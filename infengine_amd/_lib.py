@@ -76,6 +76,9 @@ SIGNATURES: dict[str, tuple] = {
     "ie_batch_workspace_size": (_sz, [_i]),
     "ie_decode_step_batched": (_i, [_p, _W, _i, C.POINTER(_i), _p, _p, _p, _p, _p,
                                     C.POINTER(_i), _p, _p]),
+    "ie_kv_page_size": (_sz, []),
+    "ie_decode_step_batched_paged": (_i, [_p, _W, _i, C.POINTER(_i), _p, _p, _p, _p, _p,
+                                          C.POINTER(_i), _p, _p, _i, _p, _i]),
     "ie_model_weights_random_init": (_i, [_W, _u64, _f]),
     "ie_model_weights_from_safetensors": (_i, [_W, C.POINTER(C.c_char_p), _i]),
     "ie_model_weights_free": (_i, [_W]),

@@ -107,14 +107,19 @@ int qkv_rope_gemv(const ie_layer& L, const ie_rope_weights& rope, const uint16_t
 // merge: also write the bf16 attention output to `out` (merge kernel); otherwise only the
 // partials are written, for an O projection that merges them.  max_len: host-known bound on
 // the context lengths; beyond kAttnFusedMaxCtx the splits go up to kAttnSplits (merge only).
+// Paged KV (block_table set): kvl is the layer's base inside page 0, n_pages the pool size.
 int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs& w,
                 const int* d_seq_len, int seq_len, int max_len, int batch, long long cache_stride,
-                bool merge, hipStream_t st) {
+                bool merge, hipStream_t st, const int* block_table = nullptr, int table_stride = 0,
+                int n_pages = 0) {
   AttnDecodeParams a{};
   a.q = q;
   a.k_cache = kvl;
-  a.v_cache = kvl + (size_t)kKVHeads * kKVPlane;
+  a.v_cache = kvl + (size_t)kKVHeads * (block_table ? kPageHead : kKVPlane);
   a.cache_batch_stride = cache_stride;
+  a.block_table = block_table;
+  a.table_stride = table_stride;
+  a.n_pages = n_pages;
   a.out = out;
   a.part_o = w.part_o;
   a.part_ml = w.part_ml;
@@ -600,11 +605,14 @@ int ie_prefill(ie_context* c, const ie_model_weights* weights, int seq_len, int*
 }
 
 // ---------------------------------------------------------------- batched decode
-int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int batch,
-                           const int* seq_lens, int* tokenid_buffs, ie_bf16* data_buffer,
-                           ie_bf16* attn_buffer, float* output_distr, int* output_tokens,
-                           int* tokens_out, void* workspace, void* kv_caches) {
-  CTX_OK(c);
+namespace {
+// One batched step over per-sequence caches (block_table null: kv = batch caches in the
+// reference layout, kv_cache_size() apart) or over a page pool (kv = n_pages pages,
+// block_table [batch][table_stride] page ids).
+int batched_step(ie_context* c, const ie_model_weights* weights, int batch, const int* seq_lens,
+                 int* tokenid_buffs, ie_bf16* data_buffer, ie_bf16* attn_buffer,
+                 float* output_distr, int* output_tokens, int* tokens_out, void* workspace,
+                 void* kv_caches, const int* block_table, int table_stride, int n_pages) {
   IE_REQUIRE(weights && weights_complete(*weights), "decode_step_batched: incomplete weights");
   IE_REQUIRE(batch >= 1 && batch <= 16, "decode_step_batched: batch %d out of [1, 16]", batch);
   IE_REQUIRE(seq_lens && tokenid_buffs && data_buffer && attn_buffer && output_distr &&
@@ -633,7 +641,8 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
   IE_TRY(launch_rmsnorm_prep(batch, data_buffer, W.layers[0].input_layernorm, w.xn, w.ss, st));
   for (int l = 0; l < kLayers; ++l) {
     const ie_layer& L = W.layers[l];
-    uint16_t* kvl = kv_layer(kv_caches, l);
+    uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_caches) + (size_t)l * kPageLayer
+                                : kv_layer(kv_caches, l);
     GemmParams g{};
     g.x = w.xn;
     g.w0 = L.transformer.w_q;
@@ -649,13 +658,17 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     g.rope_cos = W.rope.cos;
     g.rope_sin = W.rope.sin;
     g.k_cache = kvl;
-    g.v_cache = kvl + (size_t)kKVHeads * kKVPlane;
+    g.v_cache = kvl + (size_t)kKVHeads * (block_table ? kPageHead : kKVPlane);
     g.cache_stride = cstride;
+    g.block_table = block_table;
+    g.table_stride = table_stride;
+    g.n_pages = n_pages;
     g.d_seq_len = d_sl;
     g.ss_in = w.ss;
     g.ss_parts = l == 0 ? 4 : kNormParts;
     IE_TRY(launch_gemm(kGemmQkvRope, g, st));
-    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, max_len, batch, cstride, true, st));
+    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, max_len, batch, cstride, true, st,
+                       block_table, table_stride, n_pages));
     GemmParams o{};
     o.x = attn_buffer;
     o.w0 = L.transformer.w_o;
@@ -718,6 +731,39 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
     IE_CHECK_HIP(hipStreamSynchronize(st));
   }
   return IE_OK;
+}
+}  // namespace
+
+int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int batch,
+                           const int* seq_lens, int* tokenid_buffs, ie_bf16* data_buffer,
+                           ie_bf16* attn_buffer, float* output_distr, int* output_tokens,
+                           int* tokens_out, void* workspace, void* kv_caches) {
+  CTX_OK(c);
+  return batched_step(c, weights, batch, seq_lens, tokenid_buffs, data_buffer, attn_buffer,
+                      output_distr, output_tokens, tokens_out, workspace, kv_caches, nullptr, 0,
+                      0);
+}
+
+size_t ie_kv_page_size(void) { return kPageElems * sizeof(uint16_t); }
+
+int ie_decode_step_batched_paged(ie_context* c, const ie_model_weights* weights, int batch,
+                                 const int* seq_lens, int* tokenid_buffs, ie_bf16* data_buffer,
+                                 ie_bf16* attn_buffer, float* output_distr, int* output_tokens,
+                                 int* tokens_out, void* workspace, void* kv_pages, int n_pages,
+                                 const int* block_tables, int table_stride) {
+  CTX_OK(c);
+  IE_REQUIRE(kv_pages && block_tables && n_pages >= 1,
+             "decode_step_batched_paged: needs a page pool and block tables");
+  IE_REQUIRE(table_stride >= 1 && table_stride <= kMaxCtx / kPagePos,
+             "decode_step_batched_paged: table_stride %d out of [1, %d]", table_stride,
+             kMaxCtx / kPagePos);
+  for (int b = 0; seq_lens && b < batch && b < 16; ++b)
+    IE_REQUIRE(seq_lens[b] <= table_stride * kPagePos,
+               "decode_step_batched_paged: seq_lens[%d]=%d needs more than %d table entries", b,
+               seq_lens[b], table_stride);
+  return batched_step(c, weights, batch, seq_lens, tokenid_buffs, data_buffer, attn_buffer,
+                      output_distr, output_tokens, tokens_out, workspace, kv_pages, block_tables,
+                      table_stride, n_pages);
 }
 
 // ---------------------------------------------------------------- weights

@@ -26,6 +26,13 @@ constexpr float kRmsEps = 1e-5f;                     // rmsnorm.cu:5
 // Per-layer KV-cache plane: [2][8][8192][128] (attn.cu:304-307, 334-337).
 constexpr size_t kKVPlane = (size_t)kMaxCtx * kHeadDim;              // one head, K or V
 constexpr size_t kKVLayer = 2 * (size_t)kKVHeads * kKVPlane;         // elements per layer
+// Paged KV cache: a page holds kPagePos positions of every layer, [layer][K|V][kv head]
+// [kPagePos][128] bf16; a sequence's block table maps position block i (positions
+// kPagePos*i ..) to a page.
+constexpr int kPagePos = 64;
+constexpr size_t kPageHead = (size_t)kPagePos * kHeadDim;              // one head, K or V
+constexpr size_t kPageLayer = 2 * (size_t)kKVHeads * kPageHead;        // one layer in a page
+constexpr size_t kPageElems = (size_t)kLayers * kPageLayer;            // elements per page
 
 // Decode attention splits the context of each KV head over this many blocks.
 constexpr int kAttnSplits = 32;

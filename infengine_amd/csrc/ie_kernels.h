@@ -50,6 +50,9 @@ struct AttnDecodeParams {
   const uint16_t* k_cache;  // batch 0 layer K base [8][8192][128]
   const uint16_t* v_cache;  // batch 0 layer V base
   long long cache_batch_stride;  // elements between batch rows' caches
+  const int* block_table;   // paged KV: [batch][table_stride] page ids; k/v_cache = the layer's
+  int table_stride;         // head-0 K/V planes in page 0 (pages kPageElems apart); ids outside
+  int n_pages;              // [0, n_pages) read as empty
   uint16_t* out;            // [batch][32][128] bf16
   float* part_o;            // [batch][8][splits][4][128]
   float* part_ml;           // [batch][8][splits][4][2]
@@ -142,6 +145,9 @@ struct GemmParams {
   uint16_t* k_cache;       // sequence 0's K plane base of this layer [8][kMaxCtx][128]
   uint16_t* v_cache;
   long long cache_stride;  // elements between sequences' caches
+  const int* block_table;  // paged KV: [M][table_stride] page ids; k/v_cache = this layer's K/V
+  int table_stride;        // head-0 planes of page 0 (pages kPageElems apart); ids outside
+  int n_pages;             // [0, n_pages) are not written
   const int* d_seq_len;    // [M]
   // Skinny GEMM (M <= 16) only: RMSNorm folded into the projection.
   // Consumer: x holds bf16(x_row * norm_w) and ss_in [16][ss_parts] partial sums of squares of the

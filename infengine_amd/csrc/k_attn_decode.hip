@@ -70,9 +70,9 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
   const uint16_t* Kh = p.k_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
   const uint16_t* Vh = p.v_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
   // rows past S read as zero (buffer bounds) and are masked below
-  const __amdgpu_buffer_rsrc_t krs =
+  const __amdgpu_buffer_rsrc_t krs_seq =
       __builtin_amdgcn_make_buffer_rsrc((void*)Kh, 0, S * kRowBytes, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t vrs =
+  const __amdgpu_buffer_rsrc_t vrs_seq =
       __builtin_amdgcn_make_buffer_rsrc((void*)Vh, 0, S * kRowBytes, kBufferFlags);
 
   // Q^T fragments: MFMA column fr is q head 4g + fr for fr < 4 (zero elsewhere); lane supplies
@@ -95,10 +95,31 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
   u32x4_t* kt = kvlds[wave][0];
   u32x4_t* vt = kvlds[wave][KREG ? 0 : 1];
 
-  for (int t = t0 + wave; t < t1; t += NW) {
+  // paged KV: lane i holds the page of this wave's i-th tile (one load ahead of the loop)
+  const bool paged = p.block_table != nullptr;
+  int page_of = 0;
+  if (paged) {
+    const int t = t0 + wave + NW * lane;
+    page_of = t < t1 ? p.block_table[(size_t)b * p.table_stride + t] : -1;
+  }
+  int it = 0;
+  for (int t = t0 + wave; t < t1; t += NW, ++it) {
     // K fragments kk[kb][ks] = K[key0 + 16 kb + fr][32 ks + 8 G .. +8], straight from memory
     // (KREG) or from the LDS tile below
     const int key0 = t * kAttnTile;
+    // the tile's buffers: rows key0.. of the sequence's cache, or rows 0.. of its page (a page
+    // id outside the pool reads as zero)
+    __amdgpu_buffer_rsrc_t krs = krs_seq, vrs = vrs_seq;
+    int kr0 = key0;
+    if (paged) {
+      const int page = __builtin_amdgcn_readlane(page_of, it);
+      const bool ok = page >= 0 && page < p.n_pages;
+      const size_t base = (size_t)(ok ? page : 0) * kPageElems + (size_t)g * kPageHead;
+      const int bytes = ok ? min(kAttnTile, S - key0) * kRowBytes : 0;
+      krs = __builtin_amdgcn_make_buffer_rsrc((void*)(p.k_cache + base), 0, bytes, kBufferFlags);
+      vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(p.v_cache + base), 0, bytes, kBufferFlags);
+      kr0 = 0;
+    }
     u32x4_t kk[4][4];
     if constexpr (KREG) {
 #pragma unroll
@@ -106,7 +127,7 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
           kk[kb][ks] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-              krs, (uint32_t)((key0 + 16 * kb + fr) * kRowBytes + (4 * ks + G) * 16), 0, 0));
+              krs, (uint32_t)((kr0 + 16 * kb + fr) * kRowBytes + (4 * ks + G) * 16), 0, 0));
     }
     // tiles to LDS: load j fills rows 4j .. 4j+3; lane fills slot lane%16 of row 4j + lane/16
     // from global chunk (lane%16) ^ (row & 15).  The wave only reads its own slice, so its own
@@ -114,7 +135,7 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int r = 4 * j + G;
-      const uint32_t off = (uint32_t)((key0 + r) * kRowBytes + ((fr ^ (r & 15)) * 16));
+      const uint32_t off = (uint32_t)((kr0 + r) * kRowBytes + ((fr ^ (r & 15)) * 16));
       if constexpr (!KREG)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)&kt[64 * j], 16, off, 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)&vt[64 * j], 16, off, 0, 0, 0);

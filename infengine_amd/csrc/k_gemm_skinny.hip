@@ -304,13 +304,21 @@ void gemm_skinny_kernel(GemmParams p) {
       }
     }
     uint16_t* dst;
-    if (head < kQHeads)
+    if (head < kQHeads) {
       dst = p.y + ((size_t)m * kQHeads + head) * kHeadDim;
-    else if (head < kQHeads + kKVHeads)
-      dst = p.k_cache + (size_t)m * p.cache_stride + ((size_t)(head - kQHeads) * kMaxCtx + pos) * kHeadDim;
-    else
-      dst = p.v_cache + (size_t)m * p.cache_stride +
-            ((size_t)(head - kQHeads - kKVHeads) * kMaxCtx + pos) * kHeadDim;
+    } else {
+      const bool is_k = head < kQHeads + kKVHeads;
+      const int kvh = head - kQHeads - (is_k ? 0 : kKVHeads);
+      uint16_t* const plane = is_k ? p.k_cache : p.v_cache;
+      if (p.block_table) {
+        // paged: row pos % kPagePos of the page holding block pos / kPagePos
+        const int page = p.block_table[(size_t)m * p.table_stride + pos / kPagePos];
+        if (page < 0 || page >= p.n_pages) return;
+        dst = plane + (size_t)page * kPageElems + ((size_t)kvh * kPagePos + pos % kPagePos) * kHeadDim;
+      } else {
+        dst = plane + (size_t)m * p.cache_stride + ((size_t)kvh * kMaxCtx + pos) * kHeadDim;
+      }
+    }
     *reinterpret_cast<uint2*>(dst + jp + (hi ? 64 : 0)) =
         make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
     return;

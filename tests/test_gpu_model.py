@@ -263,6 +263,71 @@ def test_batched_decode_matches_single(hip, model, noise_floor, lens):
     c.close()
 
 
+@pytest.mark.parametrize("lens", [[101, 257, 64], [2100, 257, 64]])
+def test_batched_paged_equals_contiguous(hip, model, lens):
+    """ie_decode_step_batched_paged on a page pool (the sequences' 64-position blocks scattered
+    over the pool in a random order) against ie_decode_step_batched on per-sequence caches:
+    bit-identical logits and tokens, and the new K/V rows written into the right page rows."""
+    from infengine_amd.engine import Context, ptr
+    B = len(lens)
+    say(f"decode_step_batched_paged B={B} lens={lens}")
+    c = Context(0, graph=False)
+    kvsz = hip.lib.ie_kv_cache_size()
+    page_elems = hip.lib.ie_kv_page_size() // 2
+    assert page_elems == 32 * 2 * 8 * 64 * 128
+    kvs = torch.zeros(B * kvsz // 2, dtype=torch.int16, device="cuda")
+    kv6 = kvs.view(B, 32, 2, 8, 8192, 128)
+    toks = torch.zeros(B, 8192, dtype=torch.int32, device="cuda")
+    for b in range(B):
+        kv6[b, :, :, :, :lens[b] - 1] = dev(orc.synthetic((32, 2, 8, lens[b] - 1, 128), SEED,
+                                                          2000 + b, 0.0, 1.0))
+        toks[b, lens[b] - 1] = 700 * (b + 3)
+    nblk = [(n + 63) // 64 for n in lens]
+    n_pages = sum(nblk) + 3  # a few pages no table points at
+    order = np.random.default_rng(SEED).permutation(n_pages)
+    stride = max(nblk) + 1
+    table = np.full((B, stride), -1, dtype=np.int32)
+    pool = torch.zeros(n_pages * page_elems, dtype=torch.int16, device="cuda")
+    pool6 = pool.view(n_pages, 32, 2, 8, 64, 128)
+    k = 0
+    for b in range(B):
+        for i in range(nblk[b]):
+            table[b, i] = order[k]
+            pool6[order[k]] = kv6[b, :, :, :, 64 * i:64 * i + 64]
+            k += 1
+    d_table = torch.from_numpy(table).cuda()
+    seq = (C.c_int * B)(*lens)
+    outs = []
+    for paged in (False, True):
+        data = torch.zeros(B, 4096, dtype=torch.bfloat16, device="cuda")
+        attn = torch.zeros_like(data)
+        logits = torch.zeros(B, 128256, dtype=torch.float32, device="cuda")
+        out = torch.zeros(B, dtype=torch.int32, device="cuda")
+        ws = torch.zeros(hip.lib.ie_batch_workspace_size(B), dtype=torch.uint8, device="cuda")
+        th = (C.c_int * B)()
+        if paged:
+            hip.check(hip.lib.ie_decode_step_batched_paged(
+                c.handle, model.ref(), B, seq, ptr(toks), ptr(data), ptr(attn), ptr(logits),
+                ptr(out), th, ptr(ws), ptr(pool), n_pages, ptr(d_table), stride))
+        else:
+            hip.check(hip.lib.ie_decode_step_batched(
+                c.handle, model.ref(), B, seq, ptr(toks), ptr(data), ptr(attn), ptr(logits),
+                ptr(out), th, ptr(ws), ptr(kvs)))
+        torch.cuda.synchronize()
+        outs.append((host(logits).copy(), list(th)))
+    assert np.array_equal(outs[0][0], outs[1][0]), "paged logits differ from contiguous"
+    assert outs[0][1] == outs[1][1]
+    for b in range(B):
+        pos = lens[b] - 1
+        got = host(pool6[table[b, pos // 64], :, :, :, pos % 64].contiguous())
+        want = host(kv6[b, :, :, :, pos].contiguous())
+        assert got.any() and np.array_equal(got, want), f"new K/V row of sequence {b}"
+    # pages no table entry points at are untouched
+    for pid in order[sum(nblk):]:
+        assert not host(pool6[int(pid)].reshape(-1)[:4096].contiguous()).any()
+    c.close()
+
+
 @pytest.mark.parametrize("graph", [False, True])
 def test_generate_equals_manual_loop(hip, model, graph):
     """ie_generate (the Manager loop in the library, token write-back fused into the argmax)
