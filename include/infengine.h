@@ -157,6 +157,12 @@ IE_API int ie_decode_step_batched(ie_context* ctx, const ie_model_weights* weigh
  * ids outside [0, n_pages) read as zero and are not written.  Results are
  * bit-identical to ie_decode_step_batched on the same rows. */
 IE_API size_t ie_kv_page_size(void);
+/* Positions [first_pos, first_pos + n_pos) of every layer of a reference-layout
+ * KV cache (e.g. just written by ie_prefill) into the pages that block_table
+ * (device, one sequence's row) maps them to; ids outside [0, n_pages) skipped.
+ * Runs on the context's stream. */
+IE_API int ie_kv_cache_to_pages(ie_context* ctx, const void* kv_cache, int first_pos, int n_pos,
+                                void* kv_pages, int n_pages, const int* block_table);
 IE_API int ie_decode_step_batched_paged(ie_context* ctx, const ie_model_weights* weights,
                                         int batch, const int* seq_lens, int* tokenid_buffs,
                                         ie_bf16* data_buffer, ie_bf16* attn_buffer,

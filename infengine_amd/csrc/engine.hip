@@ -111,7 +111,7 @@ int qkv_rope_gemv(const ie_layer& L, const ie_rope_weights& rope, const uint16_t
 int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs& w,
                 const int* d_seq_len, int seq_len, int max_len, int batch, long long cache_stride,
                 bool merge, hipStream_t st, const int* block_table = nullptr, int table_stride = 0,
-                int n_pages = 0) {
+                int n_pages = 0, bool batched = false) {
   AttnDecodeParams a{};
   a.q = q;
   a.k_cache = kvl;
@@ -125,9 +125,10 @@ int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs&
   a.part_ml = w.part_ml;
   a.d_seq_len = d_seq_len;
   a.seq_len = seq_len;
-  // batched: 16 x 8 (sequence, kv head) workgroups already fill the chip, so up to
-  // kAttnDirectMaxCtx one split per pair writes the output (no merge launch)
-  a.max_splits = (batch > 1 && merge && max_len <= kAttnDirectMaxCtx) ? 1
+  // batched step: 16 x 8 (sequence, kv head) workgroups already fill the chip, so up to
+  // kAttnDirectMaxCtx one split per pair writes the output (no merge launch).  At every batch
+  // size, so that a sequence's results do not depend on how many others share its step.
+  a.max_splits = (batched && merge && max_len <= kAttnDirectMaxCtx) ? 1
                  : max_len <= kAttnFusedMaxCtx                        ? kAttnFusedSplits
                                                                      : kAttnSplits;
   IE_REQUIRE(merge || a.max_splits == kAttnFusedSplits,
@@ -668,7 +669,7 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
     g.ss_parts = l == 0 ? 4 : kNormParts;
     IE_TRY(launch_gemm(kGemmQkvRope, g, st));
     IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, max_len, batch, cstride, true, st,
-                       block_table, table_stride, n_pages));
+                       block_table, table_stride, n_pages, true));
     GemmParams o{};
     o.x = attn_buffer;
     o.w0 = L.transformer.w_o;
@@ -745,6 +746,14 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
 }
 
 size_t ie_kv_page_size(void) { return kPageElems * sizeof(uint16_t); }
+
+int ie_kv_cache_to_pages(ie_context* c, const void* kv_cache, int first_pos, int n_pos,
+                         void* kv_pages, int n_pages, const int* block_table) {
+  CTX_OK(c);
+  IE_TRY(launch_kv_to_pages(static_cast<const uint16_t*>(kv_cache), first_pos, n_pos,
+                            static_cast<uint16_t*>(kv_pages), n_pages, block_table, c->stream));
+  return IE_OK;
+}
 
 int ie_decode_step_batched_paged(ie_context* c, const ie_model_weights* weights, int batch,
                                  const int* seq_lens, int* tokenid_buffs, ie_bf16* data_buffer,

@@ -98,6 +98,8 @@ int launch_fill_synthetic(uint16_t* out, size_t n, uint64_t seed, uint64_t tenso
 // Rotate q,k of a [S][6144] QKV block, write k,v to cache rows start..start+S-1
 // (or, with d_seq_lens, row t to position d_seq_lens[t]-1 of cache t) and the
 // rotated q to q_out [S][4096].
+int launch_kv_to_pages(const uint16_t* kv, int first, int n, uint16_t* pages, int n_pages,
+                       const int* table, hipStream_t st);
 int launch_qkv_rope_scatter(int S, int start_pos, const uint16_t* qkv, const float* cos,
                             const float* sin, uint16_t* q_out, uint16_t* k_cache,
                             uint16_t* v_cache, const int* d_seq_lens, long long cache_stride,

@@ -313,7 +313,7 @@ int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStre
   IE_REQUIRE(p.max_splits > 1 || (merge && p.out), "attn_decode: one split writes the output");
   // one workgroup per possible split: idle ones would still cost dispatch (at batch 16 and
   // 32 splits, 4096 mostly empty workgroups took 52 us)
-  if (batch > 1 && p.max_splits == 1)  // one workgroup per (sequence, kv head): 8 waves share its tiles
+  if (p.max_splits == 1)  // one workgroup per (sequence, kv head): 8 waves share its tiles
     hipLaunchKernelGGL((attn_decode_split_kernel<true, 8>), dim3(1, kKVHeads, batch), dim3(8 * 64), 0,
                        st, p);
   else if (batch > 1)

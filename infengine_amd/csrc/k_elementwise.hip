@@ -167,6 +167,30 @@ __global__ __launch_bounds__(256) void qkv_rope_scatter_kernel(int start_pos, co
   }
 }
 
+// ---------------------------------------------------------------- contiguous cache -> pages
+// Positions [first, first + n) of every (layer, K|V, kv head) plane of a reference-layout cache
+// into the pages of one sequence's block table; 16 bytes per thread.  Page ids outside
+// [0, n_pages) are skipped.
+__global__ __launch_bounds__(256) void kv_to_pages_kernel(const uint16_t* kv, int first, int n,
+                                                          uint16_t* pages, int n_pages,
+                                                          const int* table) {
+  constexpr int kPlanes = kLayers * 2 * kKVHeads;
+  const size_t total = (size_t)n * kPlanes * 16;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i & 15);
+    const size_t rest = i >> 4;
+    const int plane = (int)(rest % kPlanes);
+    const int pos = first + (int)(rest / kPlanes);
+    const int page = table[pos / kPagePos];
+    if (page < 0 || page >= n_pages) continue;
+    const u32x4_t v =
+        *reinterpret_cast<const u32x4_t*>(kv + ((size_t)plane * kMaxCtx + pos) * kHeadDim + 8 * c);
+    *reinterpret_cast<u32x4_t*>(pages + (size_t)page * kPageElems +
+                                ((size_t)plane * kPagePos + pos % kPagePos) * kHeadDim + 8 * c) = v;
+  }
+}
+
 // ---------------------------------------------------------------- softmax
 // softmax.cu:55-160: softmax(x / sqrt(128)) per row, entries right of the
 // diagonal masked (causal) and written as 0.  fp32 throughout.
@@ -291,6 +315,20 @@ int launch_rope(int start_pos, int heads, int seq_len, const float* cos, const f
              kMaxCtx);
   hipLaunchKernelGGL(rope_kernel, dim3(heads * seq_len), dim3(64), 0, st, start_pos, seq_len, cos,
                      sin, in, out, is_kv);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+int launch_kv_to_pages(const uint16_t* kv, int first, int n, uint16_t* pages, int n_pages,
+                       const int* table, hipStream_t st) {
+  IE_REQUIRE(kv && pages && table && n_pages >= 1, "kv_to_pages: null buffer");
+  IE_REQUIRE(first >= 0 && n >= 0 && first + n <= kMaxCtx, "kv_to_pages: positions [%d, %d)",
+             first, first + n);
+  if (n == 0) return IE_OK;
+  const size_t total = (size_t)n * kLayers * 2 * kKVHeads * 16;
+  const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+  hipLaunchKernelGGL(kv_to_pages_kernel, dim3(blocks), dim3(256), 0, st, kv, first, n, pages,
+                     n_pages, table);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }

@@ -12,19 +12,36 @@ ROOT = pathlib.Path(__file__).resolve().parent.parent
 LIBDIR = ROOT / "infengine_amd"
 
 
-def build_manager(out_dir: pathlib.Path) -> pathlib.Path:
-    exe = out_dir / "manager_main"
+def build_manager(out_dir: pathlib.Path, name: str = "manager_main") -> pathlib.Path:
+    exe = out_dir / name
     cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
-           f"-I{ROOT / 'include'}", "-I/opt/rocm/include", str(ROOT / "tests/cpp/manager_main.cpp"),
+           f"-I{ROOT / 'include'}", "-I/opt/rocm/include", str(ROOT / f"tests/cpp/{name}.cpp"),
            f"-L{LIBDIR}", "-linfengine_amd", "-L/opt/rocm/lib", "-lamdhip64",
            f"-Wl,-rpath,{LIBDIR}", "-Wl,-rpath,/opt/rocm/lib", "-o", str(exe)]
-    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
     return exe
 
 
-def test_cpp_api_compiles_and_links(tmp_path, hip):
-    exe = build_manager(tmp_path)
+@pytest.mark.parametrize("name", ["manager_main", "batcher_main"])
+def test_cpp_api_compiles_and_links(tmp_path, hip, name):
+    exe = build_manager(tmp_path, name)
     assert exe.exists()
+
+
+@pytest.mark.gpu
+def test_cpp_continuous_batcher(tmp_path, hip):
+    """The continuous batcher over the paged KV cache: four requests admitted at once, joining at
+    different steps, and one at a time produce the same tokens (the program checks and prints
+    OK), and every page returns to the pool."""
+    from gpu_util import say
+    exe = build_manager(tmp_path, "batcher_main")
+    say("C++ ContinuousBatcher: 4 requests, 3 schedules")
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stdout + res.stderr
+    lines = res.stdout.splitlines()
+    assert lines[-1] == "OK"
+    assert [len(l.split()) - 2 for l in lines[:-1]] == [12, 10, 14, 16]
 
 
 @pytest.mark.gpu
