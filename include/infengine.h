@@ -157,6 +157,14 @@ IE_API int ie_decode_step_batched(ie_context* ctx, const ie_model_weights* weigh
  * ids outside [0, n_pages) read as zero and are not written.  Results are
  * bit-identical to ie_decode_step_batched on the same rows. */
 IE_API size_t ie_kv_page_size(void);
+/* ie_prefill writing the prompt's K/V rows into pages: block_table (device) is the
+ * sequence's page per 64-position block, entries 0 .. (seq_len-1)/64 set.  Same
+ * arguments and results as ie_prefill otherwise (bit-identical logits / token). */
+IE_API int ie_prefill_paged(ie_context* ctx, const ie_model_weights* weights, int seq_len,
+                            int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                            ie_bf16* attn_buffer, float* output_distr, int* output_token,
+                            void* workspace, void* kv_pages, int n_pages,
+                            const int* block_table);
 /* Positions [first_pos, first_pos + n_pos) of every layer of a reference-layout
  * KV cache (e.g. just written by ie_prefill) into the pages that block_table
  * (device, one sequence's row) maps them to; ids outside [0, n_pages) skipped.

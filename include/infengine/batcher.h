@@ -1,9 +1,9 @@
 // Continuous batching over the paged KV cache: requests join and leave between decode steps.
 // The reference serves one request at a time (manager.cpp:31-110) and keeps a per-request
 // RequestContext it never uses (manager.h:19-24); this driver is the continuous form of that
-// loop.  Each admitted request is prefilled alone (ie_prefill into a scratch reference-layout
-// cache, whose rows are then copied into the request's pages), then decoded together with
-// every other running request, up to 16 per ie_decode_step_batched_paged call.  Pages (64
+// loop.  Each admitted request is prefilled alone, straight into its pages
+// (ie_prefill_paged), then decoded together with every other running request, up to 16 per
+// ie_decode_step_batched_paged call.  Pages (64
 // positions of all layers, 8 MiB) come from a fixed pool; a request reserves the pages its
 // whole lifetime needs when it is admitted, so a running request never waits for memory, and
 // returns them when it finishes (max_new_tokens or eos_token).  Every row of the batched step
@@ -43,7 +43,7 @@ class ContinuousBatcher {
   ~ContinuousBatcher() {
     for (void* p : {pool_, (void*)d_table_, (void*)d_tokens_, (void*)d_data_, (void*)d_attn_,
                     (void*)d_logits_, (void*)d_out_, d_ws_, (void*)p_tokens_, (void*)p_data_,
-                    (void*)p_aux_, (void*)p_attn_, (void*)p_logits_, (void*)p_out_, p_ws_, p_kv_})
+                    (void*)p_aux_, (void*)p_attn_, (void*)p_logits_, (void*)p_out_, p_ws_})
       if (p) (void)hipFree(p);
   }
   ContinuousBatcher(const ContinuousBatcher&) = delete;
@@ -132,7 +132,7 @@ class ContinuousBatcher {
     r.pages.clear();
   }
 
-  // Prefill alone into the scratch cache, copy its rows into the request's pages.
+  // Prefill alone, writing the prompt's K/V rows into the request's pages.
   void admit(int id) {
     Req& r = reqs_[id];
     const int S = r.prompt_len;
@@ -143,13 +143,11 @@ class ContinuousBatcher {
       free_pages_.pop_back();
     }
     check(hipMemcpy(p_tokens_, r.tokens.data(), S * sizeof(int), hipMemcpyHostToDevice));
-    const int tok = prefill(handle_, weights_, S, p_tokens_, p_data_, p_aux_, p_attn_, p_logits_,
-                            p_out_, p_ws_, p_kv_);
     check(hipMemcpy(d_table_, r.pages.data(), r.pages.size() * sizeof(int),
                     hipMemcpyHostToDevice));
-    infengine_detail::checked(
-        ie_kv_cache_to_pages(handle_, p_kv_, 0, S, pool_, n_pages_, d_table_));
-    check(hipDeviceSynchronize());
+    const int tok = infengine_detail::checked(
+        ie_prefill_paged(handle_, &weights_, S, p_tokens_, p_data_, p_aux_, p_attn_, p_logits_,
+                         p_out_, p_ws_, pool_, n_pages_, d_table_));
     r.tokens.push_back(tok);
     if (finished_now(r)) retire(r);
     else running_.push_back(id);
@@ -158,7 +156,7 @@ class ContinuousBatcher {
   void ensure_prefill_buffers(int S) {
     const size_t ws = std::max(attn_workspace_size(S), ffn_workspace_size(S));
     if (p_ws_ && ws <= p_ws_bytes_) return;
-    if (!p_kv_) {
+    if (!p_tokens_) {
       const size_t act = (size_t)InfEngineConfig::MAX_CONTEXT_LENGTH *
                          InfEngineConfig::HIDDEN_SIZE * sizeof(bf16);
       check(hipMalloc(&p_tokens_, InfEngineConfig::MAX_CONTEXT_LENGTH * sizeof(int)));
@@ -167,7 +165,6 @@ class ContinuousBatcher {
       check(hipMalloc(&p_attn_, act));
       check(hipMalloc(&p_logits_, InfEngineConfig::VOCAB_SIZE * sizeof(float)));
       check(hipMalloc(&p_out_, sizeof(int)));
-      check(hipMalloc(&p_kv_, kv_cache_size()));
     }
     if (p_ws_) check(hipFree(p_ws_));
     check(hipMalloc(&p_ws_, ws));
@@ -196,5 +193,4 @@ class ContinuousBatcher {
   int* p_out_ = nullptr;
   void* p_ws_ = nullptr;
   size_t p_ws_bytes_ = 0;
-  void* p_kv_ = nullptr;
 };

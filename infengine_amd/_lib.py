@@ -77,6 +77,7 @@ SIGNATURES: dict[str, tuple] = {
     "ie_decode_step_batched": (_i, [_p, _W, _i, C.POINTER(_i), _p, _p, _p, _p, _p,
                                     C.POINTER(_i), _p, _p]),
     "ie_kv_page_size": (_sz, []),
+    "ie_prefill_paged": (_i, [_p, _W, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
     "ie_kv_cache_to_pages": (_i, [_p, _p, _i, _i, _p, _i, _p]),
     "ie_decode_step_batched_paged": (_i, [_p, _W, _i, C.POINTER(_i), _p, _p, _p, _p, _p,
                                           C.POINTER(_i), _p, _p, _i, _p, _i]),

@@ -523,10 +523,13 @@ int ie_generate(ie_context* c, const ie_model_weights* weights, const int* promp
 }
 
 // ---------------------------------------------------------------- prefill
-int ie_prefill(ie_context* c, const ie_model_weights* weights, int seq_len, int* tokenid_buff,
-               ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
-               float* output_distr, int* output_token, void* workspace, void* kv_cache) {
-  CTX_OK(c);
+namespace {
+// The prefill body over a reference-layout cache (block_table null) or over a page pool
+// (kv_cache = n_pages pages, block_table the sequence's page per 64-position block).
+int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, int* tokenid_buff,
+                 ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
+                 float* output_distr, int* output_token, void* workspace, void* kv_cache,
+                 const int* block_table, int n_pages) {
   IE_REQUIRE(weights && weights_complete(*weights), "prefill: incomplete weights");
   IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "prefill: seq_len %d out of [1, %d]", seq_len,
              kMaxCtx);
@@ -544,7 +547,9 @@ int ie_prefill(ie_context* c, const ie_model_weights* weights, int seq_len, int*
   IE_TRY(launch_emblookup(S, tokenid_buff, W.emb_lookup, data_buffer, nullptr, 0, st));
   for (int l = 0; l < kLayers; ++l) {
     const ie_layer& L = W.layers[l];
-    uint16_t* kvl = kv_layer(kv_cache, l);
+    uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_cache) + (size_t)l * kPageLayer
+                                : kv_layer(kv_cache, l);
+    uint16_t* vpl = kvl + (size_t)kKVHeads * (block_table ? kPageHead : kKVPlane);
     IE_TRY(launch_rmsnorm(S, data_buffer, L.input_layernorm, aux_buffer, st));
     GemmParams g{};
     g.x = aux_buffer;
@@ -559,9 +564,9 @@ int ie_prefill(ie_context* c, const ie_model_weights* weights, int seq_len, int*
     g.K = kHidden;
     g.ldy = kQKVDim;
     IE_TRY(launch_gemm(kGemmBf16, g, st));
-    IE_TRY(launch_qkv_rope_scatter(S, 0, qkv, W.rope.cos, W.rope.sin, qrot, kvl,
-                                   kvl + (size_t)kKVHeads * kKVPlane, nullptr, 0, st));
-    AttnPrefillParams a{qrot, kvl, kvl + (size_t)kKVHeads * kKVPlane, attn_buffer, S, 0};
+    IE_TRY(launch_qkv_rope_scatter(S, 0, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl, nullptr, 0,
+                                   st, block_table, n_pages));
+    AttnPrefillParams a{qrot, kvl, vpl, attn_buffer, S, 0, block_table, n_pages};
     IE_TRY(launch_attn_prefill(a, st));
     GemmParams o{};
     o.x = attn_buffer;
@@ -603,6 +608,25 @@ int ie_prefill(ie_context* c, const ie_model_weights* weights, int seq_len, int*
   IE_CHECK_HIP(hipMemcpyAsync(c->h_token, output_token, sizeof(int), hipMemcpyDeviceToHost, st));
   IE_CHECK_HIP(hipStreamSynchronize(st));
   return c->h_token[0];
+}
+}  // namespace
+
+int ie_prefill(ie_context* c, const ie_model_weights* weights, int seq_len, int* tokenid_buff,
+               ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
+               float* output_distr, int* output_token, void* workspace, void* kv_cache) {
+  CTX_OK(c);
+  return prefill_impl(c, weights, seq_len, tokenid_buff, data_buffer, aux_buffer, attn_buffer,
+                      output_distr, output_token, workspace, kv_cache, nullptr, 0);
+}
+
+int ie_prefill_paged(ie_context* c, const ie_model_weights* weights, int seq_len,
+                     int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                     ie_bf16* attn_buffer, float* output_distr, int* output_token,
+                     void* workspace, void* kv_pages, int n_pages, const int* block_table) {
+  CTX_OK(c);
+  IE_REQUIRE(kv_pages && block_table && n_pages >= 1, "prefill_paged: needs a page pool and a block table");
+  return prefill_impl(c, weights, seq_len, tokenid_buff, data_buffer, aux_buffer, attn_buffer,
+                      output_distr, output_token, workspace, kv_pages, block_table, n_pages);
 }
 
 // ---------------------------------------------------------------- batched decode

@@ -103,7 +103,7 @@ int launch_kv_to_pages(const uint16_t* kv, int first, int n, uint16_t* pages, in
 int launch_qkv_rope_scatter(int S, int start_pos, const uint16_t* qkv, const float* cos,
                             const float* sin, uint16_t* q_out, uint16_t* k_cache,
                             uint16_t* v_cache, const int* d_seq_lens, long long cache_stride,
-                            hipStream_t st);
+                            hipStream_t st, const int* block_table = nullptr, int n_pages = 0);
 
 // ------------------------------------------------------------ sampling
 // Row 0 extras of the argmax: host_tok (mapped pinned memory) receives the token with a
@@ -185,6 +185,8 @@ struct AttnPrefillParams {
   uint16_t* out;       // [S][4096]
   int S;
   int start_pos;       // absolute position of q row 0 (keys 0..start_pos+S-1)
+  const int* block_table = nullptr;  // paged KV: page of each 64-key block; k / v = the layer's
+  int n_pages = 0;                   // head-0 K / V planes in page 0 (ids outside: empty)
 };
 int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t st);
 

@@ -46,10 +46,10 @@ __device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r &
 
 // Loads of tile t into ring stage `stage`: this wave's 4 K and 4 V row groups (4 rows each).
 // The tile offset goes into the vector offset, which the buffer range check covers.
+// Paged KV: krs / vrs are the tile's page rows and toff is 0.
 __device__ __forceinline__ void issue_tile(u32x4_t* lds, __amdgpu_buffer_rsrc_t krs,
                                            __amdgpu_buffer_rsrc_t vrs, const uint32_t* voff,
-                                           int wv, int t, int stage) {
-  const uint32_t toff = (uint32_t)(t * BKEY * kRowBytes);
+                                           int wv, uint32_t toff, int stage) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     u32x4_t* kd = &lds[stage * 2 * TC + (wv + 4 * j) * 64];
@@ -115,6 +115,7 @@ __device__ __forceinline__ void softmax_tile(f32x4_t (&s)[2][4], float (&m)[2], 
   }
 }
 
+template <bool PAGED>
 __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams p) {
   __shared__ u32x4_t lds[2 * 2 * TC];  // [stage][K | V][key][16 chunks], 64 KiB
 
@@ -164,11 +165,38 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
   // m: running max of the raw scores (the scale is applied inside the exponent)
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
 
-  issue_tile(lds, krs, vrs, voff, wv, 0, 0);
+  // Paged KV: tile t's buffers are its page's rows; the page id of tile t+1 is loaded (a vector
+  // load, so the loop's vmcnt wait covers it) while tile t is multiplied.
+  constexpr bool paged = PAGED;
+  int pg_next = paged ? p.block_table[0] : 0;
+  auto tile_rsrc = [&](int t, int page, __amdgpu_buffer_rsrc_t& tk, __amdgpu_buffer_rsrc_t& tv) {
+    const bool ok = page >= 0 && page < p.n_pages;
+    const size_t base = (size_t)(ok ? page : 0) * kPageElems + (size_t)g * kPageHead;
+    const int bytes = ok ? min(BKEY, nkeys - t * BKEY) * kRowBytes : 0;
+    tk = __builtin_amdgcn_make_buffer_rsrc((void*)(p.k + base), 0, bytes, kBufferFlags);
+    tv = __builtin_amdgcn_make_buffer_rsrc((void*)(p.v + base), 0, bytes, kBufferFlags);
+  };
+  if constexpr (paged) {
+    __amdgpu_buffer_rsrc_t tk, tv;
+    tile_rsrc(0, __builtin_amdgcn_readfirstlane(pg_next), tk, tv);
+    issue_tile(lds, tk, tv, voff, wv, 0, 0);
+    pg_next = p.block_table[min(1, ntiles - 1)];
+  } else {
+    issue_tile(lds, krs, vrs, voff, wv, 0, 0);
+  }
   for (int t = 0; t < ntiles; ++t) {
     // tile t has landed (the only loads in flight) and every wave is done with tile t-1
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (t + 1 < ntiles) issue_tile(lds, krs, vrs, voff, wv, t + 1, (t + 1) & 1);
+    if (t + 1 < ntiles) {
+      if constexpr (paged) {
+        __amdgpu_buffer_rsrc_t tk, tv;
+        tile_rsrc(t + 1, __builtin_amdgcn_readfirstlane(pg_next), tk, tv);
+        issue_tile(lds, tk, tv, voff, wv, 0, (t + 1) & 1);
+        pg_next = p.block_table[min(t + 2, ntiles - 1)];
+      } else {
+        issue_tile(lds, krs, vrs, voff, wv, (uint32_t)((t + 1) * BKEY * kRowBytes), (t + 1) & 1);
+      }
+    }
     const u32x4_t* kt = &lds[(t & 1) * 2 * TC];
     const u32x4_t* vt = kt + TC;
     const int key0 = t * BKEY;
@@ -237,7 +265,10 @@ int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t st) {
   IE_REQUIRE(p.S >= 1 && p.start_pos >= 0 && p.start_pos + p.S <= kMaxCtx,
              "attn_prefill: rows [%d, %d) exceed the KV cache", p.start_pos, p.start_pos + p.S);
   const int nqb = (p.S + BQ - 1) / BQ;
-  hipLaunchKernelGGL(flash_prefill_kernel, dim3(nqb * kKVHeads), dim3(256), 0, st, p);
+  if (p.block_table)
+    hipLaunchKernelGGL(flash_prefill_kernel<true>, dim3(nqb * kKVHeads), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(flash_prefill_kernel<false>, dim3(nqb * kKVHeads), dim3(256), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }

@@ -135,7 +135,9 @@ __global__ __launch_bounds__(256) void qkv_rope_scatter_kernel(int start_pos, co
                                                                uint16_t* q_out, uint16_t* kc,
                                                                uint16_t* vc,
                                                                const int* d_seq_lens,
-                                                               long long cache_stride) {
+                                                               long long cache_stride,
+                                                               const int* block_table,
+                                                               int n_pages) {
   const int t = blockIdx.x;
   const int pos = d_seq_lens ? d_seq_lens[t] - 1 : start_pos + t;
   if (d_seq_lens) {
@@ -157,10 +159,17 @@ __global__ __launch_bounds__(256) void qkv_rope_scatter_kernel(int start_pos, co
     uint16_t* dst;
     if (head < kQHeads) {
       dst = q_out + ((size_t)t * kQHeads + head) * kHeadDim;
-    } else if (head < kQHeads + kKVHeads) {
-      dst = kc + ((size_t)(head - kQHeads) * kMaxCtx + pos) * kHeadDim;
     } else {
-      dst = vc + ((size_t)(head - kQHeads - kKVHeads) * kMaxCtx + pos) * kHeadDim;
+      const bool is_k = head < kQHeads + kKVHeads;
+      const int kvh = head - kQHeads - (is_k ? 0 : kKVHeads);
+      uint16_t* const plane = is_k ? kc : vc;
+      if (block_table) {  // paged: row pos % kPagePos of the page holding block pos / kPagePos
+        const int page = block_table[pos / kPagePos];
+        if (page < 0 || page >= n_pages) continue;
+        dst = plane + (size_t)page * kPageElems + ((size_t)kvh * kPagePos + pos % kPagePos) * kHeadDim;
+      } else {
+        dst = plane + ((size_t)kvh * kMaxCtx + pos) * kHeadDim;
+      }
     }
     dst[j] = f2bf(a);
     dst[j + 64] = f2bf(b);
@@ -336,11 +345,12 @@ int launch_kv_to_pages(const uint16_t* kv, int first, int n, uint16_t* pages, in
 int launch_qkv_rope_scatter(int S, int start_pos, const uint16_t* qkv, const float* cos,
                             const float* sin, uint16_t* q_out, uint16_t* k_cache,
                             uint16_t* v_cache, const int* d_seq_lens, long long cache_stride,
-                            hipStream_t st) {
+                            hipStream_t st, const int* block_table, int n_pages) {
   IE_REQUIRE(S >= 1 && start_pos >= 0 && (d_seq_lens || start_pos + S <= kMaxCtx),
              "qkv scatter: rows [%d, %d) exceed the KV cache", start_pos, start_pos + S);
+  IE_REQUIRE(!block_table || !d_seq_lens, "qkv scatter: paged rows are one sequence's");
   hipLaunchKernelGGL(qkv_rope_scatter_kernel, dim3(S), dim3(256), 0, st, start_pos, qkv, cos, sin,
-                     q_out, k_cache, v_cache, d_seq_lens, cache_stride);
+                     q_out, k_cache, v_cache, d_seq_lens, cache_stride, block_table, n_pages);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }

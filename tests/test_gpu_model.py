@@ -263,6 +263,47 @@ def test_batched_decode_matches_single(hip, model, noise_floor, lens):
     c.close()
 
 
+@pytest.mark.parametrize("S", [100, 600])
+def test_prefill_paged_equals_contiguous(hip, model, S):
+    """ie_prefill_paged (K/V rows into pages scattered over a pool) against ie_prefill (reference-
+    layout cache): bit-identical logits and token, and every K/V row in its page."""
+    from infengine_amd.engine import Context, ptr
+    say(f"prefill_paged S={S}")
+    c = Context(0, graph=False)
+    page_elems = hip.lib.ie_kv_page_size() // 2
+    nblk = (S + 63) // 64
+    n_pages = nblk + 2
+    order = np.random.default_rng(S).permutation(n_pages)[:nblk].astype(np.int32)
+    pool = torch.zeros(n_pages * page_elems, dtype=torch.int16, device="cuda")
+    kv = torch.zeros(hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+    toks = torch.from_numpy(((np.arange(8192) * 7919 + 31) % 128256).astype(np.int32)).cuda()
+    ws = torch.zeros(max(hip.lib.ie_attn_workspace_size(S), hip.lib.ie_ffn_workspace_size(S)),
+                     dtype=torch.uint8, device="cuda")
+    d_table = torch.from_numpy(order).cuda()
+    outs = []
+    for paged in (False, True):
+        data = torch.zeros(S, 4096, dtype=torch.bfloat16, device="cuda")
+        aux, attn = torch.zeros_like(data), torch.zeros_like(data)
+        logits = torch.zeros(128256, dtype=torch.float32, device="cuda")
+        out = torch.zeros(1, dtype=torch.int32, device="cuda")
+        if paged:
+            t = hip.lib.ie_prefill_paged(c.handle, model.ref(), S, ptr(toks), ptr(data), ptr(aux),
+                                         ptr(attn), ptr(logits), ptr(out), ptr(ws), ptr(pool),
+                                         n_pages, ptr(d_table))
+        else:
+            t = hip.lib.ie_prefill(c.handle, model.ref(), S, ptr(toks), ptr(data), ptr(aux),
+                                   ptr(attn), ptr(logits), ptr(out), ptr(ws), ptr(kv))
+        hip.check(t)
+        outs.append((t, host(logits).copy()))
+    assert outs[0][0] == outs[1][0] and np.array_equal(outs[0][1], outs[1][1])
+    kv6 = kv.view(32, 2, 8, 8192, 128)
+    pool6 = pool.view(n_pages, 32, 2, 8, 64, 128)
+    for i in range(nblk):
+        n = min(64, S - 64 * i)
+        assert torch.equal(pool6[int(order[i]), :, :, :, :n], kv6[:, :, :, 64 * i:64 * i + n]), i
+    c.close()
+
+
 @pytest.mark.parametrize("lens", [[101, 257, 64], [2100, 257, 64]])
 def test_batched_paged_equals_contiguous(hip, model, lens):
     """ie_decode_step_batched_paged on a page pool (the sequences' 64-position blocks scattered
