@@ -77,7 +77,10 @@ DecodeWs decode_ws(void* ws, int batch) {
 size_t prefill_attn_bytes(int S) {
   return align256((size_t)S * kQKVDim * 2) + align256((size_t)S * kHidden * 2);
 }
-size_t prefill_ffn_bytes(int S) { return align256((size_t)S * kFFN * 2); }
+// [h (S x 14336 bf16) | split-K partials of the 4096-column projections (S <= kSplitMaxRows)];
+// the O projection's partials reuse the start (q/k/v and rotated q are dead by then).
+size_t prefill_split_bytes(int S) { return align256(gemm_split_bytes(std::min(S, kSplitMaxRows), kHidden)); }
+size_t prefill_ffn_bytes(int S) { return align256((size_t)S * kFFN * 2) + prefill_split_bytes(S); }
 
 uint16_t* kv_layer(void* kv, int layer) {
   return static_cast<uint16_t*>(kv) + (size_t)layer * kKVLayer;
@@ -346,6 +349,7 @@ int ie_context_destroy(ie_context* c) {
   if (c->h_params) (void)hipHostFree(c->h_params);
   if (c->h_token) (void)hipHostFree(c->h_token);
   if (c->capture) (void)hipStreamDestroy(c->capture);
+  if (c->gemm_ws) (void)hipFree(c->gemm_ws);
   delete c;
   return IE_OK;
 }
@@ -577,6 +581,8 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, in
     o.N = kHidden;
     o.K = kHidden;
     o.ldy = kHidden;
+    o.split_ws = reinterpret_cast<float*>(wsb);  // q/k/v and rotated q are dead
+    o.split_ws_bytes = (long long)prefill_split_bytes(S);
     IE_TRY(launch_gemm(kGemmResid, o, st));
     IE_TRY(launch_rmsnorm(S, data_buffer, L.post_attention_layernorm, aux_buffer, st));
     GemmParams gu{};
@@ -598,6 +604,8 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, in
     dn.N = kHidden;
     dn.K = kFFN;
     dn.ldy = kHidden;
+    dn.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
+    dn.split_ws_bytes = (long long)prefill_split_bytes(S);
     IE_TRY(launch_gemm(kGemmResid, dn, st));
   }
   // prefill.cu:41-43: final norm, lm_head on the last row only, argmax
@@ -1029,6 +1037,19 @@ int ie_gemm_ex(ie_context* c, int epilogue, int m, int k, int n, const ie_bf16* 
   g.N = n;
   g.K = k;
   g.ldy = n;
+  // split K's partials: a context-owned scratch, grown on first use (op-level entry; the
+  // engine passes its own workspace)
+  const size_t need = (epilogue == IE_GEMM_BF16 || epilogue == IE_GEMM_RESID) ? gemm_split_bytes(m, n) : 0;
+  if (need > c->gemm_ws_bytes) {
+    IE_CHECK_HIP(hipStreamSynchronize(c->stream));
+    if (c->gemm_ws) IE_CHECK_HIP(hipFree(c->gemm_ws));
+    c->gemm_ws = nullptr;
+    c->gemm_ws_bytes = 0;
+    IE_CHECK_HIP(hipMalloc(reinterpret_cast<void**>(&c->gemm_ws), need));
+    c->gemm_ws_bytes = need;
+  }
+  g.split_ws = c->gemm_ws;
+  g.split_ws_bytes = (long long)c->gemm_ws_bytes;
   return launch_gemm(epilogue, g, c->stream);
 }
 

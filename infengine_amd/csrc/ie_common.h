@@ -241,6 +241,9 @@ struct Context {
   // captured decode-step graph and the arguments it was captured with
   hipGraphExec_t graph_exec = nullptr;
   const void* graph_key[12] = {};
+  // split-K partials of the op-level GEMM entry (allocated on first use)
+  float* gemm_ws = nullptr;
+  size_t gemm_ws_bytes = 0;
 };
 
 constexpr int kNumCounters = 256;

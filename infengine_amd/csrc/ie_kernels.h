@@ -161,7 +161,18 @@ struct GemmParams {
   uint16_t* xw_out;
   const uint16_t* xw_norm;
   float* ss_out;
+  // Split K (bf16 / residual epilogues, kWideMinRows <= M <= kSplitMaxRows): scratch for
+  // fp32 partial products [splits][M][N]; when set and the tiles would fill at most half the
+  // chip, K is split across workgroups and a reduction applies the epilogue.
+  float* split_ws;
+  long long split_ws_bytes;
+  int k_splits;  // set by the launcher for the wide kernel (0 / 1: no split)
 };
+constexpr int kSplitMaxRows = 512;
+// Scratch bytes split K may use for an M-row product with n output columns.
+inline size_t gemm_split_bytes(int M, int n) {
+  return M <= kSplitMaxRows ? (size_t)4 * M * n * sizeof(float) : 0;
+}
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st);
 
 // ------------------------------------------------------------ weight arena (engine.hip)

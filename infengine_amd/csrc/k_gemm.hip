@@ -268,7 +268,8 @@ struct Cfg {
 
 // Buffer descriptor for the `rows` W rows starting at tile-local row r (all in one matrix).
 template <int EPI, int BN>
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t w_group(const GemmParams& p, int ntile, int r) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t w_group(const GemmParams& p, int ntile, int r,
+                                                          int k0 = 0) {
   const uint16_t* base;
   long long rows;
   if constexpr (EPI == kGemmSwiglu) {
@@ -293,15 +294,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t w_group(const GemmParams& p, i
       rows = 0;
     }
   }
-  const long long bytes = rows > 0 ? rows * p.K * 2 : 0;
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)min(bytes, 0x7fffffffLL), kBufferFlags);
+  // (split K: the buffer starts at column k0 of its first row and ends where the rows end)
+  const long long bytes = rows > 0 ? rows * p.K * 2 - 2LL * k0 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(base + k0), 0, (int)min(bytes, 0x7fffffffLL),
+                                           kBufferFlags);
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_group(const GemmParams& p, int m0, int r) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_group(const GemmParams& p, int m0, int r,
+                                                          int k0 = 0) {
   const int R = m0 + r;
   const long long rows = p.M - R;
-  const long long bytes = rows > 0 ? rows * p.K * 2 : 0;
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(p.x + (size_t)min(R, p.M - 1) * p.K), 0,
+  const long long bytes = rows > 0 ? rows * p.K * 2 - 2LL * k0 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(p.x + (size_t)min(R, p.M - 1) * p.K + k0), 0,
                                            (int)min(bytes, 0x7fffffffLL), kBufferFlags);
 }
 
@@ -464,9 +468,15 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
   const int kg = wave / C::NW, wt = wave % C::NW;
   const int wn = wt / C::WM, wm = wt % C::WM;
   const int kk0 = __builtin_amdgcn_readfirstlane(kg * C::KSUBW);
+  // split K: workgroup b takes k-steps [split * KT, (split + 1) * KT) of tile b % tiles and
+  // writes its fp32 partial product to partial plane `split` of yf
+  const int nsplit = max(1, p.k_splits);
+  const int nb = gridDim.x / nsplit, split = blockIdx.x / nb;
   int mtile, ntile;
-  tile_of<MAPG>(blockIdx.x, gridDim.x, m_tiles, mtile, ntile);
+  tile_of<MAPG>(blockIdx.x - split * nb, nb, m_tiles, mtile, ntile);
   const int m0 = mtile * BM;
+  const int KT = p.K / BK / nsplit;
+  const int k0 = split * KT * BK;
 
   // load j of this wave covers tile rows RPL*g .. RPL*g+RPL-1 with g = wave + NWT*j;
   // lane i fills LDS slot (row RPL*g + i/CPR, chunk i%CPR) from global chunk (i%CPR) ^ swz(row)
@@ -477,7 +487,7 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
   for (int j = 0; j < C::LOADS; ++j) {
     const bool is_w = j < C::W_LOADS;
     const int g = wv + C::NWT * (is_w ? j : j - C::W_LOADS);
-    rsrc[j] = is_w ? w_group<EPI, C::BN>(p, ntile, g * C::RPL) : x_group(p, m0, g * C::RPL);
+    rsrc[j] = is_w ? w_group<EPI, C::BN>(p, ntile, g * C::RPL, k0) : x_group(p, m0, g * C::RPL, k0);
     const int rl = lane / C::CPR, c = (lane % C::CPR) ^ C::swz(g * C::RPL + rl);
     voff[j] = (uint32_t)((rl * p.K + c * 8) * 2);
   }
@@ -497,10 +507,9 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
   // The epilogue's kernel arguments are pulled into SGPRs here: a scalar load still in
   // flight inside the loop would force every LDS wait there to lgkmcnt(0).
   uint16_t* const y = p.y;
-  float* const yf = p.yf;
+  float* const yf = p.yf + (size_t)split * p.M * p.ldy;
   asm volatile("" ::"s"(y), "s"(yf), "s"(p.ldy), "s"(p.M), "s"(p.N));
 
-  const int KT = p.K / BK;
 #pragma unroll
   for (int s0 = 0; s0 < STAGES - 1; ++s0)
     if (s0 < KT) issue_stage<C>(lds, rsrc, voff, wv, s0, s0);
@@ -652,7 +661,7 @@ template <int EPI, int BM = 128, int BK = 64, int STAGES = 3, int MAPG = 1, int 
 int launch_wide(const GemmParams& p, hipStream_t st) {
   const int m_tiles = (p.M + BM - 1) / BM;
   const int n_tiles = (EPI == kGemmSwiglu) ? (p.N + 127) / 128 : (p.N + WBN - 1) / WBN;
-  const long long blocks = (long long)m_tiles * n_tiles;
+  const long long blocks = (long long)m_tiles * n_tiles * std::max(1, p.k_splits);
   IE_REQUIRE(blocks <= 0x7fffffff, "gemm: too many tiles");
   hipLaunchKernelGGL((wide::gemm_wide_kernel<EPI, BM, BK, STAGES, MAPG, WBN, KG>), dim3((unsigned)blocks),
                      dim3(wide::Cfg<BM, BK, STAGES, WBN, KG>::THREADS), 0, st, p, m_tiles);
@@ -793,6 +802,73 @@ int launch_tiled(int epi, const GemmParams& p, hipStream_t st, bool split) {
   return launch_kind(best, epi, p, st);
 }
 
+// Split K's reduction: y = epilogue(sum of the fp32 partial planes), 8 columns per thread.
+// bf16: bf16(sum); residual: bf16(y + bf16(sum)), the unsplit epilogue's roundings.
+template <int EPI>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, int splits, int M,
+                                                           int N, uint16_t* y, int ldy) {
+  const int per_row = N / 8;
+  const size_t total = (size_t)M * per_row, plane = (size_t)M * N;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int m = (int)(i / per_row), n = (int)(i % per_row) * 8;
+    const float* src = part + (size_t)m * N + n;
+    float4 a = *reinterpret_cast<const float4*>(src), b = *reinterpret_cast<const float4*>(src + 4);
+    for (int s = 1; s < splits; ++s) {
+      const float4 c = *reinterpret_cast<const float4*>(src + s * plane);
+      const float4 d = *reinterpret_cast<const float4*>(src + s * plane + 4);
+      a.x += c.x, a.y += c.y, a.z += c.z, a.w += c.w;
+      b.x += d.x, b.y += d.y, b.z += d.z, b.w += d.w;
+    }
+    uint4 o = make_uint4(pack_bf2(a.x, a.y), pack_bf2(a.z, a.w), pack_bf2(b.x, b.y), pack_bf2(b.z, b.w));
+    uint16_t* dst = y + (size_t)m * ldy + n;
+    if constexpr (EPI == kGemmResid) {
+      const uint4 r = *reinterpret_cast<const uint4*>(dst);
+      o = make_uint4(pack_bf2(bf_lo(r.x) + bf_lo(o.x), bf_hi(r.x) + bf_hi(o.x)),
+                     pack_bf2(bf_lo(r.y) + bf_lo(o.y), bf_hi(r.y) + bf_hi(o.y)),
+                     pack_bf2(bf_lo(r.z) + bf_lo(o.z), bf_hi(r.z) + bf_hi(o.z)),
+                     pack_bf2(bf_lo(r.w) + bf_lo(o.w), bf_hi(r.w) + bf_hi(o.w)));
+    }
+    *reinterpret_cast<uint4*>(dst) = o;
+  }
+}
+
+// Split K when the best tiling leaves at least half the chip idle for a single round: the wide
+// kernel's tiles times the largest K split that divides the k-steps and fits one round of
+// 256 workgroups (at least 2), fp32 partials into p.split_ws, then the reduction.  Returns
+// IE_OK after launching, 1 when split K does not apply.
+int launch_split(int epi, const GemmParams& p, hipStream_t st) {
+  if (!p.split_ws || (epi != kGemmBf16 && epi != kGemmResid) || p.M < kWideMinRows ||
+      p.M > kSplitMaxRows || p.N % 8 != 0 || p.ldy % 8 != 0)
+    return 1;
+  int best = kTileSmall;
+  for (int k = kTileWide; k < kTileKinds; ++k)
+    if (tile_ok(k, epi, p) && tile_cost(k, epi, p.M, p.N) < tile_cost(best, epi, p.M, p.N)) best = k;
+  if (tile_count(best, epi, p.M, p.N) > 128) return 1;
+  const long long tiles = tile_count(kTileWide, kGemmF32, p.M, p.N);
+  const int kt = p.K / 64;
+  int splits = 1;
+  for (int s = 2; s <= 8; ++s)
+    if (kt % s == 0 && tiles * s <= 256) splits = s;
+  if (splits < 2 || (size_t)p.split_ws_bytes < (size_t)splits * p.M * p.N * sizeof(float)) return 1;
+  GemmParams q = p;
+  q.yf = p.split_ws;
+  q.ldy = p.N;
+  q.k_splits = splits;
+  const int rc = launch_wide<kGemmF32, 128, 64, 3, 1, 256, 2>(q, st);
+  if (rc != IE_OK) return rc;
+  const size_t total = (size_t)p.M * p.N / 8;
+  const int blocks = (int)std::min<size_t>((total + 255) / 256, 2048);
+  if (epi == kGemmResid)
+    hipLaunchKernelGGL(split_reduce_kernel<kGemmResid>, dim3(blocks), dim3(256), 0, st,
+                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
+  else
+    hipLaunchKernelGGL(split_reduce_kernel<kGemmBf16>, dim3(blocks), dim3(256), 0, st,
+                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
 }  // namespace
 
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
@@ -808,6 +884,9 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
   if (gemm_skinny_fits(p)) return launch_gemm_skinny(epi, p, st);
   IE_REQUIRE(epi >= kGemmBf16 && epi <= kGemmSwiglu, "gemm: epilogue %d needs M <= 16", epi);
   IE_REQUIRE(!p.ss_in && !p.ss_out, "gemm: the folded RMSNorm needs M <= 16");
+  IE_REQUIRE(p.k_splits <= 1, "gemm: k_splits is the launcher's");
+  const int rc = launch_split(epi, p, st);
+  if (rc != 1) return rc;
   return launch_tiled(epi, p, st, true);
 }
 
