@@ -364,7 +364,9 @@ int ie_context_set_graph(ie_context* c, int enable) {
 
 size_t ie_attn_workspace_size(int max_seq_len) {
   const int S = max_seq_len < 1 ? 1 : max_seq_len;
-  const size_t a = decode_ws_bytes(1), b = prefill_attn_bytes(S);
+  // q/k/v, rotated q, then split-K partials of the q/k/v projection (prompts of up to 512)
+  const size_t a = decode_ws_bytes(1),
+               b = prefill_attn_bytes(S) + align256(gemm_split_bytes(std::min(S, kSplitMaxRows), kQKVDim));
   return a > b ? a : b;
 }
 
@@ -567,6 +569,9 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, in
     g.N = kQKVDim;
     g.K = kHidden;
     g.ldy = kQKVDim;
+    // split K's partials after q/k/v and the rotated q (the rest of the workspace)
+    g.split_ws = reinterpret_cast<float*>(wsb + prefill_attn_bytes(S));
+    g.split_ws_bytes = (long long)(ie_attn_workspace_size(S) - prefill_attn_bytes(S));
     IE_TRY(launch_gemm(kGemmBf16, g, st));
     IE_TRY(launch_qkv_rope_scatter(S, 0, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl, nullptr, 0,
                                    st, block_table, n_pages));
@@ -582,7 +587,7 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, in
     o.K = kHidden;
     o.ldy = kHidden;
     o.split_ws = reinterpret_cast<float*>(wsb);  // q/k/v and rotated q are dead
-    o.split_ws_bytes = (long long)prefill_split_bytes(S);
+    o.split_ws_bytes = (long long)std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S));
     IE_TRY(launch_gemm(kGemmResid, o, st));
     IE_TRY(launch_rmsnorm(S, data_buffer, L.post_attention_layernorm, aux_buffer, st));
     GemmParams gu{};
@@ -605,7 +610,8 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, in
     dn.K = kFFN;
     dn.ldy = kHidden;
     dn.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
-    dn.split_ws_bytes = (long long)prefill_split_bytes(S);
+    dn.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
+                                    align256((size_t)S * kFFN * 2));
     IE_TRY(launch_gemm(kGemmResid, dn, st));
   }
   // prefill.cu:41-43: final norm, lm_head on the last row only, argmax
@@ -1118,6 +1124,9 @@ int ie_attn(ie_context* c, const float* d_rope_cos, const float* d_rope_sin, int
   g.N = kQKVDim;
   g.K = kHidden;
   g.ldy = kQKVDim;
+  // split-K partials (both projections) after q/k/v and the rotated q
+  g.split_ws = reinterpret_cast<float*>(wsb + prefill_attn_bytes(S));
+  g.split_ws_bytes = (long long)(ie_attn_workspace_size(S) - prefill_attn_bytes(S));
   IE_TRY(launch_gemm(kGemmBf16, g, st));
   IE_TRY(launch_qkv_rope_scatter(S, 0, qkv, d_rope_cos, d_rope_sin, qrot, kvl,
                                  kvl + (size_t)kKVHeads * kKVPlane, nullptr, 0, st));
@@ -1133,6 +1142,8 @@ int ie_attn(ie_context* c, const float* d_rope_cos, const float* d_rope_sin, int
   o.N = kHidden;
   o.K = kHidden;
   o.ldy = kHidden;
+  o.split_ws = g.split_ws;
+  o.split_ws_bytes = g.split_ws_bytes;
   return launch_gemm(kGemmBf16, o, st);
 }
 

@@ -833,9 +833,10 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, in
   }
 }
 
-// Split K when the best tiling leaves at least half the chip idle for a single round: the wide
-// kernel's tiles times the largest K split that divides the k-steps and fits one round of
-// 256 workgroups (at least 2), fp32 partials into p.split_ws, then the reduction.  Returns
+// Split K when the best tiling is a single round that leaves at least half the chip idle, or
+// one of 128 x 128 tiles: the wide kernel's tiles times the largest K split that divides the
+// k-steps, fits one round of 256 workgroups and whose partials fit p.split_ws (at least 2),
+// fp32 partials into p.split_ws, then the reduction.  Returns
 // IE_OK after launching, 1 when split K does not apply.
 int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   if (!p.split_ws || (epi != kGemmBf16 && epi != kGemmResid) || p.M < kWideMinRows ||
@@ -844,13 +845,17 @@ int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   int best = kTileSmall;
   for (int k = kTileWide; k < kTileKinds; ++k)
     if (tile_ok(k, epi, p) && tile_cost(k, epi, p.M, p.N) < tile_cost(best, epi, p.M, p.N)) best = k;
-  if (tile_count(best, epi, p.M, p.N) > 128) return 1;
+  // a single round that leaves half the chip idle, or one of 128 x 128 tiles (the older,
+  // slower kernel)
+  const long long best_tiles = tile_count(best, epi, p.M, p.N);
+  if (best_tiles > 256 || (best_tiles > 128 && best != kTileSmall)) return 1;
   const long long tiles = tile_count(kTileWide, kGemmF32, p.M, p.N);
   const int kt = p.K / 64;
+  const size_t plane = (size_t)p.M * p.N * sizeof(float);
   int splits = 1;
   for (int s = 2; s <= 8; ++s)
-    if (kt % s == 0 && tiles * s <= 256) splits = s;
-  if (splits < 2 || (size_t)p.split_ws_bytes < (size_t)splits * p.M * p.N * sizeof(float)) return 1;
+    if (kt % s == 0 && tiles * s <= 256 && (size_t)s * plane <= (size_t)p.split_ws_bytes) splits = s;
+  if (splits < 2) return 1;
   GemmParams q = p;
   q.yf = p.split_ws;
   q.ldy = p.N;

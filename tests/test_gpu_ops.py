@@ -346,9 +346,11 @@ def test_decode_attn_config2(hip, ctx, rope, pos):
     assert int(torch.count_nonzero(others[layer + 1:])) == 0
 
 
-def test_attn_prefill_op(hip, ctx, rope):
+# S = 256: both projections split K (fp32 partials + reduction), the q/k/v one over three matrices
+@pytest.mark.parametrize("S", [96, 256])
+def test_attn_prefill_op(hip, ctx, rope, S):
     cos, sin, dcos, dsin = rope
-    S, layer = 96, 2
+    layer = 2
     say(f"attn (prefill) seq_len={S}")
     w, dw = _attn_weights(16)
     x = orc.synthetic((S, H), 16, 600, 0.0, 1.0)
