@@ -161,7 +161,7 @@ struct GemmParams {
   uint16_t* xw_out;
   const uint16_t* xw_norm;
   float* ss_out;
-  // Split K (bf16 / residual epilogues, kWideMinRows <= M <= kSplitMaxRows): scratch for
+  // Split K (bf16 / residual epilogues, 16 < M <= kSplitMaxRows): scratch for
   // fp32 partial products [splits][M][N]; when set and the tiles would fill at most half the
   // chip, K is split across workgroups and a reduction applies the epilogue.
   float* split_ws;

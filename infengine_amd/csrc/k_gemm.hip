@@ -839,8 +839,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, in
 // fp32 partials into p.split_ws, then the reduction.  Returns
 // IE_OK after launching, 1 when split K does not apply.
 int launch_split(int epi, const GemmParams& p, hipStream_t st) {
-  if (!p.split_ws || (epi != kGemmBf16 && epi != kGemmResid) || p.M < kWideMinRows ||
-      p.M > kSplitMaxRows || p.N % 8 != 0 || p.ldy % 8 != 0)
+  // (below kWideMinRows too: a 128-row tile half empty still beats a few 128 x 128 tiles)
+  if (!p.split_ws || (epi != kGemmBf16 && epi != kGemmResid) || p.M > kSplitMaxRows ||
+      p.N % 8 != 0 || p.ldy % 8 != 0)
     return 1;
   int best = kTileSmall;
   for (int k = kTileWide; k < kTileKinds; ++k)
