@@ -599,6 +599,9 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, in
     gu.N = kFFN;
     gu.K = kHidden;
     gu.ldy = kFFN;
+    gu.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
+    gu.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
+                                    align256((size_t)S * kFFN * 2));
     IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
     GemmParams dn{};
     dn.x = h;
@@ -1045,7 +1048,7 @@ int ie_gemm_ex(ie_context* c, int epilogue, int m, int k, int n, const ie_bf16* 
   g.ldy = n;
   // split K's partials: a context-owned scratch, grown on first use (op-level entry; the
   // engine passes its own workspace)
-  const size_t need = (epilogue == IE_GEMM_BF16 || epilogue == IE_GEMM_RESID) ? gemm_split_bytes(m, n) : 0;
+  const size_t need = epilogue == IE_GEMM_F32 ? 0 : gemm_split_bytes(m, epilogue == IE_GEMM_SWIGLU ? 2 * n : n);
   if (need > c->gemm_ws_bytes) {
     IE_CHECK_HIP(hipStreamSynchronize(c->stream));
     if (c->gemm_ws) IE_CHECK_HIP(hipFree(c->gemm_ws));

@@ -161,7 +161,7 @@ struct GemmParams {
   uint16_t* xw_out;
   const uint16_t* xw_norm;
   float* ss_out;
-  // Split K (bf16 / residual epilogues, 16 < M <= kSplitMaxRows): scratch for
+  // Split K (bf16 / residual / SwiGLU epilogues, 16 < M <= kSplitMaxRows): scratch for
   // fp32 partial products [splits][M][N]; when set and the tiles would fill at most half the
   // chip, K is split across workgroups and a reduction applies the epilogue.
   float* split_ws;
@@ -169,9 +169,10 @@ struct GemmParams {
   int k_splits;  // set by the launcher for the wide kernel (0 / 1: no split)
 };
 constexpr int kSplitMaxRows = 512;
-// Scratch bytes split K may use for an M-row product with n output columns.
+// Scratch bytes split K may use for an M-row product with n output columns (SwiGLU: 2 x the
+// output columns): 2048 partial rows, i.e. up to 16 planes at M <= 128, 4 at M = 512.
 inline size_t gemm_split_bytes(int M, int n) {
-  return M <= kSplitMaxRows ? (size_t)4 * M * n * sizeof(float) : 0;
+  return M <= kSplitMaxRows ? (size_t)(4 * M > 2048 ? 4 * M : 2048) * n * sizeof(float) : 0;
 }
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st);
 

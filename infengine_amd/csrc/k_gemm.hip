@@ -802,23 +802,44 @@ int launch_tiled(int epi, const GemmParams& p, hipStream_t st, bool split) {
   return launch_kind(best, epi, p, st);
 }
 
+// Sum of the split planes of 8 consecutive partials.
+__device__ __forceinline__ void split_sum8(const float* src, size_t plane, int splits, float4& a,
+                                           float4& b) {
+  a = *reinterpret_cast<const float4*>(src);
+  b = *reinterpret_cast<const float4*>(src + 4);
+  for (int s = 1; s < splits; ++s) {
+    const float4 c = *reinterpret_cast<const float4*>(src + s * plane);
+    const float4 d = *reinterpret_cast<const float4*>(src + s * plane + 4);
+    a.x += c.x, a.y += c.y, a.z += c.z, a.w += c.w;
+    b.x += d.x, b.y += d.y, b.z += d.z, b.w += d.w;
+  }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  g = bf2f(f2bf(g));
+  return g * (1.0f / (1.0f + expf(-g))) * bf2f(f2bf(u));
+}
+
 // Split K's reduction: y = epilogue(sum of the fp32 partial planes), 8 columns per thread.
-// bf16: bf16(sum); residual: bf16(y + bf16(sum)), the unsplit epilogue's roundings.
+// bf16: bf16(sum); residual: bf16(y + bf16(sum)); SwiGLU (planes of 2N columns, gate then up):
+// bf16(silu(bf16(g)) * bf16(u)) -- the unsplit epilogues' roundings.
 template <int EPI>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, int splits, int M,
                                                            int N, uint16_t* y, int ldy) {
+  constexpr int W = EPI == kGemmSwiglu ? 2 : 1;  // plane width in output columns
   const int per_row = N / 8;
-  const size_t total = (size_t)M * per_row, plane = (size_t)M * N;
+  const size_t total = (size_t)M * per_row, plane = (size_t)M * N * W;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
     const int m = (int)(i / per_row), n = (int)(i % per_row) * 8;
-    const float* src = part + (size_t)m * N + n;
-    float4 a = *reinterpret_cast<const float4*>(src), b = *reinterpret_cast<const float4*>(src + 4);
-    for (int s = 1; s < splits; ++s) {
-      const float4 c = *reinterpret_cast<const float4*>(src + s * plane);
-      const float4 d = *reinterpret_cast<const float4*>(src + s * plane + 4);
-      a.x += c.x, a.y += c.y, a.z += c.z, a.w += c.w;
-      b.x += d.x, b.y += d.y, b.z += d.z, b.w += d.w;
+    const float* src = part + (size_t)m * N * W + n;
+    float4 a, b;
+    split_sum8(src, plane, splits, a, b);
+    if constexpr (EPI == kGemmSwiglu) {
+      float4 c, d;
+      split_sum8(src + N, plane, splits, c, d);
+      a = make_float4(silu_mul(a.x, c.x), silu_mul(a.y, c.y), silu_mul(a.z, c.z), silu_mul(a.w, c.w));
+      b = make_float4(silu_mul(b.x, d.x), silu_mul(b.y, d.y), silu_mul(b.z, d.z), silu_mul(b.w, d.w));
     }
     uint4 o = make_uint4(pack_bf2(a.x, a.y), pack_bf2(a.z, a.w), pack_bf2(b.x, b.y), pack_bf2(b.z, b.w));
     uint16_t* dst = y + (size_t)m * ldy + n;
@@ -840,9 +861,10 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, in
 // IE_OK after launching, 1 when split K does not apply.
 int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   // (below kWideMinRows too: a 128-row tile half empty still beats a few 128 x 128 tiles)
-  if (!p.split_ws || (epi != kGemmBf16 && epi != kGemmResid) || p.M > kSplitMaxRows ||
-      p.N % 8 != 0 || p.ldy % 8 != 0)
+  if (!p.split_ws || epi == kGemmF32 || p.M > kSplitMaxRows || p.N % 8 != 0 || p.ldy % 8 != 0)
     return 1;
+  const bool sw = epi == kGemmSwiglu;
+  if (sw && p.N % 16 != 0) return 1;
   int best = kTileSmall;
   for (int k = kTileWide; k < kTileKinds; ++k)
     if (tile_ok(k, epi, p) && tile_cost(k, epi, p.M, p.N) < tile_cost(best, epi, p.M, p.N)) best = k;
@@ -850,22 +872,33 @@ int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   // slower kernel)
   const long long best_tiles = tile_count(best, epi, p.M, p.N);
   if (best_tiles > 256 || (best_tiles > 128 && best != kTileSmall)) return 1;
-  const long long tiles = tile_count(kTileWide, kGemmF32, p.M, p.N);
+  // SwiGLU: one fp32 product over the gate rows then the up rows (2N columns)
+  const int NP = sw ? 2 * p.N : p.N;
+  const long long tiles = tile_count(kTileWide, kGemmF32, p.M, NP);
   const int kt = p.K / 64;
-  const size_t plane = (size_t)p.M * p.N * sizeof(float);
+  const size_t plane = (size_t)p.M * NP * sizeof(float);
   int splits = 1;
   for (int s = 2; s <= 8; ++s)
     if (kt % s == 0 && tiles * s <= 256 && (size_t)s * plane <= (size_t)p.split_ws_bytes) splits = s;
   if (splits < 2) return 1;
   GemmParams q = p;
   q.yf = p.split_ws;
-  q.ldy = p.N;
+  q.ldy = NP;
   q.k_splits = splits;
+  if (sw) {
+    q.N = NP;
+    q.n0 = p.N;  // rows [0, N) of w0 (gate), then [N, 2N) of w1 (up)
+    q.n1 = p.N;
+    q.w2 = p.w1;
+  }
   const int rc = launch_wide<kGemmF32, 128, 64, 3, 1, 256, 2>(q, st);
   if (rc != IE_OK) return rc;
   const size_t total = (size_t)p.M * p.N / 8;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 2048);
-  if (epi == kGemmResid)
+  if (sw)
+    hipLaunchKernelGGL(split_reduce_kernel<kGemmSwiglu>, dim3(blocks), dim3(256), 0, st,
+                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
+  else if (epi == kGemmResid)
     hipLaunchKernelGGL(split_reduce_kernel<kGemmResid>, dim3(blocks), dim3(256), 0, st,
                        p.split_ws, splits, p.M, p.N, p.y, p.ldy);
   else
