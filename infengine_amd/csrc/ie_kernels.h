@@ -168,7 +168,7 @@ struct GemmParams {
   long long split_ws_bytes;
   int k_splits;  // set by the launcher for the wide kernel (0 / 1: no split)
 };
-constexpr int kSplitMaxRows = 512;
+constexpr int kSplitMaxRows = 1024;
 // Scratch bytes split K may use for an M-row product with n output columns (SwiGLU: 2 x the
 // output columns): 2048 partial rows, i.e. up to 16 planes at M <= 128, 4 at M = 512.
 inline size_t gemm_split_bytes(int M, int n) {
