@@ -36,7 +36,7 @@ typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) short4_t lds_short4;
 
-constexpr int BQ = 32;                // query rows per workgroup (two 16-row MFMA blocks)
+constexpr int BQ = 32;                // query rows per workgroup at most (QI = 2 blocks of 16)
 constexpr int BKEY = 64;              // keys per LDS tile
 constexpr int TC = BKEY * 16;         // 16-byte chunks per K (or V) tile
 constexpr int kRowBytes = kHeadDim * 2;
@@ -66,13 +66,13 @@ __device__ __forceinline__ void issue_tile(u32x4_t* lds, __amdgpu_buffer_rsrc_t 
 // mask (key <= q, key < nkeys).  Rescales l and o by the max's change and
 // packs P^T as the P.V MFMA's B operand: contraction slot 8 G + r <-> key 32 ks2 + 4 G + r, slot
 // 8 G + 4 + r <-> key 32 ks2 + 16 + 4 G + r.
-template <bool MASK>
-__device__ __forceinline__ void softmax_tile(f32x4_t (&s)[2][4], float (&m)[2], float (&l)[2],
-                                             f32x4_t (&o)[2][8], bf16x8_t (&pb)[2][2], int key0,
+template <bool MASK, int QI>
+__device__ __forceinline__ void softmax_tile(f32x4_t (&s)[QI][4], float (&m)[QI], float (&l)[QI],
+                                             f32x4_t (&o)[QI][8], bf16x8_t (&pb)[QI][2], int key0,
                                              int q0, int nkeys, int G) {
   constexpr float c = 0.08838834764831845f * 1.4426950408889634f;  // 1/sqrt(128) (softmax.cu:79) * log2(e)
 #pragma unroll
-  for (int qi = 0; qi < 2; ++qi) {
+  for (int qi = 0; qi < QI; ++qi) {
     float mt = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
@@ -115,9 +115,12 @@ __device__ __forceinline__ void softmax_tile(f32x4_t (&s)[2][4], float (&m)[2], 
   }
 }
 
-template <bool PAGED>
+// QI: 16-row query blocks per wave (2: 32 query rows per workgroup; 1: 16, twice the workgroups
+// for short prompts).
+template <bool PAGED, int QI>
 __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams p) {
   __shared__ u32x4_t lds[2 * 2 * TC];  // [stage][K | V][key][16 chunks], 64 KiB
+  constexpr int BQ = 16 * QI;
 
   const int nqb = (p.S + BQ - 1) / BQ;
   // workgroup b -> (query block, kv head): the first half of the grid takes the longest causal
@@ -148,22 +151,24 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
   }
 
   // Q^T fragments: qf[qi][ks] = Q[row0 + 16 qi + fr][h][32 ks + 8 G .. +8]
-  bf16x8_t qf[2][4];
+  bf16x8_t qf[QI][4];
 #pragma unroll
-  for (int qi = 0; qi < 2; ++qi) {
+  for (int qi = 0; qi < QI; ++qi) {
     const int qr = row0 + min(16 * qi + fr, rows - 1);
     const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(p.q + ((size_t)qr * kQHeads + h) * kHeadDim);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) qf[qi][ks] = __builtin_bit_cast(bf16x8_t, qrow[4 * ks + G]);
   }
 
-  f32x4_t o[2][8];
+  f32x4_t o[QI][8];
 #pragma unroll
-  for (int qi = 0; qi < 2; ++qi)
+  for (int qi = 0; qi < QI; ++qi)
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[qi][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // m: running max of the raw scores (the scale is applied inside the exponent)
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  float m[QI], l[QI];
+#pragma unroll
+  for (int qi = 0; qi < QI; ++qi) m[qi] = -INFINITY, l[qi] = 0.f;
 
   // Paged KV: tile t's buffers are its page's rows; the page id of tile t+1 is loaded (a vector
   // load, so the loop's vmcnt wait covers it) while tile t is multiplied.
@@ -202,25 +207,26 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
     const int key0 = t * BKEY;
 
     // ---- S^T blocks: s[qi][kb][r] = S[q = row0 + 16 qi + fr][key = key0 + 16 kb + 4 G + r]
-    f32x4_t s[2][4];
+    f32x4_t s[QI][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      s[0][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      s[1][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int qi = 0; qi < QI; ++qi) s[qi][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const bf16x8_t a = __builtin_bit_cast(bf16x8_t, kt[kv_slot(16 * kb + fr, 4 * ks + G)]);
-        s[0][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][ks], s[0][kb], 0, 0, 0);
-        s[1][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][ks], s[1][kb], 0, 0, 0);
+#pragma unroll
+        for (int qi = 0; qi < QI; ++qi)
+          s[qi][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[qi][ks], s[qi][kb], 0, 0, 0);
       }
     }
 
     // ---- online softmax; causal masking only on the tiles that reach past the block's first query
-    bf16x8_t pb[2][2];
+    bf16x8_t pb[QI][2];
     if (key0 + BKEY - 1 <= p.start_pos + row0)
-      softmax_tile<false>(s, m, l, o, pb, key0, p.start_pos + row0 + fr, nkeys, G);
+      softmax_tile<false, QI>(s, m, l, o, pb, key0, p.start_pos + row0 + fr, nkeys, G);
     else
-      softmax_tile<true>(s, m, l, o, pb, key0, p.start_pos + row0 + fr, nkeys, G);
+      softmax_tile<true, QI>(s, m, l, o, pb, key0, p.start_pos + row0 + fr, nkeys, G);
 
     // ---- O^T[d][q] += V^T[d][keys] . P^T[keys][q]; the V^T fragment of dims 16 db .. +15 and
     //      the slot order above is two transposed 8-byte reads per lane
@@ -237,15 +243,16 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
         const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)vb);
         const short4_t both[2] = {lo, hi};
         const bf16x8_t a = __builtin_bit_cast(bf16x8_t, both);
-        o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][ks2], o[0][db], 0, 0, 0);
-        o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][ks2], o[1][db], 0, 0, 0);
+#pragma unroll
+        for (int qi = 0; qi < QI; ++qi)
+          o[qi][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qi][ks2], o[qi][db], 0, 0, 0);
       }
     }
   }
 
   // ---- o[qi][db][r] = O[q = row0 + 16 qi + fr][d = 16 db + 4 G + r] (unnormalised)
 #pragma unroll
-  for (int qi = 0; qi < 2; ++qi) {
+  for (int qi = 0; qi < QI; ++qi) {
     if (16 * qi + fr < rows) {
       const float inv = 1.0f / l[qi];
       uint16_t* dst = p.out + (size_t)(row0 + 16 * qi + fr) * kHidden + h * kHeadDim;
@@ -264,11 +271,18 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
 int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t st) {
   IE_REQUIRE(p.S >= 1 && p.start_pos >= 0 && p.start_pos + p.S <= kMaxCtx,
              "attn_prefill: rows [%d, %d) exceed the KV cache", p.start_pos, p.start_pos + p.S);
-  const int nqb = (p.S + BQ - 1) / BQ;
-  if (p.block_table)
-    hipLaunchKernelGGL(flash_prefill_kernel<true>, dim3(nqb * kKVHeads), dim3(256), 0, st, p);
+  // 32 query rows per workgroup while that fills the chip (S >= 1024: 256 workgroups), else 16
+  const bool wide = p.S >= 1024;
+  const int nqb = wide ? (p.S + BQ - 1) / BQ : (p.S + 15) / 16;
+  const dim3 grid(nqb * kKVHeads);
+  if (p.block_table && wide)
+    hipLaunchKernelGGL((flash_prefill_kernel<true, 2>), grid, dim3(256), 0, st, p);
+  else if (p.block_table)
+    hipLaunchKernelGGL((flash_prefill_kernel<true, 1>), grid, dim3(256), 0, st, p);
+  else if (wide)
+    hipLaunchKernelGGL((flash_prefill_kernel<false, 2>), grid, dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL(flash_prefill_kernel<false>, dim3(nqb * kKVHeads), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((flash_prefill_kernel<false, 1>), grid, dim3(256), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
