@@ -878,7 +878,7 @@ int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   const int kt = p.K / 64;
   const size_t plane = (size_t)p.M * NP * sizeof(float);
   int splits = 1;
-  for (int s = 2; s <= 8; ++s)
+  for (int s = 2; s <= 16; ++s)
     if (kt % s == 0 && tiles * s <= 256 && (size_t)s * plane <= (size_t)p.split_ws_bytes) splits = s;
   if (splits < 2) return 1;
   GemmParams q = p;
