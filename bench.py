@@ -186,7 +186,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the single-GPU path is the whole deliverable; see DESIGN.md for how it shards)",
+              "(the single-GPU path is the whole deliverable of this build)",
               file=sys.stderr)
         return 2
 
