@@ -188,6 +188,9 @@ int load_safetensors(ie_model_weights* out, const char* const* paths, int n_path
 // M <= 16 streaming variant (batched decode); launch_gemm routes to it when it fits.
 bool gemm_skinny_fits(const GemmParams& p);
 int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st);
+// 16 < M <= 48 (short prompts): the streaming kernel over 2-3 X row-blocks
+bool gemm_skinny_mb_fits(int epi, const GemmParams& p);
+int launch_gemm_skinny_mb(int epi, const GemmParams& p, hipStream_t st);
 
 // ------------------------------------------------------------ prefill attention
 struct AttnPrefillParams {

@@ -921,6 +921,7 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
              "gemm: weight split points n0=%d n0+n1=%d inside N=%d must be multiples of 16", p.n0,
              p.n0 + p.n1, p.N);
   if (gemm_skinny_fits(p)) return launch_gemm_skinny(epi, p, st);
+  if (gemm_skinny_mb_fits(epi, p)) return launch_gemm_skinny_mb(epi, p, st);
   IE_REQUIRE(epi >= kGemmBf16 && epi <= kGemmSwiglu, "gemm: epilogue %d needs M <= 16", epi);
   IE_REQUIRE(!p.ss_in && !p.ss_out, "gemm: the folded RMSNorm needs M <= 16");
   IE_REQUIRE(p.k_splits <= 1, "gemm: k_splits is the launcher's");

@@ -348,6 +348,170 @@ void gemm_skinny_kernel(GemmParams p) {
   }
 }
 
+// X blocks of one step (rows 16 mb + 4 j + q, chunk r), for the 17-48-row kernel.
+template <int MB>
+__device__ __forceinline__ void mb_load_x(const __amdgpu_buffer_rsrc_t (&xr)[MB], const SkSrc& src,
+                                          int ks, u32x4_t (&xv)[MB][4]) {
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      xv[mb][j] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr[mb], src.wo[j], 2 * ks, 0));
+}
+
+// One step of the 17-48-row kernel: the X blocks into the wave's LDS slots 1..MB (then their
+// registers refilled with step kx), each W tile into slot 0 in turn, 4 k-chunks x MB MFMAs per
+// tile; the W registers refilled with step kw.
+template <int NT, int MB>
+__device__ __forceinline__ void mb_step(u32x4_t (*tr)[256], const SkSrc& src,
+                                        const __amdgpu_buffer_rsrc_t (&xr)[MB], u32x4_t (&w)[NT][4],
+                                        u32x4_t (&xv)[MB][4], f32x4_t (&acc)[NT][MB], int r, int q,
+                                        bool lx, int kx, bool lw, int kw) {
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) sk_put(tr[1 + mb], xv[mb], r, q);
+  if (lx) mb_load_x<MB>(xr, src, kx, xv);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    sk_put(tr[0], w[t], r, q);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, tr[0][r * 16 + ((4 * c + q) ^ r)]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        acc[t][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            a, __builtin_bit_cast(bf16x8_t, tr[1 + mb][r * 16 + ((4 * c + q) ^ r)]), acc[t][mb],
+            0, 0, 0);
+    }
+  }
+  if (lw) sk_load_w<NT>(src, kw, w);
+}
+
+// 17-48 rows (short prompts): the same streaming shape with the X rows as MB blocks of 16 (each
+// with its own buffer range, rows past M read as zero), every W k-chunk multiplied against each
+// block; bf16, residual and SwiGLU epilogues.  The weights stream once; the X blocks are re-read
+// by every workgroup from L2.
+template <int EPI, int KC, int MB>
+__global__ __launch_bounds__(kSkSplit * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_skinny_mb_kernel(GemmParams p) {
+  constexpr bool SW = EPI == kGemmSwiglu;
+  constexpr int NT = SW ? 2 : 1;
+  __shared__ u32x4_t tr[kSkSplit][1 + MB][256];  // per wave: a W tile, then the MB X blocks
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * kSkRows;
+  const int K = KC;
+
+  SkSrc src;
+  __amdgpu_buffer_rsrc_t xr[MB];
+  if constexpr (SW) {
+    const int rows = min(kSkRows, p.N - n0);
+    src.w[0] = sk_rsrc(p.w0 + (size_t)n0 * K, rows, K);
+    src.w[1] = sk_rsrc(p.w1 + (size_t)n0 * K, rows, K);
+  } else {
+    const int e0 = min(p.n0, p.N), e1 = min(p.n0 + p.n1, p.N);
+    const uint16_t* base;
+    int end;
+    if (n0 < e0) base = p.w0 + (size_t)n0 * K, end = e0;
+    else if (n0 < e1) base = p.w1 + (size_t)(n0 - e0) * K, end = e1;
+    else base = p.w2 + (size_t)(n0 - e1) * K, end = p.N;
+    src.w[0] = sk_rsrc(base, min(kSkRows, end - n0), K);
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+    xr[mb] = sk_rsrc(p.x + (size_t)16 * mb * K, max(0, min(16, p.M - 16 * mb)), K);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    src.wo[j] = (uint32_t)((4 * j + q) * K + 8 * r) * 2u;
+    src.xo[j] = src.wo[j];
+  }
+  asm volatile("" : "+v"(src.wo[0]), "+v"(src.wo[1]), "+v"(src.wo[2]), "+v"(src.wo[3]));
+  const int kq = K / kSkSplit;
+  const int kbase = wave * kq;
+  constexpr int steps = KC / kSkSplit / kSkStep;
+
+  f32x4_t acc[NT][MB];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  u32x4_t w0[NT][4], w1[NT][4], xv[MB][4];
+  sk_load_w<NT>(src, kbase, w0);
+  mb_load_x<MB>(xr, src, kbase, xv);
+  if (steps > 1) sk_load_w<NT>(src, kbase + kSkStep, w1);
+#pragma unroll
+  for (int s = 0; s < steps; s += 2) {
+    const int k1 = kbase + (s + 1) * kSkStep;
+    mb_step<NT, MB>(tr[wave], src, xr, w0, xv, acc, r, q, s + 1 < steps, k1, s + 2 < steps,
+                    k1 + kSkStep);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 1 < steps)
+      mb_step<NT, MB>(tr[wave], src, xr, w1, xv, acc, r, q, s + 2 < steps, k1 + kSkStep,
+                      s + 3 < steps, k1 + 2 * kSkStep);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // sum the K quarters through each wave's own LDS tiles (its last reads precede these writes)
+  u32x4_t* red = &tr[wave][0][0];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) red[(t * MB + mb) * 64 + lane] = __builtin_bit_cast(u32x4_t, acc[t][mb]);
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 1; w < kSkSplit; ++w)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        acc[t][mb] += __builtin_bit_cast(f32x4_t, tr[w][0][(t * MB + mb) * 64 + lane]);
+
+  const int n = n0 + 4 * q;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = 16 * mb + r;
+    if (m >= p.M || n >= p.N) continue;
+    uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n);
+    const f32x4_t a0 = acc[0][mb];
+    if constexpr (SW) {
+      const f32x4_t a1 = acc[NT - 1][mb];
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float g = bf2f(f2bf(a0[i])), u = bf2f(f2bf(a1[i]));
+        v[i] = g * (1.0f / (1.0f + expf(-g))) * u;
+      }
+      *dst = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+    } else if constexpr (EPI == kGemmResid) {
+      const uint2 old = *dst;
+      *dst = make_uint2(
+          pack_bf2(bf_lo(old.x) + bf2f(f2bf(a0[0])), bf_hi(old.x) + bf2f(f2bf(a0[1]))),
+          pack_bf2(bf_lo(old.y) + bf2f(f2bf(a0[2])), bf_hi(old.y) + bf2f(f2bf(a0[3]))));
+    } else {
+      *dst = make_uint2(pack_bf2(a0[0], a0[1]), pack_bf2(a0[2], a0[3]));
+    }
+  }
+}
+
+template <int EPI, int MB>
+int launch_mb_k(const GemmParams& p, hipStream_t st) {
+  const int blocks = (p.N + kSkRows - 1) / kSkRows;
+  if (p.K == 4096)
+    hipLaunchKernelGGL((gemm_skinny_mb_kernel<EPI, 4096, MB>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_skinny_mb_kernel<EPI, 14336, MB>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+template <int EPI>
+int launch_mb_e(const GemmParams& p, hipStream_t st) {
+  if (p.M <= 32) return launch_mb_k<EPI, 2>(p, st);
+  return launch_mb_k<EPI, 3>(p, st);
+}
+
 template <int EPI>
 int launch_s(const GemmParams& p, hipStream_t st) {
   const int blocks = (p.N + kSkRows - 1) / kSkRows;
@@ -374,6 +538,24 @@ int launch_s(const GemmParams& p, hipStream_t st) {
 
 bool gemm_skinny_fits(const GemmParams& p) {
   return p.M >= 1 && p.M <= kSkRows && p.K % (kSkSplit * kSkStep) == 0;
+}
+
+bool gemm_skinny_mb_fits(int epi, const GemmParams& p) {
+  // (4 blocks, M = 64, measured 3% slower than split K: 80 KiB of LDS and ~250 VGPRs)
+  return p.M > kSkRows && p.M <= 3 * kSkRows && (p.K == 4096 || p.K == 14336) &&
+         (epi == kGemmBf16 || epi == kGemmResid || epi == kGemmSwiglu) && !p.ss_in && !p.ss_out &&
+         p.N % 4 == 0;
+}
+
+int launch_gemm_skinny_mb(int epi, const GemmParams& p, hipStream_t st) {
+  IE_REQUIRE(gemm_skinny_mb_fits(epi, p), "gemm_skinny_mb: needs 16 < M <= 48, K 4096 or 14336");
+  const int e0 = std::min(p.n0, p.N), e1 = std::min(p.n0 + p.n1, p.N);
+  IE_REQUIRE(epi == kGemmSwiglu ||
+                 ((e0 == p.N || e0 % kSkRows == 0) && (e1 == p.N || e1 % kSkRows == 0)),
+             "gemm_skinny_mb: weight matrix boundaries must fall on multiples of %d rows", kSkRows);
+  if (epi == kGemmSwiglu) return launch_mb_e<kGemmSwiglu>(p, st);
+  if (epi == kGemmResid) return launch_mb_e<kGemmResid>(p, st);
+  return launch_mb_e<kGemmBf16>(p, st);
 }
 
 int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {

@@ -192,11 +192,12 @@ GEMM_EPI = {"bf16": 0, "resid": 1, "f32": 2, "swiglu": 3}
 
 
 @pytest.mark.parametrize("epi", list(GEMM_EPI))
-@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (100, 4096), (300, 1000), (512, 4096),
-                                 (2048, 6144), (2048, 4096), (2048, 14336)])
+@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (40, 1000), (48, 4096), (100, 4096),
+                                 (300, 1000), (512, 4096), (2048, 6144), (2048, 4096), (2048, 14336)])
 def test_gemm_epilogues(hip, ctx, epi, m, n):
     """Every fused epilogue of the MFMA GEMM on each kernel the launcher picks: the skinny
-    streaming kernel (m <= 16, ragged n), 128 x 128 tiles (m = 100, 300: f32 / SwiGLU), K split
+    streaming kernel (m <= 16, ragged n), its 2-4 row-block form (m = 40, 48: bf16 / resid /
+    SwiGLU), 128 x 128 tiles (m = 100, 300: f32 / SwiGLU; f32 at m = 40, 48), K split
     across workgroups with a reduction (bf16 / resid at m = 100, 300, 512), and the prefill sizes:
     192 x 256 tiles (bf16 / resid at n = 6144), 256 x 256 tiles (SwiGLU at n = 4096), 256 x 128
     tiles (the others at n = 4096 and 6144), and at n = 14336 a launch split by output columns
