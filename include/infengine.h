@@ -249,6 +249,16 @@ IE_API size_t ie_top_p_workspace_size(int rows, int vocab);
 IE_API int ie_sample_top_p(ie_context* ctx, int rows, int vocab, const float* d_logits,
                            float temperature, float top_p, uint64_t seed, uint64_t step,
                            int* d_output, void* workspace);
+/* No reference counterpart: ie_sample_top_p without the workspace, for callers that cannot
+ * allocate (HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * allocates nothing: the [rows][vocab] fp32 scratch is a static device array of the library,
+ * one per GPU (rows * vocab <= 16 * 131072 = IE_TOP_P_NOALLOC_MAX; larger calls return
+ * IE_ERR_INVALID_ARG).  Same results as ie_sample_top_p.  Calls that overlap on one GPU (any
+ * context, any stream) share that array and race. */
+#define IE_TOP_P_NOALLOC_MAX (16 * 131072)
+IE_API int ie_sample_top_p_noalloc(ie_context* ctx, int rows, int vocab, const float* d_logits,
+                                   float temperature, float top_p, uint64_t seed, uint64_t step,
+                                   int* d_output);
 
 /* ---- fused decode kernels (building blocks of ie_decode_step, exposed for tests) ---- */
 /* x_resid += W_down . (silu(W_gate . rmsnorm(x_resid)) * (W_up . rmsnorm(x_resid))) */

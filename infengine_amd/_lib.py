@@ -102,6 +102,7 @@ SIGNATURES: dict[str, tuple] = {
     "ie_sample_argmax_rows": (_i, [_p, _i, _i, _p, _p]),
     "ie_top_p_workspace_size": (_sz, [_i, _i]),
     "ie_sample_top_p": (_i, [_p, _i, _i, _p, _f, _f, _u64, _u64, _p, _p]),
+    "ie_sample_top_p_noalloc": (_i, [_p, _i, _i, _p, _f, _f, _u64, _u64, _p]),
     "ie_ffn_block_decode": (_i, [_p, _p, _p, _p, _p, _p, _p]),
     "ie_ffn_gate_up_decode": (_i, [_p, _p, _p, _p, _p, _p]),
     "ie_decoder_layer_decode": (_i, [_p, _W, _i, _i, _p, _p, _p, _p]),

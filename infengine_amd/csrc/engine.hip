@@ -321,6 +321,11 @@ int ie_context_create(ie_context** out, int device, void* stream) {
       rc = IE_ERR_HIP;
       break;
     }
+    // the no-allocation top-p sampler's scratch: resolve this device's address once
+    if (top_p_scratch_init(device) != IE_OK) {
+      rc = IE_ERR_HIP;
+      break;
+    }
     if (hipMemset(c->d_counters, 0, kNumCounters * sizeof(unsigned int)) != hipSuccess ||
         hipMemset(c->d_slots, 0, kNumSlots * sizeof(unsigned long long)) != hipSuccess ||
         hipMemset(c->d_params, 0, 64 * sizeof(int)) != hipSuccess ||
@@ -1209,6 +1214,26 @@ int ie_sample_top_p(ie_context* c, int rows, int vocab, const float* d_logits, f
   IE_REQUIRE(d_logits && d_output && workspace, "sample_top_p: null pointer");
   return launch_top_p(rows, vocab, d_logits, temperature, top_p, seed, step, d_output,
                       static_cast<float*>(workspace), c->stream);
+}
+
+// No allocation: the exponentials go to the library's static per-device scratch
+// (top_p_scratch), resolved when a context was created on this device.  Calls that overlap on
+// one GPU share that scratch and race.
+int ie_sample_top_p_noalloc(ie_context* c, int rows, int vocab, const float* d_logits,
+                            float temperature, float top_p, uint64_t seed, uint64_t step,
+                            int* d_output) {
+  CTX_OK(c);
+  IE_REQUIRE(d_logits && d_output, "sample_top_p_noalloc: null pointer");
+  IE_REQUIRE(rows >= 1 && vocab >= 1, "sample_top_p_noalloc: rows=%d vocab=%d", rows, vocab);
+  IE_REQUIRE((size_t)rows * (size_t)vocab <= kTopPScratchFloats,
+             "sample_top_p_noalloc: rows x vocab = %d x %d exceeds the static scratch of %zu "
+             "logits (use ie_sample_top_p with a workspace)",
+             rows, vocab, kTopPScratchFloats);
+  float* ws = top_p_scratch(c->device);
+  IE_REQUIRE(ws != nullptr, "sample_top_p_noalloc: scratch of device %d not initialised",
+             c->device);
+  return launch_top_p(rows, vocab, d_logits, temperature, top_p, seed, step, d_output, ws,
+                      c->stream);
 }
 
 int ie_ffn_block_decode(ie_context* c, ie_bf16* d_x_resid, const ie_bf16* d_norm_w,

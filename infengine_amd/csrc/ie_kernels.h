@@ -119,6 +119,12 @@ int launch_argmax_rows(int rows, int vocab, const float* logits, int* out,
                        ArgmaxTail tail = ArgmaxTail{});
 int launch_top_p(int rows, int vocab, const float* logits, float temperature, float top_p,
                  uint64_t seed, uint64_t step, int* out, float* ws, hipStream_t st);
+// The no-allocation top-p entry point's scratch (k_sampling.hip): rows * vocab <= this many
+// floats.  top_p_scratch_init(device) resolves the device address of that device's copy (the
+// device must be current; idempotent); top_p_scratch(device) returns it (nullptr before init).
+constexpr size_t kTopPScratchFloats = (size_t)IE_TOP_P_NOALLOC_MAX;
+int top_p_scratch_init(int device);
+float* top_p_scratch(int device);
 
 // ------------------------------------------------------------ MFMA GEMM
 enum GemmEpi : int {

@@ -20,9 +20,46 @@
 //      uniform of (seed, row, step)
 //   4. the sampled token is the smallest id whose kept prefix mass exceeds t
 //      (inverse CDF in token-id order), found with a block-wide exclusive scan.
+#include <mutex>
+
 #include "ie_kernels.h"
 
 namespace ie {
+
+// ---------------------------------------------------------------- no-allocation scratch
+// The top-p sampler's [rows][vocab] fp32 exponentials, for the entry point that takes no
+// workspace: a file-scope device array of kTopPScratchFloats floats (8 MiB), one copy per GPU
+// for the life of the process.  Host code never passes `scratch` itself to a kernel (on the
+// host the name is only a stand-in, not the device address): top_p_scratch_init looks up each
+// device's address once with hipGetSymbolAddress and the launcher passes that.
+static __device__ __align__(256) float scratch[kTopPScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+float* g_scratch_addr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+}  // namespace
+
+int top_p_scratch_init(int device) {
+  IE_REQUIRE(device >= 0 && device < kMaxDevices, "top_p scratch: device %d out of [0, %d)",
+             device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[device]) return IE_OK;
+  int cur = -1;
+  IE_CHECK_HIP(hipGetDevice(&cur));
+  IE_REQUIRE(cur == device, "top_p scratch: device %d is not current (%d is)", device, cur);
+  void* addr = nullptr;
+  IE_CHECK_HIP(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)));
+  IE_REQUIRE(addr != nullptr, "top_p scratch: no device address for device %d", device);
+  g_scratch_addr[device] = static_cast<float*>(addr);
+  return IE_OK;
+}
+
+float* top_p_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_addr[device];
+}
 
 namespace {
 
