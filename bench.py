@@ -228,6 +228,7 @@ def main() -> int:
     n_new = 1 + args.warmup + args.steps
     toks, timed_ms = req.generate(ids, n_new, timed_from=1 + args.warmup)
     assert toks[0] == tok, "ie_generate's prefill token differs from ie_prefill's"
+    assert len(toks) == n_new, "ie_generate stopped early"
     first_pos = args.prompt + args.warmup          # position of the first timed step's token
     last_pos = args.prompt + args.warmup + args.steps - 1
     dt = timed_ms / 1e3

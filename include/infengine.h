@@ -123,16 +123,18 @@ IE_API int ie_decode_step(ie_context* ctx, const ie_model_weights* weights, int 
                           ie_bf16* attn_buffer, float* output_distr, int* output_token,
                           void* workspace, void* kv_cache);
 /* manager.cpp:31-86 (Manager::handle_request) without the tokenizer: copies the prompt ids to
- * tokenid_buff, runs ie_prefill, then max_new_tokens-1 decode steps, writing each token back to
- * tokenid_buff on the device (manager.cpp:75, 84) before the next step reads it.  out_tokens
- * (host, max_new_tokens) receives the prefill's token then each step's.  timed_ms (optional)
- * receives the host wall time of decode steps timed_from .. max_new_tokens-1.  Returns
- * max_new_tokens or a negative status. */
+ * tokenid_buff, runs ie_prefill, then decode steps, writing each token back to tokenid_buff on
+ * the device (manager.cpp:75, 84) before the next step reads it.  out_tokens (host,
+ * max_new_tokens) receives the prefill's token then each step's.  The loop ends after
+ * max_new_tokens tokens, or right after a token equal to eos_token (kept in out_tokens; a
+ * negative eos_token never matches).  timed_ms (optional) receives the host wall time of decode
+ * steps timed_from .. the last one (0 when none ran).  Returns the number of tokens produced
+ * or a negative status. */
 IE_API int ie_generate(ie_context* ctx, const ie_model_weights* weights, const int* prompt,
-                       int prompt_len, int max_new_tokens, int timed_from, int* out_tokens,
-                       int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
-                       ie_bf16* attn_buffer, float* output_distr, int* output_token,
-                       void* workspace, void* kv_cache, double* timed_ms);
+                       int prompt_len, int max_new_tokens, int eos_token, int timed_from,
+                       int* out_tokens, int* tokenid_buff, ie_bf16* data_buffer,
+                       ie_bf16* aux_buffer, ie_bf16* attn_buffer, float* output_distr,
+                       int* output_token, void* workspace, void* kv_cache, double* timed_ms);
 
 /* Batched decode (no reference counterpart: manager.h:19-24 RequestContext is
  * unused there).  `batch` independent sequences; seq_lens is a HOST array;

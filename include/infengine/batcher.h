@@ -132,22 +132,32 @@ class ContinuousBatcher {
     r.pages.clear();
   }
 
-  // Prefill alone, writing the prompt's K/V rows into the request's pages.
+  // Prefill alone, writing the prompt's K/V rows into the request's pages.  If it throws, the
+  // request is back at the head of the queue with no pages and the exception propagates.
   void admit(int id) {
     Req& r = reqs_[id];
     const int S = r.prompt_len;
-    ensure_prefill_buffers(S);
     const int need = pages_for(r.tokens, r.max_new);
     for (int i = 0; i < need; ++i) {
       r.pages.push_back(free_pages_.back());
       free_pages_.pop_back();
     }
-    check(hipMemcpy(p_tokens_, r.tokens.data(), S * sizeof(int), hipMemcpyHostToDevice));
-    check(hipMemcpy(d_table_, r.pages.data(), r.pages.size() * sizeof(int),
-                    hipMemcpyHostToDevice));
-    const int tok = infengine_detail::checked(
-        ie_prefill_paged(handle_, &weights_, S, p_tokens_, p_data_, p_aux_, p_attn_, p_logits_,
-                         p_out_, p_ws_, pool_, n_pages_, d_table_));
+    int tok = -1;
+    try {
+      ensure_prefill_buffers(S);
+      check(hipMemcpy(p_tokens_, r.tokens.data(), S * sizeof(int), hipMemcpyHostToDevice));
+      check(hipMemcpy(d_table_, r.pages.data(), r.pages.size() * sizeof(int),
+                      hipMemcpyHostToDevice));
+      tok = infengine_detail::checked(
+          ie_prefill_paged(handle_, &weights_, S, p_tokens_, p_data_, p_aux_, p_attn_, p_logits_,
+                           p_out_, p_ws_, pool_, n_pages_, d_table_));
+    } catch (...) {
+      // the request goes back to the head of the queue and its pages back to the pool
+      for (auto it = r.pages.rbegin(); it != r.pages.rend(); ++it) free_pages_.push_back(*it);
+      r.pages.clear();
+      waiting_.push_front(id);
+      throw;
+    }
     r.tokens.push_back(tok);
     if (finished_now(r)) retire(r);
     else running_.push_back(id);

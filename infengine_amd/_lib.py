@@ -72,7 +72,7 @@ SIGNATURES: dict[str, tuple] = {
     "ie_kv_cache_size": (_sz, []),
     "ie_prefill": (_i, [_p, _W, _i, _p, _p, _p, _p, _p, _p, _p, _p]),
     "ie_decode_step": (_i, [_p, _W, _i, _p, _p, _p, _p, _p, _p, _p, _p]),
-    "ie_generate": (_i, [_p, _W, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
+    "ie_generate": (_i, [_p, _W, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "ie_batch_workspace_size": (_sz, [_i]),
     "ie_decode_step_batched": (_i, [_p, _W, _i, C.POINTER(_i), _p, _p, _p, _p, _p,
                                     C.POINTER(_i), _p, _p]),

@@ -40,7 +40,7 @@ struct DecodeWs {
   uint16_t* attn1;  // [batch][4096]   attention output (op-level decode_attn only)
   float* part_o;
   float* part_ml;
-  uint16_t* xn;     // [batch][4096]   rows times the next norm weight (batched path)
+  uint16_t* xn;     // [batch][4096]   final-RMSNorm rows for the lm_head (batched path)
   float* ss;        // [256][16]       partial sums of squares of those rows (batched path)
 };
 
@@ -491,46 +491,51 @@ int ie_decode_step(ie_context* c, const ie_model_weights* weights, int seq_len,
 // Manager::handle_request's generation loop (manager.cpp:60-86) without the tokenizer: the
 // prompt ids go to the device, one prefill, then decode steps, each token written back to
 // tokenid_buff on the device before the next step reads it.  out_tokens[0] is the prefill's
-// token, out_tokens[i] the i-th decode step's.  timed_ms (optional) receives the host wall time
-// of decode steps timed_from .. max_new_tokens-1 (after a stream synchronisation).
+// token, out_tokens[i] the i-th decode step's.  The loop ends after max_new_tokens tokens or
+// right after a token equal to eos_token (>= 0; negative: no EOS), which is kept in out_tokens.
+// timed_ms (optional) receives the host wall time of decode steps timed_from .. the last one
+// (after a stream synchronisation; 0 when none ran).  Returns the number of tokens produced.
 int ie_generate(ie_context* c, const ie_model_weights* weights, const int* prompt, int prompt_len,
-                int max_new_tokens, int timed_from, int* out_tokens, int* tokenid_buff,
-                ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
-                float* output_distr, int* output_token, void* workspace, void* kv_cache,
-                double* timed_ms) {
+                int max_new_tokens, int eos_token, int timed_from, int* out_tokens,
+                int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                ie_bf16* attn_buffer, float* output_distr, int* output_token, void* workspace,
+                void* kv_cache, double* timed_ms) {
   CTX_OK(c);
   IE_REQUIRE(prompt && out_tokens, "generate: null prompt / output");
   IE_REQUIRE(prompt_len >= 1 && max_new_tokens >= 1 && prompt_len + max_new_tokens <= kMaxCtx,
              "generate: prompt %d + %d new tokens exceed the context %d", prompt_len,
              max_new_tokens, kMaxCtx);
+  if (timed_ms) *timed_ms = 0.0;
   IE_CHECK_HIP(hipMemcpyAsync(tokenid_buff, prompt, prompt_len * sizeof(int),
                               hipMemcpyHostToDevice, c->stream));
   const int first = ie_prefill(c, weights, prompt_len, tokenid_buff, data_buffer, aux_buffer,
                                attn_buffer, output_distr, output_token, workspace, kv_cache);
   if (first < 0) return first;
   out_tokens[0] = first;
+  if (first == eos_token) return 1;
   IE_CHECK_HIP(hipMemcpyAsync(tokenid_buff + prompt_len, output_token, sizeof(int),
                               hipMemcpyDeviceToDevice, c->stream));
   auto t0 = std::chrono::steady_clock::now();
-  for (int i = 1; i < max_new_tokens; ++i) {
-    if (i == timed_from) {
+  bool timing = false;
+  int n = 1;
+  while (n < max_new_tokens) {
+    if (n == timed_from) {
       IE_CHECK_HIP(hipStreamSynchronize(c->stream));
       t0 = std::chrono::steady_clock::now();
+      timing = true;
     }
-    const int tok = decode_step_impl(c, weights, prompt_len + i, tokenid_buff, data_buffer,
+    const int tok = decode_step_impl(c, weights, prompt_len + n, tokenid_buff, data_buffer,
                                      attn_buffer, output_distr, output_token, workspace, kv_cache,
                                      true, true);
     if (tok < 0) return tok;
-    out_tokens[i] = tok;
+    out_tokens[n++] = tok;
+    if (tok == eos_token) break;
   }
   IE_CHECK_HIP(hipStreamSynchronize(c->stream));
-  if (timed_ms) {
-    const auto t1 = std::chrono::steady_clock::now();
-    *timed_ms = timed_from < max_new_tokens
-                    ? std::chrono::duration<double, std::milli>(t1 - t0).count()
-                    : 0.0;
-  }
-  return max_new_tokens;
+  if (timed_ms && timing)
+    *timed_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
+                    .count();
+  return n;
 }
 
 // ---------------------------------------------------------------- prefill
@@ -681,17 +686,17 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
   const DecodeWs w = decode_ws(workspace, batch);
   const long long cstride = (long long)kLayers * kKVLayer;
   IE_TRY(launch_emblookup(batch, tokenid_buffs, W.emb_lookup, data_buffer, d_sl, kMaxCtx, st));
-  // RMSNorm folded into the projections: each norm's input rows arrive as bf16(x * norm weight)
-  // with partial sums of squares (layer 0: from this prep kernel, 4 per row; later:
-  // from the residual epilogue of the O / down projection, kNormParts partials per row), and the
-  // projection scales its accumulators by rsqrt(mean + eps)
-  IE_TRY(launch_rmsnorm_prep(batch, data_buffer, W.layers[0].input_layernorm, w.xn, w.ss, st));
+  // RMSNorm inside the projections: the QKV and gate/up projections read the residual rows
+  // with partial sums of squares of them (layer 0: from this prep kernel, 4 per row; later:
+  // from the residual epilogue of the O / down projection, kNormParts partials per row) and
+  // normalise the rows on their way in, with rmsnorm.cu:61's two roundings
+  IE_TRY(launch_rmsnorm_prep(batch, data_buffer, w.ss, st));
   for (int l = 0; l < kLayers; ++l) {
     const ie_layer& L = W.layers[l];
     uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_caches) + (size_t)l * kPageLayer
                                 : kv_layer(kv_caches, l);
     GemmParams g{};
-    g.x = w.xn;
+    g.x = data_buffer;
     g.w0 = L.transformer.w_q;
     g.w1 = L.transformer.w_k;
     g.w2 = L.transformer.w_v;
@@ -713,6 +718,7 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
     g.d_seq_len = d_sl;
     g.ss_in = w.ss;
     g.ss_parts = l == 0 ? 4 : kNormParts;
+    g.x_norm_w = L.input_layernorm;
     IE_TRY(launch_gemm(kGemmQkvRope, g, st));
     IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, max_len, batch, cstride, true, st,
                        block_table, table_stride, n_pages, true));
@@ -725,12 +731,10 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
     o.N = kHidden;
     o.K = kHidden;
     o.ldy = kHidden;
-    o.xw_out = w.xn;
-    o.xw_norm = L.post_attention_layernorm;
     o.ss_out = w.ss;
     IE_TRY(launch_gemm(kGemmResid, o, st));
     GemmParams gu{};
-    gu.x = w.xn;
+    gu.x = data_buffer;
     gu.w0 = L.ffn_block.w_gate;
     gu.w1 = L.ffn_block.w_up;
     gu.y = w.h;
@@ -740,6 +744,7 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
     gu.ldy = kFFN;
     gu.ss_in = w.ss;
     gu.ss_parts = kNormParts;
+    gu.x_norm_w = L.post_attention_layernorm;
     IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
     GemmParams dn{};
     dn.x = w.h;
@@ -750,11 +755,11 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
     dn.N = kHidden;
     dn.K = kFFN;
     dn.ldy = kHidden;
-    dn.xw_out = w.xn;
-    dn.xw_norm = l + 1 < kLayers ? W.layers[l + 1].input_layernorm : W.final_norm;
-    dn.ss_out = w.ss;
+    if (l + 1 < kLayers) dn.ss_out = w.ss;
     IE_TRY(launch_gemm(kGemmResid, dn, st));
   }
+  // prefill.cu:41-43 / decode.cu:41: final RMSNorm of the rows, then the lm_head product
+  IE_TRY(launch_rmsnorm(batch, data_buffer, W.final_norm, w.xn, st));
   GemmParams lm{};
   lm.x = w.xn;
   lm.w0 = W.lm_head;
@@ -764,8 +769,6 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
   lm.N = kVocab;
   lm.K = kHidden;
   lm.ldy = kVocab;
-  lm.ss_in = w.ss;
-  lm.ss_parts = kNormParts;
   IE_TRY(launch_gemm(kGemmF32, lm, st));
   IE_TRY(launch_argmax_rows(batch, kVocab, output_distr, output_tokens, c->d_slots,
                             c->d_counters + kCntArgmax, st));

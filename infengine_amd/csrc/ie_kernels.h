@@ -81,10 +81,9 @@ size_t attn_decode_partials_bytes(int batch);
 // ------------------------------------------------------------ elementwise
 int launch_emblookup(int rows, const int* ids, const uint16_t* table, uint16_t* out,
                      const int* d_seq_len, int ids_stride, hipStream_t st);
-// For a skinny GEMM with the norm folded in: xw = bf16(x * w) and the sums of squares of rows
-// 0..15 as 4 partials per row (ss[m][4]: the row's sum, then zeros; rows >= `rows` all zero).
-int launch_rmsnorm_prep(int rows, const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ss,
-                        hipStream_t st);
+// For a skinny GEMM that normalises its X rows: the sums of squares of rows 0..15 as 4 partials
+// per row (ss[m][4]: the row's sum, then zeros; rows >= `rows` all zero).
+int launch_rmsnorm_prep(int rows, const uint16_t* x, float* ss, hipStream_t st);
 int launch_rmsnorm(int rows, const uint16_t* x, const uint16_t* w, uint16_t* out,
                    hipStream_t st);
 int launch_residual_add(size_t n, uint16_t* x, const uint16_t* d, hipStream_t st);
@@ -157,15 +156,15 @@ struct GemmParams {
   int table_stride;        // head-0 planes of page 0 (pages kPageElems apart); ids outside
   int n_pages;             // [0, n_pages) are not written
   const int* d_seq_len;    // [M]
-  // Skinny GEMM (M <= 16) only: RMSNorm folded into the projection.
-  // Consumer: x holds bf16(x_row * norm_w) and ss_in [16][ss_parts] partial sums of squares of the
-  // 16 rows (rows past M zero); the accumulators are scaled by rsqrt(sum / K + eps).
+  // Skinny GEMM (M <= 16) only: RMSNorm of the X rows inside the projection (rmsnorm.cu:49-61).
+  // Consumer (SwiGLU / QKV + RoPE): x holds the raw rows, x_norm_w the norm weight [K] and ss_in
+  // [16][ss_parts] partial sums of squares of the rows (rows past M zero); the product uses the
+  // rows as bf16(bf16(x * r) * w), r = rsqrt(sum / K + eps): the reference's two roundings.
   const float* ss_in;
   int ss_parts;
-  // Producer (kGemmResid): also writes xw_out = bf16(y_new * xw_norm) (stride ldy) and this
-  // workgroup's sums of squares of the 16 new rows to ss_out[row][blockIdx] (N / 16 per row).
-  uint16_t* xw_out;
-  const uint16_t* xw_norm;
+  const uint16_t* x_norm_w;
+  // Producer (kGemmResid): also writes this workgroup's sums of squares of the 16 new rows to
+  // ss_out[row][blockIdx] (N / 16 per row).
   float* ss_out;
   // Split K (bf16 / residual / SwiGLU epilogues, 16 < M <= kSplitMaxRows): scratch for
   // fp32 partial products [splits][M][N]; when set and the tiles would fill at most half the

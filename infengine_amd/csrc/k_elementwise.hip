@@ -251,28 +251,21 @@ int launch_emblookup(int rows, const int* ids, const uint16_t* table, uint16_t* 
 
 // One block per row of 16 (rows past `rows` write a zero sum).
 __global__ __launch_bounds__(256) void rmsnorm_prep_kernel(int rows, const uint16_t* x,
-                                                           const uint16_t* w, uint16_t* xw,
                                                            float* ss) {
   __shared__ float red[4];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float s = 0.f;
   if (row < rows) {
     const uint4* x4 = reinterpret_cast<const uint4*>(x + (size_t)row * kHidden);
-    const uint4* w4 = reinterpret_cast<const uint4*>(w);
-    uint4* o4 = reinterpret_cast<uint4*>(xw + (size_t)row * kHidden);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const uint4 v = x4[tid + k * 256], wv = w4[tid + k * 256];
+      const uint4 v = x4[tid + k * 256];
       const uint32_t e[4] = {v.x, v.y, v.z, v.w};
-      const uint32_t f[4] = {wv.x, wv.y, wv.z, wv.w};
-      uint32_t o[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         s = fmaf(bf_lo(e[q]), bf_lo(e[q]), s);
         s = fmaf(bf_hi(e[q]), bf_hi(e[q]), s);
-        o[q] = pack_bf2(bf_lo(e[q]) * bf_lo(f[q]), bf_hi(e[q]) * bf_hi(f[q]));
       }
-      o4[tid + k * 256] = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
   s = wave_sum(s);
@@ -281,10 +274,9 @@ __global__ __launch_bounds__(256) void rmsnorm_prep_kernel(int rows, const uint1
   if (tid < 4) ss[row * 4 + tid] = tid == 0 ? (red[0] + red[1]) + (red[2] + red[3]) : 0.f;
 }
 
-int launch_rmsnorm_prep(int rows, const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ss,
-                        hipStream_t st) {
+int launch_rmsnorm_prep(int rows, const uint16_t* x, float* ss, hipStream_t st) {
   IE_REQUIRE(rows >= 1 && rows <= 16, "rmsnorm_prep: rows %d out of [1, 16]", rows);
-  hipLaunchKernelGGL(rmsnorm_prep_kernel, dim3(16), dim3(256), 0, st, rows, x, w, xw, ss);
+  hipLaunchKernelGGL(rmsnorm_prep_kernel, dim3(16), dim3(256), 0, st, rows, x, ss);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }

@@ -82,6 +82,31 @@ __device__ __forceinline__ void sk_put(u32x4_t* t, const u32x4_t (&v)[4], int r,
   }
 }
 
+// rmsnorm.cu:61's two roundings on one packed pair of an X row: bf16(bf16(x * r) * w).
+__device__ __forceinline__ uint32_t norm2(uint32_t x, uint32_t w, float r) {
+  const uint32_t t = pack_bf2(bf_lo(x) * r, bf_hi(x) * r);
+  return pack_bf2(bf_lo(t) * bf_lo(w), bf_hi(t) * bf_hi(w));
+}
+
+// RMSNorm of the X operand inside the projection: rr[j] = 1/rms of the lane's row 4j + q, nw =
+// the norm weight's 8 values at the lane's chunk of the current step (refilled with the X rows).
+struct SkNorm {
+  const uint16_t* w;
+  float rr[4];
+  u32x4_t nw;
+};
+
+__device__ __forceinline__ u32x4_t sk_load_nw(const uint16_t* w, int ks, int r) {
+  return *reinterpret_cast<const u32x4_t*>(w + ks + 8 * r);
+}
+
+__device__ __forceinline__ void sk_norm_x(u32x4_t (&xv)[4], const SkNorm& nm) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[j][i] = norm2(xv[j][i], nm.nw[i], nm.rr[j]);
+}
+
 // One step: the X rows (tr[1]) and each W tile in turn (tr[0]; the second W tile overwrites the
 // first once its fragments are read -- one wave's LDS operations run in order) through the
 // wave's LDS tiles into the operand layout, 4 MFMA k-chunks per W tile (the MFMA's 32-k
@@ -89,13 +114,17 @@ __device__ __forceinline__ void sk_put(u32x4_t* t, const u32x4_t (&v)[4], int r,
 // row r and of X row r).  The X registers are refilled with step kx as soon as they are in LDS
 // (X is L2-resident: one step of lookahead hides it), the W registers with step kw once the last
 // W tile is in LDS.
-template <int NT>
+template <int NT, bool NORM>
 __device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const SkSrc& src, u32x4_t (&w)[NT][4],
                                         u32x4_t (&xv)[4], int r, int q, f32x4_t (&acc)[NT],
-                                        bool lx, int kx, bool lw, int kw) {
+                                        bool lx, int kx, bool lw, int kw, SkNorm& nm) {
   sk_put(tr[0], w[0], r, q);
+  if constexpr (NORM) sk_norm_x(xv, nm);
   sk_put(tr[1], xv, r, q);
-  if (lx) sk_load_x(src, kx, xv);
+  if (lx) {
+    sk_load_x(src, kx, xv);
+    if constexpr (NORM) nm.nw = sk_load_nw(nm.w, kx, r);
+  }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if (t > 0) sk_put(tr[0], w[t], r, q);
@@ -110,24 +139,29 @@ __device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const SkSrc& src, u3
 
 // Steps s and s+1 from the two W register buffers, each refilled with the step two ahead; X
 // one step ahead.
-template <int NT>
+template <int NT, bool NORM>
 __device__ __forceinline__ void sk_pair(u32x4_t (*tr)[256], const SkSrc& src, int kbase, int s,
                                         int steps, int r, int q, u32x4_t (&w0)[NT][4],
                                         u32x4_t (&w1)[NT][4], u32x4_t (&xv)[4],
-                                        f32x4_t (&acc)[NT]) {
+                                        f32x4_t (&acc)[NT], SkNorm& nm) {
   const int k1 = kbase + (s + 1) * kSkStep;
-  sk_step<NT>(tr, src, w0, xv, r, q, acc, s + 1 < steps, k1, s + 2 < steps, k1 + kSkStep);
+  sk_step<NT, NORM>(tr, src, w0, xv, r, q, acc, s + 1 < steps, k1, s + 2 < steps, k1 + kSkStep,
+                    nm);
   __builtin_amdgcn_sched_barrier(0);
-  sk_step<NT>(tr, src, w1, xv, r, q, acc, s + 2 < steps, k1 + kSkStep, s + 3 < steps,
-              k1 + 2 * kSkStep);
+  sk_step<NT, NORM>(tr, src, w1, xv, r, q, acc, s + 2 < steps, k1 + kSkStep, s + 3 < steps,
+                    k1 + 2 * kSkStep, nm);
   __builtin_amdgcn_sched_barrier(0);
 }
 
 // KC: K fixed at compile time (4096 or 14336; the step loop then unrolls fully), 0: at run time.
 // At most 128 VGPRs (fixed K) and 32 KiB of LDS: 4 workgroups per CU, so the 896 workgroups of
 // the gate/up projection are all resident at once (the same speed, measured, as 2 per CU).
-template <int EPI, int KC>
-__global__ __launch_bounds__(kSkSplit * 64) __attribute__((amdgpu_waves_per_eu(KC > 0 ? 4 : 1)))
+// NORM: the X rows are the raw rows of an RMSNorm input, normalised on their way into LDS.
+// The normalising SwiGLU instance gets the registers of 2 waves per SIMD (2 workgroups per CU;
+// at 4 its 128-register cap slowed it by a quarter).
+template <int EPI, int KC, bool NORM>
+__global__ __launch_bounds__(kSkSplit * 64) __attribute__((
+    amdgpu_waves_per_eu(KC > 0 ? (NORM && EPI == kGemmSwiglu ? 2 : 4) : 1)))
 void gemm_skinny_kernel(GemmParams p) {
   constexpr bool SW = EPI == kGemmSwiglu;
   constexpr int NT = SW ? 2 : 1;  // 16-row W tiles: the weight rows, or gate and up rows
@@ -196,14 +230,14 @@ void gemm_skinny_kernel(GemmParams p) {
   // is refilled with step s+2; the X rows of step s+1 are loaded during step s, ahead of the W
   // rows of step s+2 (loads return in issue order)
   u32x4_t w0[NT][4], w1[NT][4], xv[4];
-  // folded RMSNorm: the rows' sums of squares from the producer's partials, [16][ss_parts] (a
-  // multiple of 4).  Loaded before the first weight loads and summed after them: loads return in
-  // issue order, so waiting for these does not wait for the weights.
+  // RMSNorm of the X rows: the rows' sums of squares from the producer's partials, [16][ss_parts]
+  // (a multiple of 4).  Loaded before the first weight loads and summed after them: loads return
+  // in issue order, so waiting for these does not wait for the weights.
   __shared__ float ssr[16];
   float4 ssv[kSsLoads];
-  const bool norm = p.ss_in != nullptr;
+  SkNorm nm;
   const int ss_row = threadIdx.x >> 4, ss_lane = threadIdx.x & 15;
-  if (norm) {
+  if constexpr (NORM) {
 #pragma unroll
     for (int i = 0; i < kSsLoads; ++i) {
       const int b = 4 * (ss_lane + 16 * i);
@@ -214,26 +248,33 @@ void gemm_skinny_kernel(GemmParams p) {
   __builtin_amdgcn_sched_barrier(0);
   sk_load_w<NT>(src, kbase, w0);
   sk_load_x(src, kbase, xv);
+  if constexpr (NORM) {
+    nm.w = p.x_norm_w;
+    nm.nw = sk_load_nw(nm.w, kbase, r);
+  }
   if (steps > 1) sk_load_w<NT>(src, kbase + kSkStep, w1);
   __builtin_amdgcn_sched_barrier(0);
-  if (norm) {
+  if constexpr (NORM) {
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < kSsLoads; ++i) sum += (ssv[i].x + ssv[i].y) + (ssv[i].z + ssv[i].w);
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 16);
     if (ss_lane == 0) ssr[ss_row] = sum;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) nm.rr[j] = rsqrtf(ssr[4 * j + q] / (float)K + kRmsEps);
   }
   int s = 0;
   if constexpr (KC > 0) {
 #pragma unroll
     for (; s + 1 < KC / kSkSplit / kSkStep; s += 2)
-      sk_pair<NT>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc);
+      sk_pair<NT, NORM>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc, nm);
   } else {
     for (; s + 1 < steps; s += 2)
-      sk_pair<NT>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc);
+      sk_pair<NT, NORM>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc, nm);
   }
-  if (s < steps) sk_step<NT>(tr[wave], src, w0, xv, r, q, acc, false, 0, false, 0);
+  if (s < steps) sk_step<NT, NORM>(tr[wave], src, w0, xv, r, q, acc, false, 0, false, 0, nm);
   f32x4_t acc0 = acc[0], acc1 = acc[NT - 1];
 
   // sum the K quarters: waves 1..3 hand their tiles to wave 0 through their own W tile slots
@@ -249,15 +290,10 @@ void gemm_skinny_kernel(GemmParams p) {
   }
 
   const int m = r, n = n0 + 4 * q;
-  if (norm) {
-    const float inv = rsqrtf(ssr[m] / (float)K + kRmsEps);
-    acc0 *= inv;
-    if constexpr (SW) acc1 *= inv;
-  }
   if constexpr (EPI == kGemmResid) {
     if (p.ss_out) {
-      // the new residual rows, bf16(y * norm weight) for the next projection, and this
-      // workgroup's share of each row's sum of squares (lanes q = 0..3 hold 4 columns each)
+      // the new residual rows and this workgroup's share of each row's sum of squares (for the
+      // next projection's RMSNorm; lanes q = 0..3 hold 4 columns each)
       float v[4] = {0.f, 0.f, 0.f, 0.f};
       if (m < p.M && n < p.N) {
         uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n);
@@ -267,10 +303,6 @@ void gemm_skinny_kernel(GemmParams p) {
         v[2] = bf2f(f2bf(bf_lo(old.y) + bf2f(f2bf(acc0[2]))));
         v[3] = bf2f(f2bf(bf_hi(old.y) + bf2f(f2bf(acc0[3]))));
         *dst = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
-        const uint2 wv = *reinterpret_cast<const uint2*>(p.xw_norm + n);
-        *reinterpret_cast<uint2*>(p.xw_out + (size_t)m * p.ldy + n) =
-            make_uint2(pack_bf2(v[0] * bf_lo(wv.x), v[1] * bf_hi(wv.x)),
-                       pack_bf2(v[2] * bf_lo(wv.y), v[3] * bf_hi(wv.y)));
       }
       float sq = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], v[3] * v[3])));
       sq += __shfl_xor(sq, 16);
@@ -452,7 +484,9 @@ void gemm_skinny_mb_kernel(GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // sum the K quarters through each wave's own LDS tiles (its last reads precede these writes)
+  // sum the K quarters through each wave's own LDS tiles (its last reads precede these writes):
+  // NT * MB slots of 64 lanes, laid out flat over the wave's 1 + MB tiles
+  static_assert(NT * MB * 64 <= (1 + MB) * 256, "K-quarter partials overflow the wave's tiles");
   u32x4_t* red = &tr[wave][0][0];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -466,7 +500,7 @@ void gemm_skinny_mb_kernel(GemmParams p) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
-        acc[t][mb] += __builtin_bit_cast(f32x4_t, tr[w][0][(t * MB + mb) * 64 + lane]);
+        acc[t][mb] += __builtin_bit_cast(f32x4_t, (&tr[w][0][0])[(t * MB + mb) * 64 + lane]);
 
   const int n = n0 + 4 * q;
 #pragma unroll
@@ -512,25 +546,46 @@ int launch_mb_e(const GemmParams& p, hipStream_t st) {
   return launch_mb_k<EPI, 3>(p, st);
 }
 
-template <int EPI>
-int launch_s(const GemmParams& p, hipStream_t st) {
+template <int EPI, bool NORM>
+int launch_sn(const GemmParams& p, hipStream_t st) {
   const int blocks = (p.N + kSkRows - 1) / kSkRows;
   if constexpr (EPI == kGemmQkvRope) {
     IE_REQUIRE(p.K == kHidden && p.N == kQKVDim && p.n0 == kHidden && p.n1 == kKVDim && p.y &&
                    p.k_cache && p.v_cache && p.d_seq_len && p.rope_cos && p.rope_sin,
                "gemm_skinny: the QKV + RoPE epilogue is for the [q|k|v] projection");
-    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4096>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4096, NORM>), dim3(blocks), dim3(kSkSplit * 64), 0,
+                       st, p);
+    IE_CHECK_LAUNCH();
+    return IE_OK;
+  }
+  if constexpr (NORM) {
+    // RMSNorm runs over the hidden size only
+    IE_REQUIRE(p.K == kHidden, "gemm_skinny: RMSNorm of the X rows needs K = %d (K=%d)", kHidden,
+               p.K);
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4096, NORM>), dim3(blocks), dim3(kSkSplit * 64), 0,
+                       st, p);
     IE_CHECK_LAUNCH();
     return IE_OK;
   }
   if (p.K == 4096)
-    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4096>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4096, NORM>), dim3(blocks), dim3(kSkSplit * 64), 0,
+                       st, p);
   else if (p.K == 14336)
-    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 14336>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 14336, NORM>), dim3(blocks), dim3(kSkSplit * 64), 0,
+                       st, p);
   else
-    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 0>), dim3(blocks), dim3(kSkSplit * 64), 0, st, p);
+    hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 0, NORM>), dim3(blocks), dim3(kSkSplit * 64), 0, st,
+                       p);
   IE_CHECK_LAUNCH();
   return IE_OK;
+}
+
+template <int EPI>
+int launch_s(const GemmParams& p, hipStream_t st) {
+  if constexpr (EPI == kGemmSwiglu || EPI == kGemmQkvRope) {
+    if (p.ss_in) return launch_sn<EPI, true>(p, st);
+  }
+  return launch_sn<EPI, false>(p, st);
 }
 
 
@@ -562,11 +617,12 @@ int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {
   IE_REQUIRE(gemm_skinny_fits(p), "gemm_skinny: needs M <= %d and K %% %d == 0 (M=%d K=%d)",
              kSkRows, kSkSplit * kSkStep, p.M, p.K);
   IE_REQUIRE(!p.ss_in || (p.ss_parts >= 4 && p.ss_parts % 4 == 0 && p.ss_parts <= 64 * kSsLoads &&
-                          epi != kGemmResid),
-             "gemm_skinny: folded RMSNorm input needs 4..%d partial sums per row (a multiple of 4)",
+                          p.x_norm_w && (epi == kGemmSwiglu || epi == kGemmQkvRope)),
+             "gemm_skinny: RMSNorm of the X rows (SwiGLU / QKV projections) needs the norm weight "
+             "and 4..%d partial sums per row (a multiple of 4)",
              64 * kSsLoads);
-  IE_REQUIRE(!p.ss_out || (epi == kGemmResid && p.xw_out && p.xw_norm && p.N % 16 == 0),
-             "gemm_skinny: the norm-preparing output is a residual-epilogue option");
+  IE_REQUIRE(!p.ss_out || (epi == kGemmResid && p.N % 16 == 0),
+             "gemm_skinny: the sums-of-squares output is a residual-epilogue option");
   switch (epi) {
     case kGemmSwiglu: return launch_s<kGemmSwiglu>(p, st);
     case kGemmQkvRope: return launch_s<kGemmQkvRope>(p, st);

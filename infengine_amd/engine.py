@@ -159,22 +159,24 @@ class Request:
     def decode_step(self, seq_len: int) -> int:
         return check(lib.ie_decode_step(*self._args(seq_len)))
 
-    def generate(self, prompt, max_new_tokens: int, timed_from: int | None = None):
+    def generate(self, prompt, max_new_tokens: int, timed_from: int | None = None,
+                 eos_token: int = -1):
         """Manager::handle_request's loop (manager.cpp:60-86) without the tokenizer: prefill of
         `prompt` (host ints), then decode steps with the device-side token write-back, all in
-        the library.  Returns (tokens, timed_ms) where timed_ms is the wall time of decode
-        steps timed_from .. max_new_tokens-1 (None when timed_from is None)."""
+        the library, until max_new_tokens tokens or right after eos_token (>= 0).  Returns
+        (tokens, timed_ms) where timed_ms is the wall time of decode steps timed_from .. the
+        last one (None when timed_from is None)."""
         import numpy as np
         ids = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
         out = (C.c_int * max_new_tokens)()
         ms = C.c_double(0.0)
         tf = max_new_tokens if timed_from is None else timed_from
-        check(lib.ie_generate(self.ctx.handle, self.weights.ref(),
-                              ids.ctypes.data_as(C.c_void_p), len(ids), max_new_tokens, tf, out,
-                              ptr(self.tokens), ptr(self.data), ptr(self.aux), ptr(self.attn),
-                              ptr(self.logits), ptr(self.token), ptr(self.workspace),
-                              ptr(self.kv), C.byref(ms)))
-        return list(out), (ms.value if timed_from is not None else None)
+        n = check(lib.ie_generate(self.ctx.handle, self.weights.ref(),
+                                  ids.ctypes.data_as(C.c_void_p), len(ids), max_new_tokens,
+                                  eos_token, tf, out, ptr(self.tokens), ptr(self.data),
+                                  ptr(self.aux), ptr(self.attn), ptr(self.logits), ptr(self.token),
+                                  ptr(self.workspace), ptr(self.kv), C.byref(ms)))
+        return list(out)[:n], (ms.value if timed_from is not None else None)
 
     def kv_view(self) -> torch.Tensor:
         """[layers][2][8][8192][128] bf16 view of the cache."""

@@ -2,7 +2,10 @@
 // requests run (a) all admitted at once, (b) joining at different steps, (c) one at a time.
 // A request's tokens must not depend on which requests share its steps, so all three
 // schedules must produce the same tokens; every page must be back in the pool afterwards.
+// Then (d) the same requests with EOS ids stop right after them, and (e) a prefill that fails
+// leaves its request queued and no page lost.
 // Prints the tokens of schedule (a), then "OK" or the first mismatch; exit status 0 on OK.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <vector>
@@ -57,6 +60,49 @@ Result run(IEHandle h, const ModelWeights& w, int schedule) {
   return out;
 }
 
+// (d) every request stops right after a token chosen from its schedule-(a) output (the first
+// occurrence of that token): the tokens must be that prefix, and all pages back in the pool.
+bool run_eos(IEHandle h, const ModelWeights& w, const Result& a) {
+  ContinuousBatcher cb(h, w, kPages);
+  const int n = (int)a.size();
+  std::vector<int> ids;
+  std::vector<std::vector<int>> want;
+  for (int r = 0; r < n; ++r) {
+    const int eos = a[r][2 + r % 3];
+    const size_t first = std::find(a[r].begin(), a[r].end(), eos) - a[r].begin();
+    want.emplace_back(a[r].begin(), a[r].begin() + first + 1);
+    ids.push_back(cb.submit(prompt_of(r, kSpecs[r].prompt_len), kSpecs[r].new_tokens, eos));
+  }
+  cb.run();
+  bool ok = cb.free_pages() == kPages;
+  for (int r = 0; r < n; ++r) {
+    const auto& t = cb.tokens(ids[r]);
+    const std::vector<int> got(t.begin() + kSpecs[r].prompt_len, t.end());
+    ok = ok && cb.finished(ids[r]) && got == want[r];
+    std::printf("eos %d stop_after %zu\n", r, got.size());
+  }
+  return ok;
+}
+
+// (e) a prefill that fails (incomplete weights: rejected on the host before any GPU work)
+// throws out of step(), leaves the request queued and returns every page to the pool.
+bool run_failed_prefill(IEHandle h) {
+  const ModelWeights empty;
+  ContinuousBatcher cb(h, empty, kPages);
+  const int id = cb.submit(prompt_of(0, 100), 20);
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    bool threw = false;
+    try {
+      cb.step();
+    } catch (const std::exception&) {
+      threw = true;
+    }
+    if (!threw || cb.free_pages() != kPages || cb.finished(id)) return false;
+  }
+  std::printf("failed prefill: pages %d of %d free\n", cb.free_pages(), kPages);
+  return true;
+}
+
 }  // namespace
 
 int main() {
@@ -75,6 +121,14 @@ int main() {
         std::printf("MISMATCH request %zu\n", r);
         rc = 1;
       }
+    if (!run_eos(h, w, a)) {
+      std::printf("EOS MISMATCH\n");
+      rc = 1;
+    }
+    if (!run_failed_prefill(h)) {
+      std::printf("FAILED PREFILL LEAKED PAGES\n");
+      rc = 1;
+    }
     if (!rc) std::printf("OK\n");
     ie_destroy_handle(h);
     w.free();

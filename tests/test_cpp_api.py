@@ -33,15 +33,17 @@ def test_cpp_api_compiles_and_links(tmp_path, hip, name):
 def test_cpp_continuous_batcher(tmp_path, hip):
     """The continuous batcher over the paged KV cache: four requests admitted at once, joining at
     different steps, and one at a time produce the same tokens (the program checks and prints
-    OK), and every page returns to the pool."""
+    OK), and every page returns to the pool; with EOS ids each request stops right after its
+    EOS; a prefill that fails leaves its request queued and loses no page."""
     from gpu_util import say
     exe = build_manager(tmp_path, "batcher_main")
     say("C++ ContinuousBatcher: 4 requests, 3 schedules")
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert res.returncode == 0, res.stdout + res.stderr
     lines = res.stdout.splitlines()
-    assert lines[-1] == "OK"
-    assert [len(l.split()) - 2 for l in lines[:-1]] == [12, 10, 14, 16]
+    assert lines[-1] == "OK", res.stdout
+    assert [len(l.split()) - 2 for l in lines if l.startswith("tokens")] == [12, 10, 14, 16]
+    assert sum(l.startswith("eos") for l in lines) == 4
 
 
 @pytest.mark.gpu
@@ -68,3 +70,10 @@ def test_cpp_manager_matches_python_driver(tmp_path, hip):
     W.free()
     c.close()
     assert cpp_tokens == toks
+    # the same request with an EOS id: stops right after its first occurrence
+    eos = toks[4]
+    stop = toks.index(eos) + 1
+    res = subprocess.run([str(exe), "16", "8", "7", str(eos)], capture_output=True, text=True,
+                         timeout=300)
+    assert res.returncode == 0, res.stderr
+    assert [int(t) for t in res.stdout.splitlines()[0].split()[1:]] == toks[:stop]

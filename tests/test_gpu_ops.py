@@ -192,12 +192,13 @@ GEMM_EPI = {"bf16": 0, "resid": 1, "f32": 2, "swiglu": 3}
 
 
 @pytest.mark.parametrize("epi", list(GEMM_EPI))
-@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (40, 1000), (48, 4096), (100, 4096),
-                                 (300, 1000), (512, 4096), (2048, 6144), (2048, 4096), (2048, 14336)])
+@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (24, 1000), (32, 4096), (40, 1000),
+                                 (48, 4096), (100, 4096), (300, 1000), (512, 4096), (2048, 6144),
+                                 (2048, 4096), (2048, 14336)])
 def test_gemm_epilogues(hip, ctx, epi, m, n):
     """Every fused epilogue of the MFMA GEMM on each kernel the launcher picks: the skinny
-    streaming kernel (m <= 16, ragged n), its 2-4 row-block form (m = 40, 48: bf16 / resid /
-    SwiGLU), 128 x 128 tiles (m = 100, 300: f32 / SwiGLU; f32 at m = 40, 48), K split
+    streaming kernel (m <= 16, ragged n), its 2- and 3-row-block forms (m = 24, 32 and m = 40,
+    48: bf16 / resid / SwiGLU), 128 x 128 tiles (m = 100, 300: f32 / SwiGLU; f32 at m = 24..48), K split
     across workgroups with a reduction (bf16 / resid at m = 100, 300, 512), and the prefill sizes:
     192 x 256 tiles (bf16 / resid at n = 6144), 256 x 256 tiles (SwiGLU at n = 4096), 256 x 128
     tiles (the others at n = 4096 and 6144), and at n = 14336 a launch split by output columns
@@ -235,6 +236,33 @@ def test_gemm_epilogues(hip, ctx, epi, m, n):
     # the residual add cancels (y0 ~ -acc), so a 1-ulp product difference can be several ulps
     # of a small sum: admit 1e-3 of such elements (each still within 1e-2 of the scale)
     assert_bf16_close(got, want, ulps=4 if epi == "swiglu" else 2, what=f"gemm {epi}",
+                      outlier_frac=1e-3 if epi == "resid" else 0.0)
+
+
+@pytest.mark.parametrize("epi", ["bf16", "resid"])
+@pytest.mark.parametrize("m", [24, 40, 2048])
+def test_gemm_down_projection_shapes(hip, ctx, epi, m):
+    """The down projection (k 14336, n 4096) as prefill runs it: the 2- and 3-row-block streaming
+    kernel at 24 and 40 rows (K = 14336 instantiations) and the 2048-row MFMA tiles of config 4;
+    every row at 24 / 40, sampled rows at 2048, against the oracle."""
+    k, n = 14336, 4096
+    say(f"gemm_ex down {epi} m={m} k={k} n={n}")
+    x = orc.synthetic((m, k), 25, m, 0.0, 1.0)
+    w0 = orc.synthetic((n, k), 25, n + 1, 0.0, 0.02)
+    y0 = orc.synthetic((m, n), 25, n + 3, 0.0, 1.0)
+    out = dev(y0) if epi == "resid" else bf16_empty(m, n)
+    hip.check(hip.lib.ie_gemm_ex(ctx.handle, GEMM_EPI[epi], m, k, n, P(dev(x)), P(dev(w0)),
+                                 P(dev(w0)), P(out)))
+    sync()
+    rows = np.arange(m) if m <= 64 else np.random.default_rng(4).choice(m, 40, replace=False)
+    rows[:2] = [0, m - 1]
+    xs = np.ascontiguousarray(x[rows])
+    got = host(out)[rows]
+    want = orc.matmul(xs, w0)
+    if epi == "resid":
+        want = orc.residual_add(np.ascontiguousarray(y0[rows]), want)
+    assert_close(orc.bf16_to_f32(got), orc.bf16_to_f32(want), what=f"gemm down {epi} m={m}")
+    assert_bf16_close(got, want, ulps=2, what=f"gemm down {epi} m={m}",
                       outlier_frac=1e-3 if epi == "resid" else 0.0)
 
 

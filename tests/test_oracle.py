@@ -59,6 +59,18 @@ def test_synthetic_is_deterministic_and_normal_shaped():
     assert abs(n.mean() - 1.0) < 1e-3
 
 
+# ---------------------------------------------------------------- embedding gather
+def test_emblookup_is_a_row_gather():
+    """orc.emblookup == table[ids] (emblookup.cu:19-24), first and last rows included, ids
+    repeated and unsorted; a transposed or off-by-one gather fails."""
+    table = orc.synthetic((orc.VOCAB, orc.HIDDEN), 9, 1, 0.0, 0.02)
+    ids = np.array([0, orc.VOCAB - 1, 5, 5, 128000, 1, 77777, 0], np.int32)
+    got = orc.emblookup(ids, table)
+    assert got.shape == (ids.size, orc.HIDDEN)
+    assert np.array_equal(got, table[ids])
+    assert not np.array_equal(got[0], got[1])
+
+
 # ---------------------------------------------------------------- rope tables
 def test_rope_tables_match_hf_llama3():
     g = np.load(GOLD / "rope_llama3_hf.npz")
