@@ -265,7 +265,7 @@ def main() -> int:
                 seq = (C.c_int * B)(*lens)
                 if paged:
                     check(lib.ie_decode_step_batched_paged(
-                        ctx.handle, W.ref(), B, seq, ptr(toks), ptr(bdata), ptr(battn),
+                        ctx.handle, W.ref(), B, seq, ptr(toks), toks.shape[1], ptr(bdata), ptr(battn),
                         ptr(blogits), ptr(bout), th, ptr(bws), ptr(pool), B * nblk, ptr(table),
                         nblk))
                 else:

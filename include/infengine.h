@@ -32,6 +32,11 @@ extern "C" {
 
 /* config.h:5-27 (InfEngineConfig) */
 #define IE_MAX_CONTEXT_LENGTH 8192
+/* Positions the paged KV paths (ie_prefill_paged*, ie_decode_step_batched_paged) and the RoPE
+ * tables cover: Llama-3.1's 131072 (max_position_embeddings).  No reference counterpart: the
+ * reference's cache and tables stop at IE_MAX_CONTEXT_LENGTH (config.h:7, attn.cu:304-307,
+ * rope.cu:68-103), which the reference-layout entry points keep. */
+#define IE_MAX_LONG_CONTEXT 131072
 #define IE_VOCAB_SIZE 128256
 #define IE_NUM_LAYERS 32
 #define IE_HIDDEN_SIZE 4096
@@ -67,8 +72,8 @@ typedef struct ie_ffn_block_weights {
 } ie_ffn_block_weights;
 
 typedef struct ie_rope_weights {
-  float* cos; /* [8192, 64] fp32 */
-  float* sin; /* [8192, 64] fp32 */
+  float* cos; /* [131072, 64] fp32 (rows 0..8191: the reference's [8192, 64] table) */
+  float* sin; /* [131072, 64] fp32 */
 } ie_rope_weights;
 
 /* kernels/model_weights.cuh:11-19 */
@@ -160,25 +165,41 @@ IE_API int ie_decode_step_batched(ie_context* ctx, const ie_model_weights* weigh
  * bit-identical to ie_decode_step_batched on the same rows. */
 IE_API size_t ie_kv_page_size(void);
 /* ie_prefill writing the prompt's K/V rows into pages: block_table (device) is the
- * sequence's page per 64-position block, entries 0 .. (seq_len-1)/64 set.  Same
- * arguments and results as ie_prefill otherwise (bit-identical logits / token). */
+ * sequence's page per 64-position block, entries 0 .. (seq_len-1)/64 set.  Same arguments and
+ * results as ie_prefill otherwise (bit-identical logits / token); seq_len may reach
+ * IE_MAX_LONG_CONTEXT (buffers and workspace sized for seq_len rows). */
 IE_API int ie_prefill_paged(ie_context* ctx, const ie_model_weights* weights, int seq_len,
                             int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
                             ie_bf16* attn_buffer, float* output_distr, int* output_token,
                             void* workspace, void* kv_pages, int n_pages,
                             const int* block_table);
+/* Chunked prefill over pages (no reference counterpart): the n_tokens prompt tokens at
+ * positions start_pos .. start_pos + n_tokens - 1 (tokenid_buff indexed by position) attend to
+ * the K/V of positions 0 .. start_pos - 1 already in the sequence's pages and to each other
+ * causally; their K/V rows are written into the pages.  data/aux/attn buffers and the workspace
+ * are sized for n_tokens rows.  Returns the greedy token after the chunk's last position
+ * (logits in output_distr).  start_pos = 0 is ie_prefill_paged. */
+IE_API int ie_prefill_paged_chunk(ie_context* ctx, const ie_model_weights* weights, int start_pos,
+                                  int n_tokens, int* tokenid_buff, ie_bf16* data_buffer,
+                                  ie_bf16* aux_buffer, ie_bf16* attn_buffer, float* output_distr,
+                                  int* output_token, void* workspace, void* kv_pages, int n_pages,
+                                  const int* block_table);
 /* Positions [first_pos, first_pos + n_pos) of every layer of a reference-layout
  * KV cache (e.g. just written by ie_prefill) into the pages that block_table
  * (device, one sequence's row) maps them to; ids outside [0, n_pages) skipped.
  * Runs on the context's stream. */
 IE_API int ie_kv_cache_to_pages(ie_context* ctx, const void* kv_cache, int first_pos, int n_pos,
                                 void* kv_pages, int n_pages, const int* block_table);
+/* The batched step over pages.  tokenid_buffs is [batch][tokens_stride] (row b holds sequence
+ * b's ids by position; tokens_stride >= every seq_lens[b]); seq_lens[b] <= IE_MAX_LONG_CONTEXT
+ * and <= 64 * table_stride. */
 IE_API int ie_decode_step_batched_paged(ie_context* ctx, const ie_model_weights* weights,
                                         int batch, const int* seq_lens, int* tokenid_buffs,
-                                        ie_bf16* data_buffer, ie_bf16* attn_buffer,
-                                        float* output_distr, int* output_tokens, int* tokens_out,
-                                        void* workspace, void* kv_pages, int n_pages,
-                                        const int* block_tables, int table_stride);
+                                        int tokens_stride, ie_bf16* data_buffer,
+                                        ie_bf16* attn_buffer, float* output_distr,
+                                        int* output_tokens, int* tokens_out, void* workspace,
+                                        void* kv_pages, int n_pages, const int* block_tables,
+                                        int table_stride);
 
 /* ---- weights (model_weights.cu:142-172) ---- */
 /* Random-init Llama-3.1-8B: matrices ~N(0,std), norms ~1+N(0,0.02), rope tables. */
@@ -186,7 +207,8 @@ IE_API int ie_model_weights_random_init(ie_model_weights* out, uint64_t seed, fl
 IE_API int ie_model_weights_from_safetensors(ie_model_weights* out, const char* const* paths,
                                              int n_paths);
 IE_API int ie_model_weights_free(ie_model_weights* w);
-/* rope.cu:68-103: Llama-3 scaled RoPE tables, fp32 [8192, 64]; allocates. */
+/* rope.cu:68-103: Llama-3 scaled RoPE tables, fp32 [131072, 64] (the reference's [8192, 64]
+ * continued to IE_MAX_LONG_CONTEXT positions by the same formula); allocates. */
 IE_API int ie_init_rope_buffer(float** cu_rope_cos, float** cu_rope_sin);
 IE_API int ie_cleanup_rope_buffer(float* cu_rope_cos, float* cu_rope_sin);
 /* Deterministic synthetic tensor: out[i] = bf16(mean + std * z_i), z_i an
@@ -309,6 +331,12 @@ IE_API int ie_gemm_ex(ie_context* ctx, int epilogue, int m, int k, int n, const 
  * at position start_pos + i and sees keys 0..start_pos+i. */
 IE_API int ie_attn_prefill_core(ie_context* ctx, int seq_len, int start_pos, const ie_bf16* d_q,
                                 const ie_bf16* d_k, const ie_bf16* d_v, ie_bf16* d_out);
+/* The same attention core over a page pool (ie_kv_page_size() pages; block_table (device) maps
+ * 64-key block i to a page): the keys of page-layout layer `layer`, positions 0 ..
+ * start_pos + seq_len - 1 <= IE_MAX_LONG_CONTEXT - 1. */
+IE_API int ie_attn_prefill_core_paged(ie_context* ctx, int seq_len, int start_pos,
+                                      const ie_bf16* d_q, const void* kv_pages, int n_pages,
+                                      const int* block_table, int layer, ie_bf16* d_out);
 
 #ifdef __cplusplus
 }

@@ -2,8 +2,9 @@
 // The reference serves one request at a time (manager.cpp:31-110) and keeps a per-request
 // RequestContext it never uses (manager.h:19-24); this driver is the continuous form of that
 // loop.  Each admitted request is prefilled alone, straight into its pages
-// (ie_prefill_paged), then decoded together with every other running request, up to 16 per
-// ie_decode_step_batched_paged call.  Pages (64
+// (ie_prefill_paged_chunk, 8192 prompt tokens per call), then decoded together with every other
+// running request, up to 16 per ie_decode_step_batched_paged call; a request may span up to
+// IE_MAX_LONG_CONTEXT positions.  Pages (64
 // positions of all layers, 8 MiB) come from a fixed pool; a request reserves the pages its
 // whole lifetime needs when it is admitted, so a running request never waits for memory, and
 // returns them when it finishes (max_new_tokens or eos_token).  Every row of the batched step
@@ -24,7 +25,11 @@ class ContinuousBatcher {
  public:
   static constexpr int kMaxBatch = 16;
   static constexpr int kPagePos = 64;
-  static constexpr int kTableStride = InfEngineConfig::MAX_CONTEXT_LENGTH / kPagePos;
+  // a request may span the paged path's whole context; prompts are prefilled in chunks of the
+  // reference context length, so the prefill buffers stay that size
+  static constexpr int kMaxPositions = IE_MAX_LONG_CONTEXT;
+  static constexpr int kTableStride = kMaxPositions / kPagePos;
+  static constexpr int kPrefillChunk = InfEngineConfig::MAX_CONTEXT_LENGTH;
 
   // n_pages: size of the page pool (ie_kv_page_size() bytes each).
   ContinuousBatcher(IEHandle handle, const ModelWeights& weights, int n_pages)
@@ -32,7 +37,7 @@ class ContinuousBatcher {
     if (n_pages < 1) throw std::invalid_argument("ContinuousBatcher: n_pages < 1");
     check(hipMalloc(&pool_, (size_t)n_pages * ie_kv_page_size()));
     check(hipMalloc(&d_table_, sizeof(int) * kMaxBatch * kTableStride));
-    check(hipMalloc(&d_tokens_, sizeof(int) * kMaxBatch * InfEngineConfig::MAX_CONTEXT_LENGTH));
+    check(hipMalloc(&d_tokens_, sizeof(int) * kMaxBatch * kMaxPositions));
     check(hipMalloc(&d_data_, sizeof(bf16) * kMaxBatch * InfEngineConfig::HIDDEN_SIZE));
     check(hipMalloc(&d_attn_, sizeof(bf16) * kMaxBatch * InfEngineConfig::HIDDEN_SIZE));
     check(hipMalloc(&d_logits_, sizeof(float) * kMaxBatch * InfEngineConfig::VOCAB_SIZE));
@@ -53,8 +58,8 @@ class ContinuousBatcher {
   int submit(const std::vector<int>& prompt, int max_new_tokens, int eos_token = -1) {
     if (prompt.empty() || max_new_tokens < 1)
       throw std::invalid_argument("submit: empty prompt or max_new_tokens < 1");
-    if ((int)prompt.size() + max_new_tokens > InfEngineConfig::MAX_CONTEXT_LENGTH)
-      throw std::invalid_argument("submit: request exceeds the 8192-position KV cache");
+    if ((int)prompt.size() + max_new_tokens > kMaxPositions)
+      throw std::invalid_argument("submit: request exceeds the paged KV cache's positions");
     if (pages_for(prompt, max_new_tokens) > n_pages_)
       throw std::invalid_argument("submit: request needs more pages than the pool holds");
     reqs_.push_back(Req{prompt, (int)prompt.size(), max_new_tokens, eos_token, {}, false});
@@ -79,13 +84,14 @@ class ContinuousBatcher {
       const Req& r = reqs_[running_[b]];
       seq[b] = (int)r.tokens.size();  // the newest token sits at position seq - 1
       std::copy(r.pages.begin(), r.pages.end(), table.begin() + (size_t)b * kTableStride);
-      check(hipMemcpy(d_tokens_ + (size_t)b * InfEngineConfig::MAX_CONTEXT_LENGTH + seq[b] - 1,
+      check(hipMemcpy(d_tokens_ + (size_t)b * kMaxPositions + seq[b] - 1,
                       &r.tokens.back(), sizeof(int), hipMemcpyHostToDevice));
     }
     check(hipMemcpy(d_table_, table.data(), table.size() * sizeof(int), hipMemcpyHostToDevice));
     std::vector<int> out(B);
     infengine_detail::checked(ie_decode_step_batched_paged(
-        handle_, &weights_, B, seq.data(), d_tokens_, d_data_, d_attn_, d_logits_, d_out_,
+        handle_, &weights_, B, seq.data(), d_tokens_, kMaxPositions, d_data_, d_attn_, d_logits_,
+        d_out_,
         out.data(), d_ws_, pool_, n_pages_, d_table_, kTableStride));
     std::vector<int> still;
     for (int b = 0; b < B; ++b) {
@@ -132,8 +138,9 @@ class ContinuousBatcher {
     r.pages.clear();
   }
 
-  // Prefill alone, writing the prompt's K/V rows into the request's pages.  If it throws, the
-  // request is back at the head of the queue with no pages and the exception propagates.
+  // Prefill alone, writing the prompt's K/V rows into the request's pages, kPrefillChunk tokens
+  // per call.  If it throws, the request is back at the head of the queue with no pages and the
+  // exception propagates.
   void admit(int id) {
     Req& r = reqs_[id];
     const int S = r.prompt_len;
@@ -144,13 +151,14 @@ class ContinuousBatcher {
     }
     int tok = -1;
     try {
-      ensure_prefill_buffers(S);
+      ensure_prefill_buffers(std::min(S, kPrefillChunk));
       check(hipMemcpy(p_tokens_, r.tokens.data(), S * sizeof(int), hipMemcpyHostToDevice));
       check(hipMemcpy(d_table_, r.pages.data(), r.pages.size() * sizeof(int),
                       hipMemcpyHostToDevice));
-      tok = infengine_detail::checked(
-          ie_prefill_paged(handle_, &weights_, S, p_tokens_, p_data_, p_aux_, p_attn_, p_logits_,
-                           p_out_, p_ws_, pool_, n_pages_, d_table_));
+      for (int start = 0; start < S; start += kPrefillChunk)
+        tok = infengine_detail::checked(ie_prefill_paged_chunk(
+            handle_, &weights_, start, std::min(kPrefillChunk, S - start), p_tokens_, p_data_,
+            p_aux_, p_attn_, p_logits_, p_out_, p_ws_, pool_, n_pages_, d_table_));
     } catch (...) {
       // the request goes back to the head of the queue and its pages back to the pool
       for (auto it = r.pages.rbegin(); it != r.pages.rend(); ++it) free_pages_.push_back(*it);
@@ -163,13 +171,13 @@ class ContinuousBatcher {
     else running_.push_back(id);
   }
 
-  void ensure_prefill_buffers(int S) {
-    const size_t ws = std::max(attn_workspace_size(S), ffn_workspace_size(S));
+  // buffers for prefill calls of up to `rows` tokens
+  void ensure_prefill_buffers(int rows) {
+    const size_t ws = std::max(attn_workspace_size(rows), ffn_workspace_size(rows));
     if (p_ws_ && ws <= p_ws_bytes_) return;
     if (!p_tokens_) {
-      const size_t act = (size_t)InfEngineConfig::MAX_CONTEXT_LENGTH *
-                         InfEngineConfig::HIDDEN_SIZE * sizeof(bf16);
-      check(hipMalloc(&p_tokens_, InfEngineConfig::MAX_CONTEXT_LENGTH * sizeof(int)));
+      const size_t act = (size_t)kPrefillChunk * InfEngineConfig::HIDDEN_SIZE * sizeof(bf16);
+      check(hipMalloc(&p_tokens_, kMaxPositions * sizeof(int)));
       check(hipMalloc(&p_data_, act));
       check(hipMalloc(&p_aux_, act));
       check(hipMalloc(&p_attn_, act));

@@ -12,6 +12,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "libinfengine_amd.so"
 
 # include/infengine.h constants (config.h:5-27)
 MAX_CONTEXT_LENGTH = 8192
+MAX_LONG_CONTEXT = 131072
 VOCAB_SIZE = 128256
 NUM_LAYERS = 32
 HIDDEN_SIZE = 4096
@@ -78,8 +79,9 @@ SIGNATURES: dict[str, tuple] = {
                                     C.POINTER(_i), _p, _p]),
     "ie_kv_page_size": (_sz, []),
     "ie_prefill_paged": (_i, [_p, _W, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "ie_prefill_paged_chunk": (_i, [_p, _W, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
     "ie_kv_cache_to_pages": (_i, [_p, _p, _i, _i, _p, _i, _p]),
-    "ie_decode_step_batched_paged": (_i, [_p, _W, _i, C.POINTER(_i), _p, _p, _p, _p, _p,
+    "ie_decode_step_batched_paged": (_i, [_p, _W, _i, C.POINTER(_i), _p, _i, _p, _p, _p, _p,
                                           C.POINTER(_i), _p, _p, _i, _p, _i]),
     "ie_model_weights_random_init": (_i, [_W, _u64, _f]),
     "ie_model_weights_from_safetensors": (_i, [_W, C.POINTER(C.c_char_p), _i]),
@@ -110,6 +112,7 @@ SIGNATURES: dict[str, tuple] = {
     "ie_gemm_bf16": (_i, [_p, _i, _i, _i, _p, _p, _p]),
     "ie_gemm_ex": (_i, [_p, _i, _i, _i, _i, _p, _p, _p, _p]),
     "ie_attn_prefill_core": (_i, [_p, _i, _i, _p, _p, _p, _p]),
+    "ie_attn_prefill_core_paged": (_i, [_p, _i, _i, _p, _p, _i, _p, _i, _p]),
     "ie_tune_gemv_waves": (_i, [_i]),
     "ie_tune_gemv_pairs_per_wave": (_i, [_i]),
 }

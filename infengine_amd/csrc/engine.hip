@@ -258,9 +258,10 @@ void rope_tables_host(std::vector<float>& cos_t, std::vector<float>& sin_t) {
       freqs[i] = (1 - smooth) * (freq / factor) + smooth * freq;
     }
   }
-  cos_t.resize((size_t)kMaxCtx * 64);
-  sin_t.resize((size_t)kMaxCtx * 64);
-  for (int pos = 0; pos < kMaxCtx; ++pos)
+  // rows 0..8191 are the reference's table; the same formula continues to kMaxLongCtx
+  cos_t.resize((size_t)kMaxLongCtx * 64);
+  sin_t.resize((size_t)kMaxLongCtx * 64);
+  for (int pos = 0; pos < kMaxLongCtx; ++pos)
     for (int i = 0; i < 64; ++i) {
       const float angle = pos * freqs[i];
       cos_t[(size_t)pos * 64 + i] = std::cos(angle);
@@ -541,14 +542,19 @@ int ie_generate(ie_context* c, const ie_model_weights* weights, const int* promp
 // ---------------------------------------------------------------- prefill
 namespace {
 // The prefill body over a reference-layout cache (block_table null) or over a page pool
-// (kv_cache = n_pages pages, block_table the sequence's page per 64-position block).
-int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, int* tokenid_buff,
-                 ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
-                 float* output_distr, int* output_token, void* workspace, void* kv_cache,
-                 const int* block_table, int n_pages) {
+// (kv_cache = n_pages pages, block_table the sequence's page per 64-position block).  The
+// seq_len tokens sit at positions start_pos .. (tokenid_buff indexed by position); with pages,
+// the K/V of positions before start_pos are already there (chunked prefill).
+int prefill_impl(ie_context* c, const ie_model_weights* weights, int start_pos, int seq_len,
+                 int* tokenid_buff, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                 ie_bf16* attn_buffer, float* output_distr, int* output_token, void* workspace,
+                 void* kv_cache, const int* block_table, int n_pages) {
   IE_REQUIRE(weights && weights_complete(*weights), "prefill: incomplete weights");
-  IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "prefill: seq_len %d out of [1, %d]", seq_len,
-             kMaxCtx);
+  const int cap = block_table ? kMaxLongCtx : kMaxCtx;
+  IE_REQUIRE(start_pos >= 0 && (start_pos == 0 || block_table),
+             "prefill: start_pos %d needs the paged cache", start_pos);
+  IE_REQUIRE(seq_len >= 1 && start_pos + seq_len <= cap,
+             "prefill: positions [%d, %d) out of [0, %d]", start_pos, start_pos + seq_len, cap);
   IE_REQUIRE(tokenid_buff && data_buffer && aux_buffer && attn_buffer && output_distr &&
                  output_token && workspace && kv_cache,
              "prefill: null buffer");
@@ -560,7 +566,7 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, in
   uint16_t* qrot = reinterpret_cast<uint16_t*>(wsb + align256((size_t)S * kQKVDim * 2));
   uint16_t* h = reinterpret_cast<uint16_t*>(wsb);
 
-  IE_TRY(launch_emblookup(S, tokenid_buff, W.emb_lookup, data_buffer, nullptr, 0, st));
+  IE_TRY(launch_emblookup(S, tokenid_buff + start_pos, W.emb_lookup, data_buffer, nullptr, 0, st));
   for (int l = 0; l < kLayers; ++l) {
     const ie_layer& L = W.layers[l];
     uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_cache) + (size_t)l * kPageLayer
@@ -583,9 +589,9 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int seq_len, in
     g.split_ws = reinterpret_cast<float*>(wsb + prefill_attn_bytes(S));
     g.split_ws_bytes = (long long)(ie_attn_workspace_size(S) - prefill_attn_bytes(S));
     IE_TRY(launch_gemm(kGemmBf16, g, st));
-    IE_TRY(launch_qkv_rope_scatter(S, 0, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl, nullptr, 0,
-                                   st, block_table, n_pages));
-    AttnPrefillParams a{qrot, kvl, vpl, attn_buffer, S, 0, block_table, n_pages};
+    IE_TRY(launch_qkv_rope_scatter(S, start_pos, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl,
+                                   nullptr, 0, st, block_table, n_pages));
+    AttnPrefillParams a{qrot, kvl, vpl, attn_buffer, S, start_pos, block_table, n_pages};
     IE_TRY(launch_attn_prefill(a, st));
     GemmParams o{};
     o.x = attn_buffer;
@@ -642,7 +648,7 @@ int ie_prefill(ie_context* c, const ie_model_weights* weights, int seq_len, int*
                ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
                float* output_distr, int* output_token, void* workspace, void* kv_cache) {
   CTX_OK(c);
-  return prefill_impl(c, weights, seq_len, tokenid_buff, data_buffer, aux_buffer, attn_buffer,
+  return prefill_impl(c, weights, 0, seq_len, tokenid_buff, data_buffer, aux_buffer, attn_buffer,
                       output_distr, output_token, workspace, kv_cache, nullptr, 0);
 }
 
@@ -652,8 +658,21 @@ int ie_prefill_paged(ie_context* c, const ie_model_weights* weights, int seq_len
                      void* workspace, void* kv_pages, int n_pages, const int* block_table) {
   CTX_OK(c);
   IE_REQUIRE(kv_pages && block_table && n_pages >= 1, "prefill_paged: needs a page pool and a block table");
-  return prefill_impl(c, weights, seq_len, tokenid_buff, data_buffer, aux_buffer, attn_buffer,
+  return prefill_impl(c, weights, 0, seq_len, tokenid_buff, data_buffer, aux_buffer, attn_buffer,
                       output_distr, output_token, workspace, kv_pages, block_table, n_pages);
+}
+
+int ie_prefill_paged_chunk(ie_context* c, const ie_model_weights* weights, int start_pos,
+                           int n_tokens, int* tokenid_buff, ie_bf16* data_buffer,
+                           ie_bf16* aux_buffer, ie_bf16* attn_buffer, float* output_distr,
+                           int* output_token, void* workspace, void* kv_pages, int n_pages,
+                           const int* block_table) {
+  CTX_OK(c);
+  IE_REQUIRE(kv_pages && block_table && n_pages >= 1,
+             "prefill_paged_chunk: needs a page pool and a block table");
+  return prefill_impl(c, weights, start_pos, n_tokens, tokenid_buff, data_buffer, aux_buffer,
+                      attn_buffer, output_distr, output_token, workspace, kv_pages, block_table,
+                      n_pages);
 }
 
 // ---------------------------------------------------------------- batched decode
@@ -662,17 +681,20 @@ namespace {
 // reference layout, kv_cache_size() apart) or over a page pool (kv = n_pages pages,
 // block_table [batch][table_stride] page ids).
 int batched_step(ie_context* c, const ie_model_weights* weights, int batch, const int* seq_lens,
-                 int* tokenid_buffs, ie_bf16* data_buffer, ie_bf16* attn_buffer,
-                 float* output_distr, int* output_tokens, int* tokens_out, void* workspace,
-                 void* kv_caches, const int* block_table, int table_stride, int n_pages) {
+                 int* tokenid_buffs, int tokens_stride, ie_bf16* data_buffer,
+                 ie_bf16* attn_buffer, float* output_distr, int* output_tokens, int* tokens_out,
+                 void* workspace, void* kv_caches, const int* block_table, int table_stride,
+                 int n_pages) {
   IE_REQUIRE(weights && weights_complete(*weights), "decode_step_batched: incomplete weights");
   IE_REQUIRE(batch >= 1 && batch <= 16, "decode_step_batched: batch %d out of [1, 16]", batch);
   IE_REQUIRE(seq_lens && tokenid_buffs && data_buffer && attn_buffer && output_distr &&
                  output_tokens && workspace && kv_caches,
              "decode_step_batched: null buffer");
+  const int cap = block_table ? kMaxLongCtx : kMaxCtx;
   for (int b = 0; b < batch; ++b)
-    IE_REQUIRE(seq_lens[b] >= 1 && seq_lens[b] <= kMaxCtx,
-               "decode_step_batched: seq_lens[%d]=%d out of [1, %d]", b, seq_lens[b], kMaxCtx);
+    IE_REQUIRE(seq_lens[b] >= 1 && seq_lens[b] <= cap && seq_lens[b] <= tokens_stride,
+               "decode_step_batched: seq_lens[%d]=%d out of [1, %d] (token rows of %d)", b,
+               seq_lens[b], cap, tokens_stride);
   const ie_model_weights& W = *weights;
   hipStream_t st = c->stream;
   int max_len = 1;
@@ -685,7 +707,8 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
   const int* d_sl = c->d_params + 1;
   const DecodeWs w = decode_ws(workspace, batch);
   const long long cstride = (long long)kLayers * kKVLayer;
-  IE_TRY(launch_emblookup(batch, tokenid_buffs, W.emb_lookup, data_buffer, d_sl, kMaxCtx, st));
+  IE_TRY(launch_emblookup(batch, tokenid_buffs, W.emb_lookup, data_buffer, d_sl, tokens_stride,
+                          st));
   // RMSNorm inside the projections: the QKV and gate/up projections read the residual rows
   // with partial sums of squares of them (layer 0: from this prep kernel, 4 per row; later:
   // from the residual epilogue of the O / down projection, kNormParts partials per row) and
@@ -789,9 +812,9 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
                            ie_bf16* attn_buffer, float* output_distr, int* output_tokens,
                            int* tokens_out, void* workspace, void* kv_caches) {
   CTX_OK(c);
-  return batched_step(c, weights, batch, seq_lens, tokenid_buffs, data_buffer, attn_buffer,
-                      output_distr, output_tokens, tokens_out, workspace, kv_caches, nullptr, 0,
-                      0);
+  return batched_step(c, weights, batch, seq_lens, tokenid_buffs, kMaxCtx, data_buffer,
+                      attn_buffer, output_distr, output_tokens, tokens_out, workspace, kv_caches,
+                      nullptr, 0, 0);
 }
 
 size_t ie_kv_page_size(void) { return kPageElems * sizeof(uint16_t); }
@@ -805,23 +828,25 @@ int ie_kv_cache_to_pages(ie_context* c, const void* kv_cache, int first_pos, int
 }
 
 int ie_decode_step_batched_paged(ie_context* c, const ie_model_weights* weights, int batch,
-                                 const int* seq_lens, int* tokenid_buffs, ie_bf16* data_buffer,
-                                 ie_bf16* attn_buffer, float* output_distr, int* output_tokens,
-                                 int* tokens_out, void* workspace, void* kv_pages, int n_pages,
-                                 const int* block_tables, int table_stride) {
+                                 const int* seq_lens, int* tokenid_buffs, int tokens_stride,
+                                 ie_bf16* data_buffer, ie_bf16* attn_buffer, float* output_distr,
+                                 int* output_tokens, int* tokens_out, void* workspace,
+                                 void* kv_pages, int n_pages, const int* block_tables,
+                                 int table_stride) {
   CTX_OK(c);
   IE_REQUIRE(kv_pages && block_tables && n_pages >= 1,
              "decode_step_batched_paged: needs a page pool and block tables");
-  IE_REQUIRE(table_stride >= 1 && table_stride <= kMaxCtx / kPagePos,
+  IE_REQUIRE(table_stride >= 1 && table_stride <= kMaxLongCtx / kPagePos,
              "decode_step_batched_paged: table_stride %d out of [1, %d]", table_stride,
-             kMaxCtx / kPagePos);
+             kMaxLongCtx / kPagePos);
+  IE_REQUIRE(tokens_stride >= 1, "decode_step_batched_paged: tokens_stride %d", tokens_stride);
   for (int b = 0; seq_lens && b < batch && b < 16; ++b)
     IE_REQUIRE(seq_lens[b] <= table_stride * kPagePos,
                "decode_step_batched_paged: seq_lens[%d]=%d needs more than %d table entries", b,
                seq_lens[b], table_stride);
-  return batched_step(c, weights, batch, seq_lens, tokenid_buffs, data_buffer, attn_buffer,
-                      output_distr, output_tokens, tokens_out, workspace, kv_pages, block_tables,
-                      table_stride, n_pages);
+  return batched_step(c, weights, batch, seq_lens, tokenid_buffs, tokens_stride, data_buffer,
+                      attn_buffer, output_distr, output_tokens, tokens_out, workspace, kv_pages,
+                      block_tables, table_stride, n_pages);
 }
 
 // ---------------------------------------------------------------- weights
@@ -879,7 +904,8 @@ size_t weights_arena_bytes() {
   size_t total = align256(emb * 2);
   for (int l = 0; l < kLayers; ++l)
     for (int f = 0; f < kLayerFields; ++f) total += align256(layer_field_elems(f) * 2);
-  return total + align256(kHidden * 2) + align256(emb * 2) + 2 * align256((size_t)kMaxCtx * 64 * 4);
+  return total + align256(kHidden * 2) + align256(emb * 2) +
+         2 * align256((size_t)kMaxLongCtx * 64 * 4);
 }
 
 void weights_arena_assign(ie_model_weights* w, void* arena) {
@@ -897,8 +923,8 @@ void weights_arena_assign(ie_model_weights* w, void* arena) {
       *layer_field(w->layers[l], f) = static_cast<ie_bf16*>(take(layer_field_elems(f) * 2));
   w->final_norm = static_cast<ie_bf16*>(take(kHidden * 2));
   w->lm_head = static_cast<ie_bf16*>(take(emb * 2));
-  w->rope.cos = static_cast<float*>(take((size_t)kMaxCtx * 64 * 4));
-  w->rope.sin = static_cast<float*>(take((size_t)kMaxCtx * 64 * 4));
+  w->rope.cos = static_cast<float*>(take((size_t)kMaxLongCtx * 64 * 4));
+  w->rope.sin = static_cast<float*>(take((size_t)kMaxLongCtx * 64 * 4));
 }
 
 int weights_upload_rope(ie_model_weights* w) {
@@ -1030,6 +1056,19 @@ int ie_attn_prefill_core(ie_context* c, int seq_len, int start_pos, const ie_bf1
   CTX_OK(c);
   IE_REQUIRE(d_q && d_k && d_v && d_out, "attn_prefill_core: null pointer");
   AttnPrefillParams a{d_q, d_k, d_v, d_out, seq_len, start_pos};
+  return launch_attn_prefill(a, c->stream);
+}
+
+int ie_attn_prefill_core_paged(ie_context* c, int seq_len, int start_pos, const ie_bf16* d_q,
+                               const void* kv_pages, int n_pages, const int* block_table,
+                               int layer, ie_bf16* d_out) {
+  CTX_OK(c);
+  IE_REQUIRE(d_q && kv_pages && block_table && d_out, "attn_prefill_core_paged: null pointer");
+  IE_REQUIRE(n_pages >= 1 && layer >= 0 && layer < kLayers,
+             "attn_prefill_core_paged: n_pages %d, layer %d", n_pages, layer);
+  const uint16_t* kl = static_cast<const uint16_t*>(kv_pages) + (size_t)layer * kPageLayer;
+  AttnPrefillParams a{d_q, kl, kl + (size_t)kKVHeads * kPageHead, d_out, seq_len, start_pos,
+                      block_table, n_pages};
   return launch_attn_prefill(a, c->stream);
 }
 

@@ -11,7 +11,8 @@
 
 namespace ie {
 
-constexpr int kMaxCtx = IE_MAX_CONTEXT_LENGTH;
+constexpr int kMaxCtx = IE_MAX_CONTEXT_LENGTH;       // reference-layout KV cache positions
+constexpr int kMaxLongCtx = IE_MAX_LONG_CONTEXT;    // paged KV paths and RoPE table rows
 constexpr int kVocab = IE_VOCAB_SIZE;
 constexpr int kLayers = IE_NUM_LAYERS;
 constexpr int kHidden = IE_HIDDEN_SIZE;

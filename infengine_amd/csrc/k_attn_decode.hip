@@ -45,6 +45,9 @@ static_assert(kAttnTile == 64, "tile = 4 x 16-key MFMA blocks");
 __device__ __forceinline__ int kv_slot(int r, int c) { return r * 16 + (c ^ (r & 15)); }
 
 static_assert(kAttnSplits <= 64, "the merge gives each split one lane");
+// A wave preloads the page ids of its tiles, one per lane: with kAttnSplits splits of
+// kSplitWaves waves, the longest context keeps that within 64 tiles per wave.
+static_assert(kMaxLongCtx / kAttnTile <= 64 * kAttnSplits * 4, "page ids per wave exceed a wave");
 
 // Phase 1: split s of (batch b, kv head g) attends its run of tiles (its NW waves take every
 // NW-th tile) and writes the unnormalised partial (m, l, o) of each of the 4 q heads; with one

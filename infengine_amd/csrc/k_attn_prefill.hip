@@ -269,7 +269,9 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(AttnPrefillParams
 }  // namespace
 
 int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t st) {
-  IE_REQUIRE(p.S >= 1 && p.start_pos >= 0 && p.start_pos + p.S <= kMaxCtx,
+  // the reference-layout planes hold kMaxCtx rows; pages reach kMaxLongCtx positions
+  IE_REQUIRE(p.S >= 1 && p.start_pos >= 0 &&
+                 p.start_pos + p.S <= (p.block_table ? kMaxLongCtx : kMaxCtx),
              "attn_prefill: rows [%d, %d) exceed the KV cache", p.start_pos, p.start_pos + p.S);
   // 32 query rows per workgroup while that fills the chip (S >= 1024: 256 workgroups), else 16
   const bool wide = p.S >= 1024;

@@ -338,7 +338,8 @@ int launch_qkv_rope_scatter(int S, int start_pos, const uint16_t* qkv, const flo
                             const float* sin, uint16_t* q_out, uint16_t* k_cache,
                             uint16_t* v_cache, const int* d_seq_lens, long long cache_stride,
                             hipStream_t st, const int* block_table, int n_pages) {
-  IE_REQUIRE(S >= 1 && start_pos >= 0 && (d_seq_lens || start_pos + S <= kMaxCtx),
+  IE_REQUIRE(S >= 1 && start_pos >= 0 &&
+                 (d_seq_lens || start_pos + S <= (block_table ? kMaxLongCtx : kMaxCtx)),
              "qkv scatter: rows [%d, %d) exceed the KV cache", start_pos, start_pos + S);
   IE_REQUIRE(!block_table || !d_seq_lens, "qkv scatter: paged rows are one sequence's");
   hipLaunchKernelGGL(qkv_rope_scatter_kernel, dim3(S), dim3(256), 0, st, start_pos, qkv, cos, sin,

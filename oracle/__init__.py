@@ -9,7 +9,9 @@ bf16 tensors are numpy uint16 arrays holding the bit patterns.
 
 Parity status of each function (how it is pinned, see tests/test_oracle.py):
   fill_synthetic  - statistics (mean/std) + GPU generator bit-equality
-  rope_tables     - HF transformers _compute_llama3_parameters (library) + closed form
+  rope_freqs      - HF transformers _compute_llama3_parameters (library)
+  rope_tables     - HF llama3 parameters and HF LlamaRotaryEmbedding past 8192 positions
+                    (library fixtures) + closed form cos(fp32(pos * freq)), cos^2 + sin^2 = 1
   rmsnorm         - HF LlamaRMSNorm (library) in bf16
   matmul          - float64 brute force; torch bf16 nn.functional.linear (library)
   swiglu          - torch.nn.functional.silu (library)
@@ -32,6 +34,7 @@ HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "liboracle.so"
 
 HIDDEN, FFN, QH, KVH, HD, VOCAB, MAXCTX, LAYERS = 4096, 14336, 32, 8, 128, 128256, 8192, 32
+LONGCTX = 131072   # positions of the paged (long-context) paths and their RoPE tables
 
 
 def build() -> pathlib.Path:
@@ -48,7 +51,8 @@ def _load() -> C.CDLL:
         "orc_set_sum_order": (None, [I]),
         "orc_fill_synthetic": (None, [P, SZ, U64, U64, F, F]),
         "orc_tensor_id": (U64, [I, I]),
-        "orc_rope_tables": (None, [P, P]),
+        "orc_rope_freqs": (None, [P]),
+        "orc_rope_tables": (None, [I, P, P]),
         "orc_emblookup": (None, [I, P, P, P]),
         "orc_rmsnorm": (None, [I, I, P, P, P]),
         "orc_residual_add": (None, [SZ, P, P]),
@@ -154,10 +158,17 @@ def lm_head_weight(seed: int, std: float = 0.02) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- ops
-def rope_tables() -> tuple[np.ndarray, np.ndarray]:
-    c = np.empty((MAXCTX, 64), np.float32)
-    s = np.empty((MAXCTX, 64), np.float32)
-    _lib.orc_rope_tables(_p(c), _p(s))
+def rope_freqs() -> np.ndarray:
+    """The 64 fp32 Llama-3 scaled inverse frequencies the tables are built from."""
+    f = np.empty(64, np.float32)
+    _lib.orc_rope_freqs(_p(f))
+    return f
+
+
+def rope_tables(n_pos: int = MAXCTX) -> tuple[np.ndarray, np.ndarray]:
+    c = np.empty((n_pos, 64), np.float32)
+    s = np.empty((n_pos, 64), np.float32)
+    _lib.orc_rope_tables(n_pos, _p(c), _p(s))
     return c, s
 
 
@@ -269,9 +280,9 @@ class SyntheticModel:
     """The oracle's copy of ie_model_weights_random_init(seed, std): the same
     tensors, regenerated layer by layer on the host (decode.cu / prefill.cu order)."""
 
-    def __init__(self, seed: int, std: float = 0.02):
+    def __init__(self, seed: int, std: float = 0.02, n_pos: int = LONGCTX):
         self.seed, self.std = seed, std
-        self.cos, self.sin = rope_tables()
+        self.cos, self.sin = rope_tables(n_pos)
         self._emb = None
         self._lm = None
 

@@ -111,13 +111,13 @@ uint64_t orc_tensor_id(int layer, int field) { return 16 + (uint64_t)layer * 16 
 
 // ---------------------------------------------------------------- rope tables
 // rope.cu:68-96 (init_rope_buffer): Llama-3 scaled inverse frequencies (theta
-// 500000, factor 8, low 1, high 4, original context 8192) and fp32 cos/sin of
-// pos * freq for pos < 8192, i < 64.  Same arithmetic types as the reference.
-void orc_rope_tables(float* cos_t, float* sin_t) {
+// 500000, factor 8, low 1, high 4, original context 8192; orc_rope_freqs) and fp32
+// cos/sin of pos * freq for pos < n_pos, i < 64 (the reference stops at 8192; the same
+// formula continues for long contexts).  Same arithmetic types as the reference.
+void orc_rope_freqs(float* freqs) {
   const float theta = 500000.0f;
   const int factor = 8, low_ff = 1, high_ff = 4, orig = 8192;
   const int low_wl = orig / low_ff, high_wl = orig / high_ff;
-  float freqs[64];
   for (int i = 0; i < 64; ++i) {
     const float freq = 1 / std::pow(theta, 2.0 * i / kHeadDim);
     const float wavelength = 2 * std::numbers::pi / freq;
@@ -130,7 +130,13 @@ void orc_rope_tables(float* cos_t, float* sin_t) {
       freqs[i] = (1 - smooth) * (freq / factor) + smooth * freq;
     }
   }
-  for (int pos = 0; pos < kMaxCtx; ++pos)
+}
+
+void orc_rope_tables(int n_pos, float* cos_t, float* sin_t) {
+  float freqs[64];
+  orc_rope_freqs(freqs);
+#pragma omp parallel for schedule(static)
+  for (int pos = 0; pos < n_pos; ++pos)
     for (int i = 0; i < 64; ++i) {
       const float angle = pos * freqs[i];
       cos_t[(size_t)pos * 64 + i] = std::cos(angle);

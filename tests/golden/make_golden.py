@@ -66,6 +66,26 @@ def rope_llama3() -> None:
                         sin=ang.sin().numpy())
 
 
+def rope_llama3_long() -> None:
+    """cos/sin past the reference's 8192 positions (Llama-3.1 runs to 131072), from HF's own
+    LlamaRotaryEmbedding forward: fp32 angles position * inv_freq, as the model computes them."""
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, max_position_embeddings=131072,
+                      rope_parameters={"rope_type": "llama3", "rope_theta": 500000.0,
+                                       "factor": 8.0, "low_freq_factor": 1.0,
+                                       "high_freq_factor": 4.0,
+                                       "original_max_position_embeddings": 8192})
+    rot = LlamaRotaryEmbedding(cfg)
+    pos = torch.tensor([8191, 8192, 8193, 9000, 12345, 16383, 16384, 32768, 65535, 100000,
+                        131071])
+    cos, sin = rot(torch.zeros(1, pos.numel(), 128), pos[None, :])
+    assert rot.attention_scaling == 1.0
+    np.savez_compressed(HERE / "rope_llama3_hf_long.npz", positions=pos.numpy().astype(np.int32),
+                        cos=cos[0, :, :64].numpy(), sin=sin[0, :, :64].numpy())
+
+
 def rmsnorm_hf() -> None:
     from transformers.models.llama.modeling_llama import LlamaRMSNorm
     g = torch.Generator().manual_seed(7)
@@ -95,6 +115,7 @@ def top_p_hf() -> None:
 if __name__ == "__main__":
     argmax_cases()
     rope_llama3()
+    rope_llama3_long()
     rmsnorm_hf()
     top_p_hf()
     for f in sorted(HERE.glob("*.npz")):

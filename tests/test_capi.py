@@ -74,6 +74,8 @@ BOGUS = C.c_void_p(0x1000)   # never dereferenced: every call below fails valida
     lambda l: l.ie_model_weights_free(None),
     lambda l: l.ie_sample_top_p(None, 1, 128256, BOGUS, 0.7, 0.9, 1, 0, BOGUS, BOGUS),
     lambda l: l.ie_sample_top_p_noalloc(None, 17, 131072, BOGUS, 0.7, 0.9, 1, 0, BOGUS),
+    lambda l: l.ie_prefill_paged_chunk(None, None, 0, 1, *[BOGUS] * 8, 1, BOGUS),
+    lambda l: l.ie_attn_prefill_core_paged(None, 1, 9000, BOGUS, BOGUS, 1, BOGUS, 0, BOGUS),
     lambda l: l.ie_decoder_layer_decode(None, None, 0, 1, BOGUS, BOGUS, BOGUS, BOGUS),
 ])
 def test_host_side_validation(hip, call):

@@ -323,7 +323,7 @@ def test_batched_paged_equals_contiguous(hip, model, lens):
         th = (C.c_int * B)()
         if paged:
             hip.check(hip.lib.ie_decode_step_batched_paged(
-                c.handle, model.ref(), B, seq, ptr(toks), ptr(data), ptr(attn), ptr(logits),
+                c.handle, model.ref(), B, seq, ptr(toks), 8192, ptr(data), ptr(attn), ptr(logits),
                 ptr(out), th, ptr(ws), ptr(pool), n_pages, ptr(d_table), stride))
         else:
             hip.check(hip.lib.ie_decode_step_batched(

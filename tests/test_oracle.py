@@ -86,6 +86,35 @@ def test_rope_tables_match_hf_llama3():
     np.testing.assert_allclose(cos.astype(np.float64) ** 2 + sin.astype(np.float64) ** 2, 1.0, atol=1e-6)
 
 
+def test_rope_tables_past_8192_positions():
+    """Rows past the reference's 8192 (the paged paths run to 131072 positions).  Closed form:
+    each row is cos / sin of the fp32 product position * freq_i (numpy's float32 multiply is the
+    same IEEE product).  Against HF's own LlamaRotaryEmbedding forward (fixture): the only
+    difference is the inverse frequencies' rounding (the reference rounds a double, HF computes
+    them in fp32), so |ours - HF| <= pos * |freq_i - inv_freq_i| + ulp(pos * freq_i) per element,
+    a bound a wrong position, frequency or pairing exceeds."""
+    g = np.load(GOLD / "rope_llama3_hf_long.npz")
+    h = np.load(GOLD / "rope_llama3_hf.npz")
+    cos, sin = orc.rope_tables(orc.LONGCTX)
+    freqs = orc.rope_freqs()
+    np.testing.assert_allclose(freqs, h["inv_freq"], rtol=4e-7)
+    short_cos, short_sin = orc.rope_tables()
+    assert np.array_equal(cos[:8192], short_cos) and np.array_equal(sin[:8192], short_sin)
+    pos = g["positions"]
+    ang = (pos.astype(np.float32)[:, None] * freqs[None, :]).astype(np.float64)
+    np.testing.assert_allclose(cos[pos], np.cos(ang), rtol=0, atol=2e-7)
+    np.testing.assert_allclose(sin[pos], np.sin(ang), rtol=0, atol=2e-7)
+    p64 = pos.astype(np.float64)[:, None]
+    dfreq = np.abs(freqs.astype(np.float64) - h["inv_freq"].astype(np.float64))[None, :]
+    prod = np.abs(ang)
+    ulp = np.spacing(prod.astype(np.float32)).astype(np.float64)
+    bound = p64 * dfreq + ulp + 1e-6
+    assert (np.abs(cos[pos] - g["cos"]) <= bound).all()
+    assert (np.abs(sin[pos] - g["sin"]) <= bound).all()
+    np.testing.assert_allclose(cos[pos].astype(np.float64) ** 2 + sin[pos].astype(np.float64) ** 2,
+                               1.0, atol=1e-6)
+
+
 # ---------------------------------------------------------------- rmsnorm
 def test_rmsnorm_matches_hf_fixture():
     g = np.load(GOLD / "rmsnorm_hf.npz")
