@@ -273,8 +273,10 @@ int launch_attn_prefill(const AttnPrefillParams& p, hipStream_t st) {
   IE_REQUIRE(p.S >= 1 && p.start_pos >= 0 &&
                  p.start_pos + p.S <= (p.block_table ? kMaxLongCtx : kMaxCtx),
              "attn_prefill: rows [%d, %d) exceed the KV cache", p.start_pos, p.start_pos + p.S);
-  // 32 query rows per workgroup while that fills the chip (S >= 1024: 256 workgroups), else 16
-  const bool wide = p.S >= 1024;
+  // 32 query rows per workgroup from S = 1792 (448+ workgroups, two per CU), else 16: measured
+  // at S = 1024 / 1280 / 1536 / 1792 / 2048, 16 rows 23.4 / 29.2 / 40.2 / 49.7 / 59.2 us against
+  // 32 rows 29.7 / 38.0 / 43.4 / 49.1 / 54.7 us
+  const bool wide = p.S >= 1792;
   const int nqb = wide ? (p.S + BQ - 1) / BQ : (p.S + 15) / 16;
   const dim3 grid(nqb * kKVHeads);
   if (p.block_table && wide)
