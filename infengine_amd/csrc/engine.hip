@@ -677,33 +677,15 @@ int ie_prefill_paged_chunk(ie_context* c, const ie_model_weights* weights, int s
 
 // ---------------------------------------------------------------- batched decode
 namespace {
-// One batched step over per-sequence caches (block_table null: kv = batch caches in the
-// reference layout, kv_cache_size() apart) or over a page pool (kv = n_pages pages,
-// block_table [batch][table_stride] page ids).
-int batched_step(ie_context* c, const ie_model_weights* weights, int batch, const int* seq_lens,
-                 int* tokenid_buffs, int tokens_stride, ie_bf16* data_buffer,
-                 ie_bf16* attn_buffer, float* output_distr, int* output_tokens, int* tokens_out,
-                 void* workspace, void* kv_caches, const int* block_table, int table_stride,
-                 int n_pages) {
-  IE_REQUIRE(weights && weights_complete(*weights), "decode_step_batched: incomplete weights");
-  IE_REQUIRE(batch >= 1 && batch <= 16, "decode_step_batched: batch %d out of [1, 16]", batch);
-  IE_REQUIRE(seq_lens && tokenid_buffs && data_buffer && attn_buffer && output_distr &&
-                 output_tokens && workspace && kv_caches,
-             "decode_step_batched: null buffer");
-  const int cap = block_table ? kMaxLongCtx : kMaxCtx;
-  for (int b = 0; b < batch; ++b)
-    IE_REQUIRE(seq_lens[b] >= 1 && seq_lens[b] <= cap && seq_lens[b] <= tokens_stride,
-               "decode_step_batched: seq_lens[%d]=%d out of [1, %d] (token rows of %d)", b,
-               seq_lens[b], cap, tokens_stride);
-  const ie_model_weights& W = *weights;
-  hipStream_t st = c->stream;
-  int max_len = 1;
-  for (int b = 0; b < batch; ++b) {
-    c->h_params[1 + b] = seq_lens[b];
-    max_len = std::max(max_len, seq_lens[b]);
-  }
-  IE_CHECK_HIP(hipMemcpyAsync(c->d_params + 1, c->h_params + 1, batch * sizeof(int),
-                              hipMemcpyHostToDevice, st));
+// The kernels of one batched step on stream st, the sequences' lengths already in
+// d_params[1 .. batch].  len_class bounds the longest context and picks the attention path:
+// kAttnDirectMaxCtx (one split per sequence and kv head, no merge launch), kAttnFusedMaxCtx or
+// beyond (split contexts + the merge kernel).
+int enqueue_batched(Context* c, hipStream_t st, const ie_model_weights& W, int batch,
+                    int len_class, int* tokenid_buffs, int tokens_stride, ie_bf16* data_buffer,
+                    ie_bf16* attn_buffer, float* output_distr, int* output_tokens,
+                    void* workspace, void* kv_caches, const int* block_table, int table_stride,
+                    int n_pages) {
   const int* d_sl = c->d_params + 1;
   const DecodeWs w = decode_ws(workspace, batch);
   const long long cstride = (long long)kLayers * kKVLayer;
@@ -743,7 +725,7 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
     g.ss_parts = l == 0 ? 4 : kNormParts;
     g.x_norm_w = L.input_layernorm;
     IE_TRY(launch_gemm(kGemmQkvRope, g, st));
-    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, max_len, batch, cstride, true, st,
+    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, len_class, batch, cstride, true, st,
                        block_table, table_stride, n_pages, true));
     GemmParams o{};
     o.x = attn_buffer;
@@ -795,6 +777,84 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
   IE_TRY(launch_gemm(kGemmF32, lm, st));
   IE_TRY(launch_argmax_rows(batch, kVocab, output_distr, output_tokens, c->d_slots,
                             c->d_counters + kCntArgmax, st));
+  return IE_OK;
+}
+
+// One batched step over per-sequence caches (block_table null: kv = batch caches in the
+// reference layout, kv_cache_size() apart) or over a page pool (kv = n_pages pages,
+// block_table [batch][table_stride] page ids).  With graphs on (the default) the kernels are
+// replayed from a graph captured on first use of the same arguments.
+int batched_step(ie_context* c, const ie_model_weights* weights, int batch, const int* seq_lens,
+                 int* tokenid_buffs, int tokens_stride, ie_bf16* data_buffer,
+                 ie_bf16* attn_buffer, float* output_distr, int* output_tokens, int* tokens_out,
+                 void* workspace, void* kv_caches, const int* block_table, int table_stride,
+                 int n_pages) {
+  IE_REQUIRE(weights && weights_complete(*weights), "decode_step_batched: incomplete weights");
+  IE_REQUIRE(batch >= 1 && batch <= 16, "decode_step_batched: batch %d out of [1, 16]", batch);
+  IE_REQUIRE(seq_lens && tokenid_buffs && data_buffer && attn_buffer && output_distr &&
+                 output_tokens && workspace && kv_caches,
+             "decode_step_batched: null buffer");
+  const int cap = block_table ? kMaxLongCtx : kMaxCtx;
+  for (int b = 0; b < batch; ++b)
+    IE_REQUIRE(seq_lens[b] >= 1 && seq_lens[b] <= cap && seq_lens[b] <= tokens_stride,
+               "decode_step_batched: seq_lens[%d]=%d out of [1, %d] (token rows of %d)", b,
+               seq_lens[b], cap, tokens_stride);
+  hipStream_t st = c->stream;
+  int max_len = 1;
+  for (int b = 0; b < batch; ++b) {
+    c->h_params[1 + b] = seq_lens[b];
+    max_len = std::max(max_len, seq_lens[b]);
+  }
+  IE_CHECK_HIP(hipMemcpyAsync(c->d_params + 1, c->h_params + 1, batch * sizeof(int),
+                              hipMemcpyHostToDevice, st));
+  const int len_class = max_len <= kAttnDirectMaxCtx  ? kAttnDirectMaxCtx
+                        : max_len <= kAttnFusedMaxCtx ? kAttnFusedMaxCtx
+                                                      : cap;
+  if (c->use_graph) {
+    // replayed from a graph captured with the same buffers, batch and attention path (the
+    // lengths are read from d_params on the device)
+    const void* key[16] = {(const void*)weights,
+                           (const void*)(uintptr_t)hash_bytes(weights, sizeof(*weights)),
+                           tokenid_buffs, (const void*)(intptr_t)tokens_stride, data_buffer,
+                           attn_buffer, output_distr, output_tokens, workspace, kv_caches,
+                           block_table, (const void*)(intptr_t)table_stride,
+                           (const void*)(intptr_t)n_pages, (const void*)(intptr_t)batch,
+                           (const void*)(intptr_t)len_class, nullptr};
+    Context::BatchGraph* slot = nullptr;
+    for (auto& bg : c->bgraph)
+      if (bg.exec && std::memcmp(bg.key, key, sizeof key) == 0) slot = &bg;
+    if (!slot) {
+      slot = &c->bgraph[0];
+      for (auto& bg : c->bgraph)
+        if (!bg.exec || bg.used < slot->used) slot = &bg;
+      if (slot->exec) {
+        IE_CHECK_HIP(hipGraphExecDestroy(slot->exec));
+        slot->exec = nullptr;
+      }
+      hipGraph_t g = nullptr;
+      IE_CHECK_HIP(hipStreamBeginCapture(c->capture, hipStreamCaptureModeThreadLocal));
+      const int rc = enqueue_batched(c, c->capture, *weights, batch, len_class, tokenid_buffs,
+                                     tokens_stride, data_buffer, attn_buffer, output_distr,
+                                     output_tokens, workspace, kv_caches, block_table,
+                                     table_stride, n_pages);
+      const hipError_t ec = hipStreamEndCapture(c->capture, &g);
+      if (rc != IE_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+      }
+      IE_CHECK_HIP(ec);
+      const hipError_t ei = hipGraphInstantiate(&slot->exec, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      IE_CHECK_HIP(ei);
+      std::memcpy(slot->key, key, sizeof key);
+    }
+    slot->used = ++c->bgraph_tick;
+    IE_CHECK_HIP(hipGraphLaunch(slot->exec, st));
+  } else {
+    IE_TRY(enqueue_batched(c, st, *weights, batch, len_class, tokenid_buffs, tokens_stride,
+                           data_buffer, attn_buffer, output_distr, output_tokens, workspace,
+                           kv_caches, block_table, table_stride, n_pages));
+  }
   if (tokens_out) {
     IE_CHECK_HIP(hipMemcpyAsync(c->h_token, output_tokens, batch * sizeof(int),
                                 hipMemcpyDeviceToHost, st));

@@ -242,6 +242,14 @@ struct Context {
   // captured decode-step graph and the arguments it was captured with
   hipGraphExec_t graph_exec = nullptr;
   const void* graph_key[12] = {};
+  // captured batched steps, least recently used replaced first (a serving loop alternates
+  // between a few batch compositions)
+  struct BatchGraph {
+    hipGraphExec_t exec = nullptr;
+    const void* key[16] = {};
+    unsigned long long used = 0;
+  } bgraph[4];
+  unsigned long long bgraph_tick = 0;
   // split-K partials of the op-level GEMM entry (allocated on first use)
   float* gemm_ws = nullptr;
   size_t gemm_ws_bytes = 0;

@@ -279,6 +279,67 @@ def test_prefill_paged_equals_contiguous(hip, model, S):
     c.close()
 
 
+def test_batched_graph_replays_equal_eager(hip, ctx, model):
+    """Batched steps replayed from captured graphs against the same steps launched eagerly, on
+    paged caches: batches of 16 and 3 alternate (a graph per composition, reused), and sequence 0
+    crosses the 2048-position switch of the attention path (a new capture); the next tokens are
+    written back by eager device work between replays.  Every step's logits and tokens and the
+    final pools bit-identical."""
+    from infengine_amd.engine import Context, ptr
+    B = 16
+    lens0 = [2046] + [300 + 37 * b for b in range(1, B)]
+    schedule = [16, 16, 3, 16, 3, 3, 16, 16]
+    say(f"batched graph replays vs eager, schedule {schedule}")
+    page_elems = hip.lib.ie_kv_page_size() // 2
+    stride = (max(lens0) + len(schedule) + 63) // 64
+    nblk = [(n + len(schedule) + 63) // 64 for n in lens0]
+    n_pages = sum(nblk)
+    tab = np.full((B, stride), -1, dtype=np.int32)
+    first = np.cumsum([0] + nblk[:-1])
+    for b in range(B):
+        tab[b, :nblk[b]] = first[b] + np.arange(nblk[b])
+    table = torch.from_numpy(tab).cuda()
+    g = torch.Generator(device="cuda").manual_seed(SEED)
+    pool0 = (torch.randn(n_pages * page_elems, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+    toks0 = torch.randint(0, 128256, (B, stride * 64), dtype=torch.int32, device="cuda",
+                          generator=g)
+    runs = []
+    for graph in (False, True):
+        c = Context(0, graph=graph)
+        pool = pool0.clone().view(torch.int16)
+        toks = toks0.clone()
+        ws = torch.zeros(hip.lib.ie_batch_workspace_size(B), dtype=torch.uint8, device="cuda")
+        data = torch.zeros(B, 4096, dtype=torch.bfloat16, device="cuda")
+        attn = torch.zeros_like(data)
+        logits = torch.zeros(B, 128256, dtype=torch.float32, device="cuda")
+        out = torch.zeros(B, dtype=torch.int32, device="cuda")
+        lens = list(lens0)
+        steps = []
+        for nb in schedule:
+            seq = (C.c_int * nb)(*lens[:nb])
+            th = (C.c_int * nb)()
+            hip.check(hip.lib.ie_decode_step_batched_paged(
+                c.handle, model.ref(), nb, seq, ptr(toks), toks.shape[1], ptr(data), ptr(attn),
+                ptr(logits), ptr(out), th, ptr(ws), ptr(pool), n_pages, ptr(table), stride))
+            torch.cuda.synchronize()
+            assert list(th) == host(out[:nb]).tolist()
+            steps.append((host(logits[:nb]).copy(), list(th)))
+            # eager device work between replays: the new tokens into the token rows
+            rows = torch.arange(nb, device="cuda")
+            cols = torch.tensor(lens[:nb], device="cuda", dtype=torch.long)
+            toks[rows, cols] = out[:nb]
+            for b in range(nb):
+                lens[b] += 1
+        runs.append((steps, pool))
+        c.close()
+    assert lens0[0] < 2049 <= lens0[0] + schedule.count(16) + schedule.count(3)
+    for i, ((le, te), (lg, tg)) in enumerate(zip(runs[0][0], runs[1][0])):
+        assert te == tg, f"step {i}: tokens differ"
+        assert np.array_equal(le, lg), f"step {i}: logits differ"
+    assert torch.equal(runs[0][1], runs[1][1]), "pools differ"
+    torch.cuda.set_stream(ctx.stream)
+
+
 @pytest.mark.parametrize("lens", [[101, 257, 64], [2100, 257, 64], LENS16, LENS16_LONG])
 def test_batched_paged_equals_contiguous(hip, model, lens):
     """ie_decode_step_batched_paged on a page pool (the sequences' 64-position blocks scattered
