@@ -192,13 +192,16 @@ GEMM_EPI = {"bf16": 0, "resid": 1, "f32": 2, "swiglu": 3}
 
 
 @pytest.mark.parametrize("epi", list(GEMM_EPI))
-@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (24, 1000), (32, 4096), (40, 1000),
-                                 (48, 4096), (100, 4096), (300, 1000), (512, 4096), (2048, 6144),
+@pytest.mark.parametrize("m,n", [(7, 1000), (16, 4096), (17, 4096), (24, 1000), (32, 4096),
+                                 (33, 6144), (40, 1000), (48, 4096), (64, 4096), (64, 14336),
+                                 (100, 4096), (300, 1000), (512, 4096), (2048, 6144),
                                  (2048, 4096), (2048, 14336)])
 def test_gemm_epilogues(hip, ctx, epi, m, n):
     """Every fused epilogue of the MFMA GEMM on each kernel the launcher picks: the skinny
-    streaming kernel (m <= 16, ragged n), its 2- and 3-row-block forms (m = 24, 32 and m = 40,
-    48: bf16 / resid / SwiGLU), 128 x 128 tiles (m = 100, 300: f32 / SwiGLU; f32 at m = 24..48), K split
+    streaming kernel (m <= 16, ragged n), its 2- and 3-row-block forms (m = 17, 24, 32 and m = 33,
+    40, 48: bf16 / resid / SwiGLU), 128 x 128 tiles (m = 100, 300: f32 / SwiGLU; f32 at
+    m = 17..64), K split across workgroups with a reduction at m = 64 (n = 4096, and 14336 where
+    SwiGLU splits its 2 x 14336-column product), K split
     across workgroups with a reduction (bf16 / resid at m = 100, 300, 512), and the prefill sizes:
     192 x 256 tiles (bf16 / resid at n = 6144), 256 x 256 tiles (SwiGLU at n = 4096), 256 x 128
     tiles (the others at n = 4096 and 6144), and at n = 14336 a launch split by output columns
@@ -240,11 +243,12 @@ def test_gemm_epilogues(hip, ctx, epi, m, n):
 
 
 @pytest.mark.parametrize("epi", ["bf16", "resid"])
-@pytest.mark.parametrize("m", [24, 40, 2048])
+@pytest.mark.parametrize("m", [17, 24, 40, 64, 2048])
 def test_gemm_down_projection_shapes(hip, ctx, epi, m):
     """The down projection (k 14336, n 4096) as prefill runs it: the 2- and 3-row-block streaming
-    kernel at 24 and 40 rows (K = 14336 instantiations) and the 2048-row MFMA tiles of config 4;
-    every row at 24 / 40, sampled rows at 2048, against the oracle."""
+    kernel at 17, 24 and 40 rows (K = 14336 instantiations), K split across workgroups at 64 rows
+    and the 2048-row MFMA tiles of config 4; every row up to 64, sampled rows at 2048, against the
+    oracle."""
     k, n = 14336, 4096
     say(f"gemm_ex down {epi} m={m} k={k} n={n}")
     x = orc.synthetic((m, k), 25, m, 0.0, 1.0)
