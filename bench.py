@@ -106,6 +106,53 @@ def calibration_copy(nbytes: int = 256 << 20) -> None:
     torch.cuda.synchronize()
 
 
+def timed_launches(stream, fn) -> float:
+    """Microseconds per call of fn, timed with HIP events on `stream`. The clocks settle over the
+    first ~0.1 s of sustained MFMA load (a cold launch runs 10-15 % slow), as they do inside a
+    prefill's 32 back-to-back layers: warm up for 150 ms, then take the median of three timed
+    runs of 10 launches."""
+    import torch
+
+    t_end = time.perf_counter() + 0.15
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+    runs = []
+    for _ in range(3):
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record(stream)
+        for _ in range(10):
+            fn()
+        g1.record(stream)
+        g1.synchronize()
+        runs.append(g0.elapsed_time(g1) * 1e3 / 10)
+    return sorted(runs)[1]
+
+
+def prefill_attention(ctx, S: int) -> dict:
+    """One layer's causal flash attention at S query rows (start 0) through
+    ie_attn_prefill_core, timed like the GEMMs: 4 * 32 * 128 * S (S + 1) / 2 flop of causal
+    work against the bf16 MFMA peak."""
+    import torch
+
+    from infengine_amd import check, lib
+    from infengine_amd.engine import ptr
+
+    q = torch.randn(S, 32, 128, device="cuda").to(torch.bfloat16)
+    k = torch.randn(8, 8192, 128, device="cuda").to(torch.bfloat16)
+    v = torch.randn(8, 8192, 128, device="cuda").to(torch.bfloat16)
+    out = torch.empty(S, HIDDEN, dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+    us = timed_launches(ctx.stream, lambda: check(lib.ie_attn_prefill_core(
+        ctx.handle, S, 0, ptr(q), ptr(k), ptr(v), ptr(out))))
+    flop = 4.0 * 32 * 128 * S * (S + 1) / 2
+    tf = flop / (us * 1e-6) / 1e12
+    del q, k, v, out
+    return {"seq_len": S, "us": round(us, 1), "tflops": round(tf, 1),
+            "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
 def prefill_gemms(ctx, P: int) -> dict:
     """The four prefill GEMM shapes at M = P (QKV, O with residual, gate/up with SwiGLU, down with
     residual) through ie_gemm_ex, and the same products through torch.matmul (hipBLASLt), each
@@ -116,27 +163,8 @@ def prefill_gemms(ctx, P: int) -> dict:
     from infengine_amd import check, lib
     from infengine_amd.engine import ptr
 
-    stream = ctx.stream
-
     def timed(fn) -> float:
-        # The clocks settle over the first ~0.1 s of sustained MFMA load (a cold launch runs
-        # 10-15 % slow), as they do inside a prefill's 32 back-to-back layers: warm up for
-        # 150 ms, then take the median of three timed runs of 10 launches.
-        t_end = time.perf_counter() + 0.15
-        while time.perf_counter() < t_end:
-            for _ in range(8):
-                fn()
-            torch.cuda.synchronize()
-        runs = []
-        for _ in range(3):
-            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            g0.record(stream)
-            for _ in range(10):
-                fn()
-            g1.record(stream)
-            g1.synchronize()
-            runs.append(g0.elapsed_time(g1) * 1e3 / 10)
-        return sorted(runs)[1]
+        return timed_launches(ctx.stream, fn)
 
     gemms = {}
     for name, epi, k, n in (("qkv", 0, HIDDEN, 6144), ("o", 1, HIDDEN, HIDDEN),
@@ -181,6 +209,9 @@ def main() -> int:
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill GEMM shapes at M = --prefill-len, ours and torch.matmul "
                          "(for profiling them); prints their JSON")
+    ap.add_argument("--attn-only", action="store_true",
+                    help="only the prefill attention at S = --prefill-len (for profiling it); "
+                         "prints its JSON")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -205,6 +236,11 @@ def main() -> int:
     ctx = Context(0, graph=not args.no_graph)
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": prefill_gemms(ctx, args.prefill_len or 2048)}), flush=True)
+        ctx.close()
+        return 0
+    if args.attn_only:
+        print(json.dumps({"prefill_attention": prefill_attention(ctx, args.prefill_len or 2048)}),
+              flush=True)
         ctx.close()
         return 0
     log("random-init weights (16.06 GB)")
@@ -314,10 +350,12 @@ def main() -> int:
         pdt = (time.perf_counter() - t0) / reps
         del req2
         gemms = prefill_gemms(ctx, P)
+        attention = prefill_attention(ctx, P)
         flops = 2.0 * P * LAYER_GEMM_PARAMS * LAYERS
         prefill2048 = {"seq_len": P, "ms": round(pdt * 1e3, 2), "tokens_per_s": round(P / pdt, 1),
                        "layer_gemm_tflops_per_s": round(flops / pdt / 1e12, 1),
-                       "gemm": gemms, "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS}
+                       "gemm": gemms, "attention": attention,
+                       "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS}
 
     # ---- dominant kernel, timed live on its own stream with HIP events
     log("gate/up GEMV kernel timing")
