@@ -34,8 +34,12 @@ def reference(q, k, v, start_pos):
     return out
 
 
+# the kernel forms: 16 rows per 4-wave workgroup below 1280 rows, two 16-row blocks per 8-wave
+# workgroup up to 2559 (1500 + 37: the two blocks of a workgroup end in different key tiles), 32
+# rows per wave from 2560
 @pytest.mark.parametrize("S,start_pos", [(1, 0), (17, 0), (96, 0), (300, 5), (1000, 0),
-                                         (2048, 0), (200, 2000)])
+                                         (1500, 37), (2048, 0), (200, 2000), (2600, 0),
+                                         (3000, 1000)])
 def test_attn_prefill_core(hip, ctx, S, start_pos):
     say(f"attn_prefill_core S={S} start_pos={start_pos}")
     g = torch.Generator(device="cuda").manual_seed(1000 + S + start_pos)

@@ -70,7 +70,8 @@ def _attn_reference(q, k, v, start_pos):
 
 
 # start positions past 8192, a chunk that crosses it, and the 16384 mark
-@pytest.mark.parametrize("S,start_pos", [(300, 9000), (1100, 7800), (64, 16371), (2048, 14336)])
+@pytest.mark.parametrize("S,start_pos", [(300, 9000), (1100, 7800), (64, 16371), (2048, 14336),
+                                         (2600, 9000)])
 def test_attn_prefill_core_paged_long(hip, ctx, S, start_pos):
     say(f"attn_prefill_core_paged S={S} start_pos={start_pos}")
     n = start_pos + S
