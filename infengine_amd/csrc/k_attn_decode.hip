@@ -8,9 +8,9 @@
 //
 //   grid  = (max_splits, 8 kv heads, batch), block = 4 waves
 //   split s of kv head g owns a contiguous run of 64-key tiles of the context 0..S-1 (four
-//   tiles per split, one per wave, while the split cap allows); a wave stages its tile's V
-//   rows (and at batch 1 its K rows) in its own LDS slice with direct-to-LDS loads, and
-//   computes, with
+//   tiles per split, one per wave, while the split cap allows); a wave stages its tile's K
+//   and V rows in LDS (K by direct-to-LDS loads; V likewise at batch 1, through registers in
+//   the batched forms), and computes, with
 //   v_mfma_f32_16x16x32_bf16, S^T = K . Q^T for the 4 GQA q heads of the kv head (GQA: q head h
 //   reads kv head h/4, attn.cu:51-53) as 4 of the 16 MFMA columns, an online softmax per head,
 //   and O^T += V^T . P^T with P^T taken straight from the S^T accumulators and V^T read with
@@ -51,14 +51,17 @@ static_assert(kMaxLongCtx / kAttnTile <= 64 * kAttnSplits * 4, "page ids per wav
 
 // Phase 1: split s of (batch b, kv head g) attends its run of tiles (its NW waves take every
 // NW-th tile) and writes the unnormalised partial (m, l, o) of each of the 4 q heads; with one
-// split (max_splits = 1, batched, NW = 8) it writes the normalised bf16 output instead.  KREG: K
-// fragments are loaded straight into registers (72 KiB of LDS per 4-wave workgroup, two
-// workgroups per CU: the batched grid); otherwise K goes through LDS like V (136 KiB, one
-// workgroup per CU; measured 0.7% faster per decode step at batch 1).
-template <bool KREG, int NW>
+// split (max_splits = 1, batched, NW = 8) it writes the normalised bf16 output instead.  VREG: one
+// 16 KiB LDS slice per wave, K through it and V staged in registers then written over K (72 KiB
+// of LDS per 4-wave workgroup, two workgroups per CU: the batched grid; 144 KiB for the 8-wave
+// form); otherwise K and V each have a slice (136 KiB, one workgroup per CU; 0.7% faster per
+// decode step at batch 1 than K fragments loaded straight into registers).
+template <bool VREG, int NW>
 __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodeParams p) {
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave id made provably uniform: the tile indices and buffer descriptors derived from it stay
+  // in SGPRs (otherwise every buffer load becomes a readfirstlane loop)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int fr = lane & 15, G = lane >> 4;
   const int S = p.d_seq_len ? p.d_seq_len[b] : p.seq_len;
   const int ntiles = (S + kAttnTile - 1) / kAttnTile;
@@ -67,7 +70,7 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
   const int tps = (ntiles + ns - 1) / ns;
   const int t0 = split * tps, t1 = min(ntiles, t0 + tps);
 
-  __shared__ u32x4_t kvlds[NW][KREG ? 1 : 2][kTC];  // per wave: (K tile,) V tile
+  __shared__ u32x4_t kvlds[NW][VREG ? 1 : 2][kTC];  // per wave: K tile (then V over it), V tile
   __shared__ float xo[NW][kGQA][kHeadDim];
   __shared__ float xml[NW][kGQA][2];
   const uint16_t* Kh = p.k_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
 #pragma unroll
   for (int db = 0; db < 8; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   u32x4_t* kt = kvlds[wave][0];
-  u32x4_t* vt = kvlds[wave][KREG ? 0 : 1];
+  u32x4_t* vt = kvlds[wave][VREG ? 0 : 1];
 
   // paged KV: lane i holds the page of this wave's i-th tile (one load ahead of the loop)
   const bool paged = p.block_table != nullptr;
@@ -107,8 +110,6 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
   }
   int it = 0;
   for (int t = t0 + wave; t < t1; t += NW, ++it) {
-    // K fragments kk[kb][ks] = K[key0 + 16 kb + fr][32 ks + 8 G .. +8], straight from memory
-    // (KREG) or from the LDS tile below
     const int key0 = t * kAttnTile;
     // the tile's buffers: rows key0.. of the sequence's cache, or rows 0.. of its page (a page
     // id outside the pool reads as zero)
@@ -123,33 +124,35 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
       vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(p.v_cache + base), 0, bytes, kBufferFlags);
       kr0 = 0;
     }
-    u32x4_t kk[4][4];
-    if constexpr (KREG) {
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          kk[kb][ks] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-              krs, (uint32_t)((kr0 + 16 * kb + fr) * kRowBytes + (4 * ks + G) * 16), 0, 0));
-    }
-    // tiles to LDS: load j fills rows 4j .. 4j+3; lane fills slot lane%16 of row 4j + lane/16
-    // from global chunk (lane%16) ^ (row & 15).  The wave only reads its own slice, so its own
-    // vmcnt wait is the whole synchronisation.
+    // Tile to LDS: load j fills rows 4j .. 4j+3; lane fills slot lane%16 of row 4j + lane/16
+    // with global chunk (lane%16) ^ (row & 15).  The wave only reads its own slice, so its own
+    // vmcnt wait is the whole synchronisation.  VREG (the 8-wave form, one 16 KiB slice per
+    // wave): K goes through the slice by direct-to-LDS loads while V is loaded into registers,
+    // row-contiguous, and written over K once the K fragments are in registers.  (Loading the
+    // K fragments straight from memory instead reads 64-byte pieces of 16 rows per lane
+    // quad and issued ~3x slower than row-contiguous loads.)
+    u32x4_t vv[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int r = 4 * j + G;
       const uint32_t off = (uint32_t)((kr0 + r) * kRowBytes + ((fr ^ (r & 15)) * 16));
-      if constexpr (!KREG)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)&kt[64 * j], 16, off, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)&vt[64 * j], 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)&kt[64 * j], 16, off, 0, 0, 0);
+      if constexpr (!VREG)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)&vt[64 * j], 16, off, 0, 0, 0);
     }
-    if constexpr (!KREG) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if constexpr (VREG) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kk[kb][ks] = kt[kv_slot(16 * kb + fr, 4 * ks + G)];
+      for (int j = 0; j < 16; ++j)
+        vv[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+            vrs, (uint32_t)((kr0 + 4 * j + G) * kRowBytes + fr * 16), 0, 0));
     }
+    // K fragments kk[kb][ks] = K[key0 + 16 kb + fr][32 ks + 8 G .. +8] from the LDS tile
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VREG ? 16 : 0) : "memory");
+    u32x4_t kk[4][4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kk[kb][ks] = kt[kv_slot(16 * kb + fr, 4 * ks + G)];
 
     // ---- S^T blocks: s[kb][r] = S[q head 4g + fr][key key0 + 16 kb + 4 G + r]
     f32x4_t s[4];
@@ -200,7 +203,13 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
     }
     // ---- O^T[d][q] += V^T[d][keys] . P^T[keys][q]; V^T by transposed LDS reads (source lane
     //      s of a 16-lane group reads V[key0 + s/4][d0 + 4 (s%4) .. +3])
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the V tile has landed in LDS
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the V tile has landed (LDS or registers)
+    if constexpr (VREG) {
+      // every K fragment read has returned (the MFMAs above consumed them): V over K
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < 16; ++j) vt[kv_slot(4 * j + G, fr)] = vv[j];
+    }
     const int kr = fr >> 2, dq = fr & 3;
 #pragma unroll
     for (int db = 0; db < 8; ++db) {

@@ -50,8 +50,12 @@ struct SkSrc {
   uint32_t wo[4], xo[4];
 };
 
+// (the byte count is made provably uniform: a row count clamped with min/max can come out of a
+// VALU instruction, and a descriptor in VGPRs turns every load into a readfirstlane loop)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const uint16_t* base, int rows, int K) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, rows * K * 2, kBufferFlags);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0,
+                                           __builtin_amdgcn_readfirstlane(rows * K * 2),
+                                           kBufferFlags);
 }
 
 // Loads of one step (k offset ks from each row start), 4 rows x 256 bytes per instruction: lane
