@@ -59,7 +59,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const uint16_t* base, 
 }
 
 // Loads of one step (k offset ks from each row start), 4 rows x 256 bytes per instruction: lane
-// (r, q) loads 16-byte chunk r of row 4j + q of each W tile, or of the X rows.
+// (r, q) loads 16-byte chunk r of row 4j + q of each W tile, or of the X rows.  The weights are
+// read exactly once per launch: nontemporal loads (cache policy nt), as the GEMV's; measured 8-10%
+// faster per projection than the default policy (the X rows, re-read by every workgroup, keep it).
 template <int NT>
 __device__ __forceinline__ void sk_load_w(const SkSrc& src, int ks, u32x4_t (&w)[NT][4]) {
 #pragma unroll
@@ -67,7 +69,7 @@ __device__ __forceinline__ void sk_load_w(const SkSrc& src, int ks, u32x4_t (&w)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       w[t][j] = __builtin_bit_cast(
-          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src.w[t], src.wo[j], 2 * ks, 0));
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src.w[t], src.wo[j], 2 * ks, 2));
 }
 
 __device__ __forceinline__ void sk_load_x(const SkSrc& src, int ks, u32x4_t (&xv)[4]) {
