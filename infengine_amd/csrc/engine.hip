@@ -44,8 +44,6 @@ struct DecodeWs {
   float* ss;        // [256][16]       partial sums of squares of those rows (batched path)
 };
 
-// Producer workgroups of a 4096-column skinny GEMM: the partial sums of squares per row.
-constexpr int kNormParts = kHidden / 16;
 
 size_t decode_ws_bytes(int batch) {
   return align256((size_t)batch * kHidden * 2) + align256((size_t)batch * kFFN * 2) +
@@ -722,7 +720,7 @@ int enqueue_batched(Context* c, hipStream_t st, const ie_model_weights& W, int b
     g.n_pages = n_pages;
     g.d_seq_len = d_sl;
     g.ss_in = w.ss;
-    g.ss_parts = l == 0 ? 4 : kNormParts;
+    g.ss_parts = kNormParts;
     g.x_norm_w = L.input_layernorm;
     IE_TRY(launch_gemm(kGemmQkvRope, g, st));
     IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, len_class, batch, cstride, true, st,

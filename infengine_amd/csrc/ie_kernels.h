@@ -83,6 +83,9 @@ int launch_emblookup(int rows, const int* ids, const uint16_t* table, uint16_t* 
                      const int* d_seq_len, int ids_stride, hipStream_t st);
 // For a skinny GEMM that normalises its X rows: the sums of squares of rows 0..15 as 4 partials
 // per row (ss[m][4]: the row's sum, then zeros; rows >= `rows` all zero).
+// Partial sums of squares per row handed to an RMSNorm folded into the next projection: one per
+// producer workgroup of a 4096-column skinny GEMM (16 columns each).
+constexpr int kNormParts = kHidden / 16;
 int launch_rmsnorm_prep(int rows, const uint16_t* x, float* ss, hipStream_t st);
 int launch_rmsnorm(int rows, const uint16_t* x, const uint16_t* w, uint16_t* out,
                    hipStream_t st);

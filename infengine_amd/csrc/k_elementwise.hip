@@ -249,7 +249,8 @@ int launch_emblookup(int rows, const int* ids, const uint16_t* table, uint16_t* 
   return IE_OK;
 }
 
-// One block per row of 16 (rows past `rows` write a zero sum).
+// One block per row of 16 (rows past `rows` write a zero sum); thread t writes partial t.
+static_assert(kNormParts == 256, "one partial per thread");
 __global__ __launch_bounds__(256) void rmsnorm_prep_kernel(int rows, const uint16_t* x,
                                                            float* ss) {
   __shared__ float red[4];
@@ -271,7 +272,8 @@ __global__ __launch_bounds__(256) void rmsnorm_prep_kernel(int rows, const uint1
   s = wave_sum(s);
   if (lane == 0) red[wave] = s;
   __syncthreads();
-  if (tid < 4) ss[row * 4 + tid] = tid == 0 ? (red[0] + red[1]) + (red[2] + red[3]) : 0.f;
+  // the layout of the skinny GEMM's residual epilogue: kNormParts partials per row
+  ss[row * kNormParts + tid] = tid == 0 ? (red[0] + red[1]) + (red[2] + red[3]) : 0.f;
 }
 
 int launch_rmsnorm_prep(int rows, const uint16_t* x, float* ss, hipStream_t st) {

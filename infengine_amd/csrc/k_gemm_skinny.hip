@@ -35,9 +35,10 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kSkRows = 16;   // weight rows (output columns) per workgroup
 constexpr int kSkSplit = 4;   // waves per workgroup = K quarters
 constexpr int kSkStep = 128;  // k per step
-// Folded RMSNorm: each of a row's 16 summing threads takes up to kSsLoads float4 partials, so up
-// to 16 * 4 * kSsLoads = 256 producer workgroups.
+// Folded RMSNorm: each of a row's 16 summing threads takes kSsLoads float4 partials, the row's
+// kNormParts partial sums of squares (one per producer workgroup, zeros where fewer produce).
 constexpr int kSsLoads = 4;
+static_assert(kNormParts == 16 * 4 * kSsLoads, "kNormParts partials per row");
 
 constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw 32-bit access)
 
@@ -247,10 +248,19 @@ void gemm_skinny_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < kSsLoads; ++i) {
       const int b = 4 * (ss_lane + 16 * i);
-      ssv[i] = b < p.ss_parts ? *reinterpret_cast<const float4*>(p.ss_in + ss_row * p.ss_parts + b)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
+      // (every row has kNormParts partials, so no load is conditional: a load under a
+      // condition made the compiler wait for each one before the weight stream started)
+      ssv[i] = *reinterpret_cast<const float4*>(p.ss_in + ss_row * kNormParts + b);
     }
   }
+  // Epilogue operands, loaded ahead of the weight stream so that the epilogue does not end the
+  // workgroup on load latencies: the residual columns, or the RoPE position (then its angles and
+  // page below).  Every wave loads them (wave 0 stores the outputs): no load is conditional.
+  const int em = min(r, max(p.M - 1, 0)), en = min(n0 + 4 * q, max(p.N - 4, 0));
+  int epos = 0;  // (the sequence length here; the position after the weight loads are issued)
+  uint2 eold = make_uint2(0u, 0u);
+  if constexpr (EPI == kGemmQkvRope) epos = p.d_seq_len[em];
+  if constexpr (EPI == kGemmResid) eold = *reinterpret_cast<const uint2*>(p.y + (size_t)em * p.ldy + en);
   __builtin_amdgcn_sched_barrier(0);
   sk_load_w<NT>(src, kbase, w0);
   sk_load_x(src, kbase, xv);
@@ -259,6 +269,21 @@ void gemm_skinny_kernel(GemmParams p) {
     nm.nw = sk_load_nw(nm.w, kbase, r);
   }
   if (steps > 1) sk_load_w<NT>(src, kbase + kSkStep, w1);
+  float ecos[4], esin[4];
+  int epage = 0;
+  if constexpr (EPI == kGemmQkvRope) {
+    epos -= 1;
+    const int jp = (blockIdx.x & 7) * 8 + 4 * (q & 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ecos[i] = p.rope_cos[epos * 64 + jp + i];
+      esin[i] = p.rope_sin[epos * 64 + jp + i];
+    }
+    // (a table entry of row 0 when the cache is not paged: the load stays unconditional)
+    const int* bt = p.block_table ? p.block_table + (size_t)em * p.table_stride + epos / kPagePos
+                                  : p.d_seq_len;
+    epage = *bt;
+  }
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (NORM) {
     float sum = 0.f;
@@ -303,7 +328,7 @@ void gemm_skinny_kernel(GemmParams p) {
       float v[4] = {0.f, 0.f, 0.f, 0.f};
       if (m < p.M && n < p.N) {
         uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n);
-        const uint2 old = *dst;
+        const uint2 old = eold;
         v[0] = bf2f(f2bf(bf_lo(old.x) + bf2f(f2bf(acc0[0]))));
         v[1] = bf2f(f2bf(bf_hi(old.x) + bf2f(f2bf(acc0[1]))));
         v[2] = bf2f(f2bf(bf_lo(old.y) + bf2f(f2bf(acc0[2]))));
@@ -330,12 +355,12 @@ void gemm_skinny_kernel(GemmParams p) {
     }
     if (m >= p.M) return;
     const int head = blockIdx.x >> 3, jp = (blockIdx.x & 7) * 8 + 4 * (q & 1);
-    const int pos = p.d_seq_len[m] - 1;
+    const int pos = epos;
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (head < kQHeads + kKVHeads) {
-        const float c = p.rope_cos[pos * 64 + jp + i], sn = p.rope_sin[pos * 64 + jp + i];
+        const float c = ecos[i], sn = esin[i];
         v[i] = hi ? a[i] * sn + b[i] * c : a[i] * c - b[i] * sn;
       } else {
         v[i] = hi ? b[i] : a[i];
@@ -350,7 +375,7 @@ void gemm_skinny_kernel(GemmParams p) {
       uint16_t* const plane = is_k ? p.k_cache : p.v_cache;
       if (p.block_table) {
         // paged: row pos % kPagePos of the page holding block pos / kPagePos
-        const int page = p.block_table[(size_t)m * p.table_stride + pos / kPagePos];
+        const int page = epage;
         if (page < 0 || page >= p.n_pages) return;
         dst = plane + (size_t)page * kPageElems + ((size_t)kvh * kPagePos + pos % kPagePos) * kHeadDim;
       } else {
@@ -367,7 +392,7 @@ void gemm_skinny_kernel(GemmParams p) {
         make_float4(acc0[0], acc0[1], acc0[2], acc0[3]);
   } else if constexpr (EPI == kGemmResid) {
     uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n);
-    const uint2 old = *dst;
+    const uint2 old = eold;
     *dst = make_uint2(
         pack_bf2(bf_lo(old.x) + bf2f(f2bf(acc0[0])), bf_hi(old.x) + bf2f(f2bf(acc0[1]))),
         pack_bf2(bf_lo(old.y) + bf2f(f2bf(acc0[2])), bf_hi(old.y) + bf2f(f2bf(acc0[3]))));
@@ -622,11 +647,11 @@ int launch_gemm_skinny_mb(int epi, const GemmParams& p, hipStream_t st) {
 int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {
   IE_REQUIRE(gemm_skinny_fits(p), "gemm_skinny: needs M <= %d and K %% %d == 0 (M=%d K=%d)",
              kSkRows, kSkSplit * kSkStep, p.M, p.K);
-  IE_REQUIRE(!p.ss_in || (p.ss_parts >= 4 && p.ss_parts % 4 == 0 && p.ss_parts <= 64 * kSsLoads &&
+  IE_REQUIRE(!p.ss_in || (p.ss_parts == kNormParts &&
                           p.x_norm_w && (epi == kGemmSwiglu || epi == kGemmQkvRope)),
              "gemm_skinny: RMSNorm of the X rows (SwiGLU / QKV projections) needs the norm weight "
-             "and 4..%d partial sums per row (a multiple of 4)",
-             64 * kSsLoads);
+             "and %d partial sums per row",
+             kNormParts);
   IE_REQUIRE(!p.ss_out || (epi == kGemmResid && p.N % 16 == 0),
              "gemm_skinny: the sums-of-squares output is a residual-epilogue option");
   switch (epi) {
