@@ -308,7 +308,7 @@ int ie_context_create(ie_context** out, int device, void* stream) {
       break;
     }
     if (hipMalloc(&c->d_counters, kNumCounters * sizeof(unsigned int)) != hipSuccess ||
-        hipMalloc(&c->d_slots, kNumSlots * sizeof(unsigned long long)) != hipSuccess ||
+        hipMalloc(&c->d_slots, kNumSlots * kSlotStride * sizeof(unsigned long long)) != hipSuccess ||
         hipMalloc(&c->d_params, 64 * sizeof(int)) != hipSuccess ||
         hipHostMalloc(&c->h_params, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc(&c->h_token, 64 * sizeof(int), hipHostMallocMapped) != hipSuccess) {
@@ -326,7 +326,7 @@ int ie_context_create(ie_context** out, int device, void* stream) {
       break;
     }
     if (hipMemset(c->d_counters, 0, kNumCounters * sizeof(unsigned int)) != hipSuccess ||
-        hipMemset(c->d_slots, 0, kNumSlots * sizeof(unsigned long long)) != hipSuccess ||
+        hipMemset(c->d_slots, 0, kNumSlots * kSlotStride * sizeof(unsigned long long)) != hipSuccess ||
         hipMemset(c->d_params, 0, 64 * sizeof(int)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
       rc = IE_ERR_HIP;

@@ -255,11 +255,15 @@ struct Context {
   size_t gemm_ws_bytes = 0;
 };
 
-constexpr int kNumCounters = 256;
+// Per-row reduction state sits one 128-byte line apart: device-scope atomics on one line
+// serialise (the bs=16 argmax, 64 workgroups per row, took 15.5 us with the 16 rows' slots and
+// counters on 3 lines, 5.4 us with a line per row).
+constexpr int kSlotStride = 16;  // 64-bit slots per row
+constexpr int kCntStride = 32;   // 32-bit counters per row
 constexpr int kNumSlots = 64;
 // Counter bank offsets.
-constexpr int kCntAttn = 0;      // [kKVHeads * 16] decode attention (per batch row x kv head)
-constexpr int kCntArgmax = 192;  // [64] argmax rows
+constexpr int kCntArgmax = 0;  // [64][kCntStride] argmax rows
+constexpr int kNumCounters = kCntArgmax + kNumSlots * kCntStride;
 
 inline hipStream_t stream_of(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

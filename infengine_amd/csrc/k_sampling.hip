@@ -95,9 +95,20 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int vo
   const int beg = blockIdx.x * chunk;
   const int end = min(vocab, beg + chunk);
   unsigned long long best = 0ull;
-  for (int i = beg + tid; i < end; i += 256) {
-    const unsigned long long k = argmax_key(L[i], (unsigned)i);
-    best = k > best ? k : best;
+  // 8 loads in flight per thread per round (a chunk of the 128256-entry vocabulary is one
+  // round): indices past the chunk load its last element and count as key 0
+  for (int i0 = beg + tid; i0 < end; i0 += 8 * 256) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = L[min(i0 + u * 256, end - 1)];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * 256;
+      // (masked arithmetically: a select let the compiler move a load under a branch)
+      const unsigned long long k =
+          argmax_key(v[u], (unsigned)i) & (0ull - (unsigned long long)(i < end));
+      best = k > best ? k : best;
+    }
   }
   best = wave_max_u64(best);
   if (lane == 0) red[wave] = best;
@@ -108,13 +119,15 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int vo
     // Device-scope atomics on one address are coherent across the XCDs; waiting for the max
     // to be performed before counting in orders the two, so the workgroup that counts last
     // exchanges out the final max.  (No __threadfence: on this part it writes back the L2.)
-    atomicMax(&slots[row], b);
+    unsigned long long* slot = slots + row * kSlotStride;
+    unsigned int* counter = counters + row * kCntStride;
+    atomicMax(slot, b);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (atomicAdd(&counters[row], 1u) == gridDim.x - 1) {
-      const unsigned long long fin = atomicExch(&slots[row], 0ull);
+    if (atomicAdd(counter, 1u) == gridDim.x - 1) {
+      const unsigned long long fin = atomicExch(slot, 0ull);
       const int tok = (int)(0xFFFFFFFFu - (unsigned)(fin & 0xFFFFFFFFull));
       out[row] = tok;
-      atomicExch(&counters[row], 0u);
+      atomicExch(counter, 0u);
       if (row == 0) {
         if (tail.host_tok)
           __hip_atomic_store(tail.host_tok, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
