@@ -25,7 +25,11 @@ __global__ __launch_bounds__(256) void emblookup_kernel(const int* ids, const ui
     return;
   }
   const uint4* src = reinterpret_cast<const uint4*>(table + (size_t)id * kHidden);
-  for (int i = threadIdx.x; i < kHidden / 8; i += 256) dst[i] = src[i];
+  // both loads before either store (the compiler cannot tell the row from the output apart)
+  static_assert(kHidden / 8 == 2 * 256, "two 16-byte chunks per thread");
+  const uint4 a = src[threadIdx.x], b = src[threadIdx.x + 256];
+  dst[threadIdx.x] = a;
+  dst[threadIdx.x + 256] = b;
 }
 
 // ---------------------------------------------------------------- rmsnorm
@@ -37,11 +41,16 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const u
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint4* x4 = reinterpret_cast<const uint4*>(x + (size_t)row * kHidden);
   const uint4* w4 = reinterpret_cast<const uint4*>(w);
-  uint4 v[2];
-  float ss = 0.f;
+  uint4 v[2], wv[2];
+  // every load up front (the weight's with the row's): one memory latency, not two
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     v[k] = x4[tid + k * 256];
+    wv[k] = w4[tid + k * 256];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
     const uint32_t e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -56,9 +65,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const u
   uint4* o4 = reinterpret_cast<uint4*>(out + (size_t)row * kHidden);
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
-    const uint4 wv = w4[tid + k * 256];
     const uint32_t e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-    const uint32_t f[4] = {wv.x, wv.y, wv.z, wv.w};
+    const uint32_t f[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
     uint32_t o[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
