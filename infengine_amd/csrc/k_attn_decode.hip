@@ -51,26 +51,36 @@ static_assert(kMaxLongCtx / kAttnTile <= 64 * kAttnSplits * 4, "page ids per wav
 
 // Phase 1: split s of (batch b, kv head g) attends its run of tiles (its NW waves take every
 // NW-th tile) and writes the unnormalised partial (m, l, o) of each of the 4 q heads; with one
-// split (max_splits = 1, batched, NW = 8) it writes the normalised bf16 output instead.  VREG: one
-// 16 KiB LDS slice per wave, K through it and V staged in registers then written over K (72 KiB
-// of LDS per 4-wave workgroup, two workgroups per CU: the batched grid; 144 KiB for the 8-wave
-// form); otherwise K and V each have a slice (136 KiB, one workgroup per CU; 0.7% faster per
-// decode step at batch 1 than K fragments loaded straight into registers).
-template <bool VREG, int NW>
+// split (max_splits = 1, batched: 12 waves on 32-key tiles) it writes the normalised bf16 output
+// instead.  VREG: one LDS slice per wave, K through it and V staged in registers then written over
+// K (72 KiB per 4-wave workgroup of 64-key tiles, two workgroups per CU: the batched split grid;
+// 120 KiB for the 12-wave form); otherwise K and V each have a slice (136 KiB, one workgroup per
+// CU; 0.7% faster per decode step at batch 1 than K fragments loaded straight into registers).
+// The batched one-split form takes 32-key tiles so that 12 waves (3 per SIMD within the registers)
+// cover a context of 17-24 half tiles in two rounds of half the work: 10.6 against 11.8 us per
+// layer for 8 waves on 64-key tiles at bs = 16, S = 517-564, where one wave's ninth full tile
+// ended each workgroup ~3 us after the others.
+template <bool VREG, int NW, int KT = kAttnTile>
 __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodeParams p) {
+  // KT: keys per tile, 64 or 32 (half tiles: twice the waves on a context's tiles; a page
+  // holds two)
+  static_assert(KT == 64 || KT == 32, "tile of 64 or 32 keys");
+  constexpr int KB = KT / 16;   // 16-key MFMA blocks per tile
+  constexpr int KS2 = KT / 32;  // 32-key P.V contraction chunks per tile
+  constexpr int NJ = KT / 4;    // 1 KiB loads per tile (4 rows each)
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   // wave id made provably uniform: the tile indices and buffer descriptors derived from it stay
   // in SGPRs (otherwise every buffer load becomes a readfirstlane loop)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int fr = lane & 15, G = lane >> 4;
   const int S = p.d_seq_len ? p.d_seq_len[b] : p.seq_len;
-  const int ntiles = (S + kAttnTile - 1) / kAttnTile;
-  const int ns = attn_decode_splits(ntiles, p.max_splits);
+  const int ntiles = (S + KT - 1) / KT;
+  const int ns = KT == kAttnTile ? attn_decode_splits(ntiles, p.max_splits) : 1;
   if (split >= ns) return;  // whole workgroup: nobody reads a partial past ns
   const int tps = (ntiles + ns - 1) / ns;
   const int t0 = split * tps, t1 = min(ntiles, t0 + tps);
 
-  __shared__ u32x4_t kvlds[NW][VREG ? 1 : 2][kTC];  // per wave: K tile (then V over it), V tile
+  __shared__ u32x4_t kvlds[NW][VREG ? 1 : 2][KT * 16];  // per wave: K tile (then V over it), V tile
   __shared__ float xo[NW][kGQA][kHeadDim];
   __shared__ float xml[NW][kGQA][2];
   const uint16_t* Kh = p.k_cache + (size_t)b * p.cache_batch_stride + (size_t)g * kKVPlane;
@@ -106,11 +116,11 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
   int page_of = 0;
   if (paged) {
     const int t = t0 + wave + NW * lane;
-    page_of = t < t1 ? p.block_table[(size_t)b * p.table_stride + t] : -1;
+    page_of = t < t1 ? p.block_table[(size_t)b * p.table_stride + t * KT / kAttnTile] : -1;
   }
   int it = 0;
   for (int t = t0 + wave; t < t1; t += NW, ++it) {
-    const int key0 = t * kAttnTile;
+    const int key0 = t * KT;
     // the tile's buffers: rows key0.. of the sequence's cache, or rows 0.. of its page (a page
     // id outside the pool reads as zero)
     __amdgpu_buffer_rsrc_t krs = krs_seq, vrs = vrs_seq;
@@ -119,21 +129,21 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
       const int page = __builtin_amdgcn_readlane(page_of, it);
       const bool ok = page >= 0 && page < p.n_pages;
       const size_t base = (size_t)(ok ? page : 0) * kPageElems + (size_t)g * kPageHead;
-      const int bytes = ok ? min(kAttnTile, S - key0) * kRowBytes : 0;
+      kr0 = key0 % kAttnTile;  // the tile's first row in its page
+      const int bytes = ok ? min(kAttnTile, S - (key0 - kr0)) * kRowBytes : 0;
       krs = __builtin_amdgcn_make_buffer_rsrc((void*)(p.k_cache + base), 0, bytes, kBufferFlags);
       vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(p.v_cache + base), 0, bytes, kBufferFlags);
-      kr0 = 0;
     }
     // Tile to LDS: load j fills rows 4j .. 4j+3; lane fills slot lane%16 of row 4j + lane/16
     // with global chunk (lane%16) ^ (row & 15).  The wave only reads its own slice, so its own
-    // vmcnt wait is the whole synchronisation.  VREG (the 8-wave form, one 16 KiB slice per
+    // vmcnt wait is the whole synchronisation.  VREG (the batched forms, one slice per
     // wave): K goes through the slice by direct-to-LDS loads while V is loaded into registers,
     // row-contiguous, and written over K once the K fragments are in registers.  (Loading the
     // K fragments straight from memory instead reads 64-byte pieces of 16 rows per lane
     // quad and issued ~3x slower than row-contiguous loads.)
-    u32x4_t vv[16];
+    u32x4_t vv[NJ];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int r = 4 * j + G;
       const uint32_t off = (uint32_t)((kr0 + r) * kRowBytes + ((fr ^ (r & 15)) * 16));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)&kt[64 * j], 16, off, 0, 0, 0);
@@ -142,22 +152,22 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
     }
     if constexpr (VREG) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
+      for (int j = 0; j < NJ; ++j)
         vv[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
             vrs, (uint32_t)((kr0 + 4 * j + G) * kRowBytes + fr * 16), 0, 0));
     }
     // K fragments kk[kb][ks] = K[key0 + 16 kb + fr][32 ks + 8 G .. +8] from the LDS tile
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VREG ? 16 : 0) : "memory");
-    u32x4_t kk[4][4];
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VREG ? NJ : 0) : "memory");
+    u32x4_t kk[KB][4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) kk[kb][ks] = kt[kv_slot(16 * kb + fr, 4 * ks + G)];
 
     // ---- S^T blocks: s[kb][r] = S[q head 4g + fr][key key0 + 16 kb + 4 G + r]
-    f32x4_t s[4];
+    f32x4_t s[KB];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       s[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
@@ -167,7 +177,7 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
     // ---- online softmax per q column (spread over lanes fr, fr+16, fr+32, fr+48)
     float mt = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = key0 + 16 * kb + 4 * G + r;
@@ -180,7 +190,7 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
     const float alpha = __expf(m - mn);
     float ls = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float e = __expf(s[kb][r] - mn);
@@ -193,9 +203,9 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
     for (int db = 0; db < 8; ++db) o[db] *= alpha;
     // P^T fragments: slot 8 G + r <-> key 32 ks2 + 4 G + r, slot 8 G + 4 + r <-> key
     // 32 ks2 + 16 + 4 G + r
-    bf16x8_t pb[2];
+    bf16x8_t pb[KS2];
 #pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
+    for (int ks2 = 0; ks2 < KS2; ++ks2) {
       const u32x4_t w = {pack_bf2(s[2 * ks2][0], s[2 * ks2][1]), pack_bf2(s[2 * ks2][2], s[2 * ks2][3]),
                          pack_bf2(s[2 * ks2 + 1][0], s[2 * ks2 + 1][1]),
                          pack_bf2(s[2 * ks2 + 1][2], s[2 * ks2 + 1][3])};
@@ -208,14 +218,14 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
       // every K fragment read has returned (the MFMAs above consumed them): V over K
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-      for (int j = 0; j < 16; ++j) vt[kv_slot(4 * j + G, fr)] = vv[j];
+      for (int j = 0; j < NJ; ++j) vt[kv_slot(4 * j + G, fr)] = vv[j];
     }
     const int kr = fr >> 2, dq = fr & 3;
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       const int c = 2 * db + (dq >> 1), hb = (dq & 1) * 8;
 #pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2) {
+      for (int ks2 = 0; ks2 < KS2; ++ks2) {
         const int ka = 32 * ks2 + 4 * G + kr;
         const char* va = reinterpret_cast<const char*>(&vt[kv_slot(ka, c)]) + hb;
         const char* vb = reinterpret_cast<const char*>(&vt[kv_slot(ka + 16, c)]) + hb;
@@ -243,7 +253,7 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
     }
   }
   __syncthreads();
-  if (wave >= kGQA) return;  // (NW = 8) waves past the 4 q heads only contribute partials
+  if (wave >= kGQA) return;  // (NW > 4) waves past the 4 q heads only contribute partials
   const int h = wave;  // wave h merges q head 4g + h; lane d owns dims 2d, 2d+1
   const float mw = lane < NW ? xml[lane][h][0] : -INFINITY;
   const float lw = lane < NW ? xml[lane][h][1] : 0.f;
@@ -325,9 +335,9 @@ int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStre
   IE_REQUIRE(p.max_splits > 1 || (merge && p.out), "attn_decode: one split writes the output");
   // one workgroup per possible split: idle ones would still cost dispatch (at batch 16 and
   // 32 splits, 4096 mostly empty workgroups took 52 us)
-  if (p.max_splits == 1)  // one workgroup per (sequence, kv head): 8 waves share its tiles
-    hipLaunchKernelGGL((attn_decode_split_kernel<true, 8>), dim3(1, kKVHeads, batch), dim3(8 * 64), 0,
-                       st, p);
+  if (p.max_splits == 1)  // one workgroup per (sequence, kv head): 12 waves share its tiles
+    hipLaunchKernelGGL((attn_decode_split_kernel<true, 12, 32>), dim3(1, kKVHeads, batch),
+                       dim3(12 * 64), 0, st, p);
   else if (batch > 1)
     hipLaunchKernelGGL((attn_decode_split_kernel<true, kSplitWaves>),
                        dim3(p.max_splits, kKVHeads, batch), dim3(kSplitWaves * 64), 0, st, p);
