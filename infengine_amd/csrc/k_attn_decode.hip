@@ -6,19 +6,21 @@
 // sqrt(128)) . V for all 32 q heads runs as split-context ("flash decoding")
 // attention on MFMA:
 //
-//   grid  = (max_splits, 8 kv heads, batch), block = 4 waves
-//   split s of kv head g owns a contiguous run of 64-key tiles of the context 0..S-1 (four
-//   tiles per split, one per wave, while the split cap allows); a wave stages its tile's K
-//   and V rows in LDS (K by direct-to-LDS loads; V likewise at batch 1, through registers in
-//   the batched forms), and computes, with
+//   grid  = (max_splits, 8 kv heads, batch), block = NW waves
+//   split s of kv head g owns a contiguous run of the context 0..S-1 (at most 256 positions,
+//   while the split cap allows), cut into tiles of 64 or 32 keys that its waves take in turn
+//   (batch 1: 8 waves on 32-key tiles; batched: 12 waves on 32-key tiles for one split per
+//   sequence, 4 on 64-key tiles for several); a wave stages its tile's K and V rows in LDS (K by
+//   direct-to-LDS loads; V likewise at batch 1, through registers in the batched forms), and
+//   computes, with
 //   v_mfma_f32_16x16x32_bf16, S^T = K . Q^T for the 4 GQA q heads of the kv head (GQA: q head h
 //   reads kv head h/4, attn.cu:51-53) as 4 of the 16 MFMA columns, an online softmax per head,
 //   and O^T += V^T . P^T with P^T taken straight from the S^T accumulators and V^T read with
-//   ds_read_b64_tr_b16, as in the prefill kernel.  The 4 waves are merged in LDS and the split
+//   ds_read_b64_tr_b16, as in the prefill kernel.  The waves are merged in LDS and the split
 //   writes one partial (m, l, o) per q head.
 //
 // The partials of the ns splits are merged either by the O projection itself (its
-// input-staging prologue reads them; decode with max_splits = 8, no extra launch)
+// input-staging prologue reads them; decode with max_splits = 4, no extra launch)
 // or by a small merge kernel writing bf16 [h][128] (attn.cu:433-438) for the
 // batched GEMM path and long contexts (max_splits = 32).  A device-scope "last
 // workgroup merges" scheme is not used: its fence (L2 write-back / invalidate on
@@ -59,7 +61,9 @@ static_assert(kMaxLongCtx / kAttnTile <= 64 * kAttnSplits * 4, "page ids per wav
 // The batched one-split form takes 32-key tiles so that 12 waves (3 per SIMD within the registers)
 // cover a context of 17-24 half tiles in two rounds of half the work: 10.6 against 11.8 us per
 // layer for 8 waves on 64-key tiles at bs = 16, S = 517-564, where one wave's ninth full tile
-// ended each workgroup ~3 us after the others.
+// ended each workgroup ~3 us after the others.  The batch-1 split form likewise runs 8 waves on
+// 32-key tiles (the same tiles per split, half the work per wave): 4.85 against 5.07 us at
+// S = 550-610.  Splits are counted in 64-key tiles whatever the tile, as the merge counts them.
 template <bool VREG, int NW, int KT = kAttnTile>
 __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodeParams p) {
   // KT: keys per tile, 64 or 32 (half tiles: twice the waves on a context's tiles; a page
@@ -75,7 +79,8 @@ __global__ __launch_bounds__(NW * 64) void attn_decode_split_kernel(AttnDecodePa
   const int fr = lane & 15, G = lane >> 4;
   const int S = p.d_seq_len ? p.d_seq_len[b] : p.seq_len;
   const int ntiles = (S + KT - 1) / KT;
-  const int ns = KT == kAttnTile ? attn_decode_splits(ntiles, p.max_splits) : 1;
+  // (split count in 64-key tiles whatever KT: the merge and the O projection count the same)
+  const int ns = attn_decode_splits((S + kAttnTile - 1) / kAttnTile, p.max_splits);
   if (split >= ns) return;  // whole workgroup: nobody reads a partial past ns
   const int tps = (ntiles + ns - 1) / ns;
   const int t0 = split * tps, t1 = min(ntiles, t0 + tps);
@@ -342,8 +347,8 @@ int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStre
     hipLaunchKernelGGL((attn_decode_split_kernel<true, kSplitWaves>),
                        dim3(p.max_splits, kKVHeads, batch), dim3(kSplitWaves * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((attn_decode_split_kernel<false, kSplitWaves>),
-                       dim3(p.max_splits, kKVHeads, batch), dim3(kSplitWaves * 64), 0, st, p);
+    hipLaunchKernelGGL((attn_decode_split_kernel<false, 8, 32>), dim3(p.max_splits, kKVHeads, batch),
+                       dim3(8 * 64), 0, st, p);
   IE_CHECK_LAUNCH();
   if (merge && p.max_splits > 1) {
     IE_REQUIRE(p.out, "attn_decode: merge needs an output buffer");
