@@ -42,13 +42,15 @@ struct DecodeWs {
   float* part_ml;
   uint16_t* xn;     // [batch][4096]   final-RMSNorm rows for the lm_head (batched path)
   float* ss;        // [256][16]       partial sums of squares of those rows (batched path)
+  float* sk_part;   // the skinny GEMM's K-half partials (batched path)
 };
 
 
 size_t decode_ws_bytes(int batch) {
   return align256((size_t)batch * kHidden * 2) + align256((size_t)batch * kFFN * 2) +
          align256((size_t)batch * kHidden * 2) + align256(attn_decode_partials_bytes(batch)) +
-         align256((size_t)batch * kHidden * 2) + align256((size_t)kNormParts * 16 * sizeof(float));
+         align256((size_t)batch * kHidden * 2) + align256((size_t)kNormParts * 16 * sizeof(float)) +
+         align256(kSkPartBytes);
 }
 
 DecodeWs decode_ws(void* ws, int batch) {
@@ -67,6 +69,8 @@ DecodeWs decode_ws(void* ws, int batch) {
   d.xn = reinterpret_cast<uint16_t*>(p);
   p += align256((size_t)batch * kHidden * 2);
   d.ss = reinterpret_cast<float*>(p);
+  p += align256((size_t)kNormParts * 16 * sizeof(float));
+  d.sk_part = reinterpret_cast<float*>(p);
   return d;
 }
 
@@ -722,6 +726,9 @@ int enqueue_batched(Context* c, hipStream_t st, const ie_model_weights& W, int b
     g.ss_in = w.ss;
     g.ss_parts = kNormParts;
     g.x_norm_w = L.input_layernorm;
+    g.sk_tail = gemm_skinny_tail(kQKVDim);
+    g.sk_part = w.sk_part;
+    g.sk_cnt = c->d_counters + kCntSkinny;
     IE_TRY(launch_gemm(kGemmQkvRope, g, st));
     IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, len_class, batch, cstride, true, st,
                        block_table, table_stride, n_pages, true));
@@ -748,6 +755,9 @@ int enqueue_batched(Context* c, hipStream_t st, const ie_model_weights& W, int b
     gu.ss_in = w.ss;
     gu.ss_parts = kNormParts;
     gu.x_norm_w = L.post_attention_layernorm;
+    gu.sk_tail = gemm_skinny_tail(kFFN);
+    gu.sk_part = w.sk_part;
+    gu.sk_cnt = c->d_counters + kCntSkinny;
     IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
     GemmParams dn{};
     dn.x = w.h;

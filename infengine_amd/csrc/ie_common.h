@@ -263,7 +263,11 @@ constexpr int kCntStride = 32;   // 32-bit counters per row
 constexpr int kNumSlots = 64;
 // Counter bank offsets.
 constexpr int kCntArgmax = 0;  // [64][kCntStride] argmax rows
-constexpr int kNumCounters = kCntArgmax + kNumSlots * kCntStride;
+// The skinny GEMM's split tail tiles: one arrival counter per tile (two K halves), at most
+// kSkTailMax tiles per launch.
+constexpr int kSkTailMax = 256;
+constexpr int kCntSkinny = kCntArgmax + kNumSlots * kCntStride;  // [kSkTailMax][kCntStride]
+constexpr int kNumCounters = kCntSkinny + kSkTailMax * kCntStride;
 
 inline hipStream_t stream_of(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -175,7 +175,16 @@ struct GemmParams {
   float* split_ws;
   long long split_ws_bytes;
   int k_splits;  // set by the launcher for the wide kernel (0 / 1: no split)
+  // Skinny GEMM (SwiGLU / QKV + RoPE epilogues): the last sk_tail of the N / 16 tiles run as two
+  // workgroups each, one per K half, so that every CU gets the same share of the weight stream
+  // (gemm_skinny_tail gives the count).  sk_part: fp32 partials [sk_tail][2][2][64][4];
+  // sk_cnt: one zeroed arrival counter per tile, kCntStride apart (reset by the tile's finisher).
+  float* sk_part;
+  unsigned int* sk_cnt;
+  int sk_tail;
 };
+// Bytes of sk_part for up to kSkTailMax split tiles.
+constexpr size_t kSkPartBytes = (size_t)kSkTailMax * 2 * 2 * 64 * 4 * sizeof(float);
 constexpr int kSplitMaxRows = 1024;
 // Scratch bytes split K may use for an M-row product with n output columns (SwiGLU: 2 x the
 // output columns): 2048 partial rows, i.e. up to 16 planes at M <= 128, 4 at M = 512.
@@ -196,6 +205,9 @@ int load_safetensors(ie_model_weights* out, const char* const* paths, int n_path
 // M <= 16 streaming variant (batched decode); launch_gemm routes to it when it fits.
 bool gemm_skinny_fits(const GemmParams& p);
 int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st);
+// Tiles of an N-column skinny product to split in K halves (the part of the last round of
+// tiles that would leave CUs idle), 0 for none.
+int gemm_skinny_tail(int N);
 // 16 < M <= 48 (short prompts): the streaming kernel over 2-3 X row-blocks
 bool gemm_skinny_mb_fits(int epi, const GemmParams& p);
 int launch_gemm_skinny_mb(int epi, const GemmParams& p, hipStream_t st);

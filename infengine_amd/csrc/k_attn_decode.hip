@@ -38,7 +38,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) short4_t lds_short4;
 
 constexpr int kSplitWaves = 4;
-constexpr int kTC = kAttnTile * 16;        // 16-byte chunks of one K (or V) tile
 constexpr int kRowBytes = kHeadDim * 2;
 constexpr int kBufferFlags = 0x00020000;   // buffer descriptor word 3 (raw 32-bit access)
 static_assert(kAttnTile == 64, "tile = 4 x 16-key MFMA blocks");

@@ -6,7 +6,10 @@
 // a workgroup owns 16 weight rows (output columns) and its 4 waves split K in quarters; each
 // wave runs v_mfma_f32_16x16x32_bf16 with the 16 weight rows as A and the (up to) 16 X rows
 // as B, and the quarters are summed through LDS.  Grid = N / 16 workgroups (256 for N = 4096,
-// 8016 for the lm_head), enough to fill the chip where a 128-row tile GEMM had 32.
+// 8016 for the lm_head), enough to fill the chip where a 128-row tile GEMM had 32.  The SwiGLU
+// and QKV projections (896 and 384 tiles: 3.5 and 1.5 per CU) run their last partial round of
+// tiles as two workgroups each, one per K half, so that every CU streams the same share; the
+// second half to finish adds the first's fp32 partials and stores the tile (no waiting).
 //
 // Load pattern: a step covers 128 k (256 bytes of each of the tile's 16 weight rows) as 4 MFMA
 // k-chunks of 32.  The MFMA operand layout (lane l: row l % 16, 8 k at 8 (l / 16)) would make
@@ -48,6 +51,7 @@ constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw 32-bi
 struct SkSrc {
   __amdgpu_buffer_rsrc_t w[2];  // the W tiles: the weight rows, or gate and up rows
   __amdgpu_buffer_rsrc_t x;
+  __amdgpu_buffer_rsrc_t nul;   // an empty range: loads through it read zeros and no memory
   uint32_t wo[4], xo[4];
 };
 
@@ -63,21 +67,29 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const uint16_t* base, 
 // (r, q) loads 16-byte chunk r of row 4j + q of each W tile, or of the X rows.  The weights are
 // read exactly once per launch: nontemporal loads (cache policy nt), as the GEMV's; measured 8-10%
 // faster per projection than the default policy (the X rows, re-read by every workgroup, keep it).
+// live = false reads through the empty range instead (a uniform select, not a branch: a load
+// under a run-time condition makes the compiler wait for every load in flight where the paths
+// join).
 template <int NT>
-__device__ __forceinline__ void sk_load_w(const SkSrc& src, int ks, u32x4_t (&w)[NT][4]) {
+__device__ __forceinline__ void sk_load_w(const SkSrc& src, int ks, u32x4_t (&w)[NT][4],
+                                          bool live = true) {
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < NT; ++t) {
+    const __amdgpu_buffer_rsrc_t rs = live ? src.w[t] : src.nul;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       w[t][j] = __builtin_bit_cast(
-          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src.w[t], src.wo[j], 2 * ks, 2));
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, src.wo[j], 2 * ks, 2));
+  }
 }
 
-__device__ __forceinline__ void sk_load_x(const SkSrc& src, int ks, u32x4_t (&xv)[4]) {
+__device__ __forceinline__ void sk_load_x(const SkSrc& src, int ks, u32x4_t (&xv)[4],
+                                          bool live = true) {
+  const __amdgpu_buffer_rsrc_t rs = live ? src.x : src.nul;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     xv[j] = __builtin_bit_cast(
-        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(src.x, src.xo[j], 2 * ks, 0));
+        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, src.xo[j], 2 * ks, 0));
 }
 
 // One 16-row tile into a wave's LDS tile: row R's 16-byte chunk c goes to slot R*16 + (c ^ R).
@@ -124,13 +136,16 @@ __device__ __forceinline__ void sk_norm_x(u32x4_t (&xv)[4], const SkNorm& nm) {
 template <int NT, bool NORM>
 __device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const SkSrc& src, u32x4_t (&w)[NT][4],
                                         u32x4_t (&xv)[4], int r, int q, f32x4_t (&acc)[NT],
-                                        bool lx, int kx, bool lw, int kw, SkNorm& nm) {
+                                        bool lx, int kx, bool lw, int kw, SkNorm& nm,
+                                        bool xlive = true, bool wlive = true) {
   sk_put(tr[0], w[0], r, q);
   if constexpr (NORM) sk_norm_x(xv, nm);
   sk_put(tr[1], xv, r, q);
   if (lx) {
-    sk_load_x(src, kx, xv);
-    if constexpr (NORM) nm.nw = sk_load_nw(nm.w, kx, r);
+    // (a step that is not live reads X through the empty range and re-reads the start of the
+    // norm weight, a plain array)
+    sk_load_x(src, kx, xv, xlive);
+    if constexpr (NORM) nm.nw = sk_load_nw(nm.w, xlive ? kx : 0, r);
   }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -141,22 +156,23 @@ __device__ __forceinline__ void sk_step(u32x4_t (*tr)[256], const SkSrc& src, u3
           __builtin_bit_cast(bf16x8_t, tr[0][r * 16 + ((4 * c + q) ^ r)]),
           __builtin_bit_cast(bf16x8_t, tr[1][r * 16 + ((4 * c + q) ^ r)]), acc[t], 0, 0, 0);
   }
-  if (lw) sk_load_w<NT>(src, kw, w);
+  if (lw) sk_load_w<NT>(src, kw, w, wlive);
 }
 
 // Steps s and s+1 from the two W register buffers, each refilled with the step two ahead; X
 // one step ahead.
+// (loads are issued for the steps below `steps`, and read memory for those below `live`)
 template <int NT, bool NORM>
 __device__ __forceinline__ void sk_pair(u32x4_t (*tr)[256], const SkSrc& src, int kbase, int s,
                                         int steps, int r, int q, u32x4_t (&w0)[NT][4],
                                         u32x4_t (&w1)[NT][4], u32x4_t (&xv)[4],
-                                        f32x4_t (&acc)[NT], SkNorm& nm) {
+                                        f32x4_t (&acc)[NT], SkNorm& nm, int live) {
   const int k1 = kbase + (s + 1) * kSkStep;
   sk_step<NT, NORM>(tr, src, w0, xv, r, q, acc, s + 1 < steps, k1, s + 2 < steps, k1 + kSkStep,
-                    nm);
+                    nm, s + 1 < live, s + 2 < live);
   __builtin_amdgcn_sched_barrier(0);
   sk_step<NT, NORM>(tr, src, w1, xv, r, q, acc, s + 2 < steps, k1 + kSkStep, s + 3 < steps,
-                    k1 + 2 * kSkStep, nm);
+                    k1 + 2 * kSkStep, nm, s + 2 < live, s + 3 < live);
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -176,7 +192,16 @@ void gemm_skinny_kernel(GemmParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
-  const int n0 = blockIdx.x * kSkRows;
+  // tiles 0 .. tfull-1 are one workgroup each; each of the p.sk_tail tiles after them is two,
+  // K half 0 then K half 1 (the second to arrive sums the halves and runs the epilogue)
+  constexpr bool TAIL = KC > 0 && (SW || EPI == kGemmQkvRope);  // (the launcher checks sk_tail)
+  const int tfull = gridDim.x - 2 * p.sk_tail;
+  int tile = blockIdx.x, half = -1;
+  if (TAIL && (int)blockIdx.x >= tfull) {
+    tile = tfull + ((blockIdx.x - tfull) >> 1);
+    half = (blockIdx.x - tfull) & 1;
+  }
+  const int n0 = tile * kSkRows;
   const int K = KC > 0 ? KC : p.K;
 
   SkSrc src;
@@ -185,7 +210,7 @@ void gemm_skinny_kernel(GemmParams p) {
   if constexpr (EPI == kGemmQkvRope) {
     // head b / 8 of the [q|k|v] rows; the tile's rows are pairs 8 (b % 8) .. +7, first halves
     // (rows 0..7) then second halves (rows 8..15, 64 rows further on)
-    const int head = blockIdx.x >> 3, pr = (blockIdx.x & 7) * 8;
+    const int head = tile >> 3, pr = (tile & 7) * 8;
     const uint16_t* base = head < kQHeads ? p.w0 + (size_t)head * kHeadDim * K
                            : head < kQHeads + kKVHeads
                                ? p.w1 + (size_t)(head - kQHeads) * kHeadDim * K
@@ -215,6 +240,7 @@ void gemm_skinny_kernel(GemmParams p) {
     for (int j = 0; j < 4; ++j) wrow[j] = 4 * j + q;
   }
   src.x = sk_rsrc(p.x, p.M, K);
+  src.nul = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, 0, 0, kBufferFlags);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     src.wo[j] = (uint32_t)(wrow[j] * K + 8 * r) * 2u;
@@ -226,8 +252,8 @@ void gemm_skinny_kernel(GemmParams p) {
   asm volatile("" : "+v"(src.xo[0]), "+v"(src.xo[1]), "+v"(src.xo[2]), "+v"(src.xo[3]));
   // wave w takes K quarter w (interleaving the waves' steps, so that the 4 waves read 1 KiB runs
   // of each row together, measured 4-6% slower)
-  const int kq = K / kSkSplit;
-  const int kbase = wave * kq;
+  const int kq = half < 0 ? K / kSkSplit : K / (2 * kSkSplit);
+  const int kbase = (half < 0 ? 0 : half * (K / 2)) + wave * kq;
   const int steps = kq / kSkStep;
 
   f32x4_t acc[NT];
@@ -268,12 +294,12 @@ void gemm_skinny_kernel(GemmParams p) {
     nm.w = p.x_norm_w;
     nm.nw = sk_load_nw(nm.w, kbase, r);
   }
-  if (steps > 1) sk_load_w<NT>(src, kbase + kSkStep, w1);
+  if (KC > 0 || steps > 1) sk_load_w<NT>(src, kbase + kSkStep, w1);
   float ecos[4], esin[4];
   int epage = 0;
   if constexpr (EPI == kGemmQkvRope) {
     epos -= 1;
-    const int jp = (blockIdx.x & 7) * 8 + 4 * (q & 1);
+    const int jp = (tile & 7) * 8 + 4 * (q & 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       ecos[i] = p.rope_cos[epos * 64 + jp + i];
@@ -297,13 +323,28 @@ void gemm_skinny_kernel(GemmParams p) {
     for (int j = 0; j < 4; ++j) nm.rr[j] = rsqrtf(ssr[4 * j + q] / (float)K + kRmsEps);
   }
   int s = 0;
-  if constexpr (KC > 0) {
+  if constexpr (KC > 0 && !TAIL) {
 #pragma unroll
     for (; s + 1 < KC / kSkSplit / kSkStep; s += 2)
-      sk_pair<NT, NORM>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc, nm);
+      sk_pair<NT, NORM>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc, nm, steps);
+  } else if constexpr (KC > 0) {
+    // steps of a whole tile; a K half runs the first FS / 2 (the same code, its lookahead loads
+    // past them switched off by the run-time step count)
+    constexpr int FS = KC / kSkSplit / kSkStep;
+    static_assert(FS % 4 == 0, "whole and half tiles run in step pairs");
+#pragma unroll
+    for (int s0 = 0; s0 < FS / 2; s0 += 2)
+      sk_pair<NT, NORM>(tr[wave], src, kbase, s0, FS, r, q, w0, w1, xv, acc, nm, steps);
+    s = FS / 2;
+    if (half < 0) {
+#pragma unroll
+      for (int s0 = FS / 2; s0 < FS; s0 += 2)
+        sk_pair<NT, NORM>(tr[wave], src, kbase, s0, FS, r, q, w0, w1, xv, acc, nm, FS);
+      s = FS;
+    }
   } else {
     for (; s + 1 < steps; s += 2)
-      sk_pair<NT, NORM>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc, nm);
+      sk_pair<NT, NORM>(tr[wave], src, kbase, s, steps, r, q, w0, w1, xv, acc, nm, steps);
   }
   if (s < steps) sk_step<NT, NORM>(tr[wave], src, w0, xv, r, q, acc, false, 0, false, 0, nm);
   f32x4_t acc0 = acc[0], acc1 = acc[NT - 1];
@@ -318,6 +359,37 @@ void gemm_skinny_kernel(GemmParams p) {
   for (int w = 1; w < kSkSplit; ++w) {
     acc0 += __builtin_bit_cast(f32x4_t, tr[w][0][lane]);
     if constexpr (SW) acc1 += __builtin_bit_cast(f32x4_t, tr[w][0][64 + lane]);
+  }
+  if constexpr (TAIL) {
+    if (half >= 0) {
+      // A K half: store this half's partials, then count the tile's arrivals; the second to
+      // arrive adds the other half's (a + b: the same sum whichever half arrives last) and
+      // stores the tile.  The halves may run on different XCDs, whose L2s are not coherent with
+      // each other: device-scope stores and loads, and the stores performed (vmcnt) before the
+      // count, which is a device-scope atomic.
+      float* const part = p.sk_part + (size_t)(tile - tfull) * (4 * 64 * 4);
+      float* const mine = part + half * (2 * 64 * 4) + 4 * lane;
+      const float* const other = part + (half ^ 1) * (2 * 64 * 4) + 4 * lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __hip_atomic_store(mine + i, acc0[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (SW)
+          __hip_atomic_store(mine + 256 + i, acc1[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      unsigned int* const cnt = p.sk_cnt + (size_t)(tile - tfull) * kCntStride;
+      unsigned int prev = 0;
+      if (lane == 0) prev = atomicAdd(cnt, 1u);
+      if (__builtin_amdgcn_readfirstlane(prev) == 0) return;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc0[i] += __hip_atomic_load(other + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (SW)
+          acc1[i] +=
+              __hip_atomic_load(other + 256 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 
   const int m = r, n = n0 + 4 * q;
@@ -354,7 +426,7 @@ void gemm_skinny_kernel(GemmParams p) {
       b[i] = hi ? mine : other;
     }
     if (m >= p.M) return;
-    const int head = blockIdx.x >> 3, jp = (blockIdx.x & 7) * 8 + 4 * (q & 1);
+    const int head = tile >> 3, jp = (tile & 7) * 8 + 4 * (q & 1);
     const int pos = epos;
     float v[4];
 #pragma unroll
@@ -579,7 +651,7 @@ int launch_mb_e(const GemmParams& p, hipStream_t st) {
 
 template <int EPI, bool NORM>
 int launch_sn(const GemmParams& p, hipStream_t st) {
-  const int blocks = (p.N + kSkRows - 1) / kSkRows;
+  const int blocks = (p.N + kSkRows - 1) / kSkRows + p.sk_tail;
   if constexpr (EPI == kGemmQkvRope) {
     IE_REQUIRE(p.K == kHidden && p.N == kQKVDim && p.n0 == kHidden && p.n1 == kKVDim && p.y &&
                    p.k_cache && p.v_cache && p.d_seq_len && p.rope_cos && p.rope_sin,
@@ -622,6 +694,12 @@ int launch_s(const GemmParams& p, hipStream_t st) {
 
 }  // namespace
 
+int gemm_skinny_tail(int N) {
+  // 256 CUs: the tiles past the last whole round of 256
+  const int tiles = (N + kSkRows - 1) / kSkRows;
+  return tiles > 256 ? std::min(tiles % 256, kSkTailMax) : 0;
+}
+
 bool gemm_skinny_fits(const GemmParams& p) {
   return p.M >= 1 && p.M <= kSkRows && p.K % (kSkSplit * kSkStep) == 0;
 }
@@ -654,6 +732,14 @@ int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {
              kNormParts);
   IE_REQUIRE(!p.ss_out || (epi == kGemmResid && p.N % 16 == 0),
              "gemm_skinny: the sums-of-squares output is a residual-epilogue option");
+  IE_REQUIRE(p.sk_tail == 0 ||
+                 ((epi == kGemmSwiglu || epi == kGemmQkvRope) && p.sk_part && p.sk_cnt &&
+                  p.sk_tail > 0 && p.sk_tail <= kSkTailMax &&
+                  p.sk_tail <= (p.N + kSkRows - 1) / kSkRows &&
+                  (p.ss_in || epi == kGemmQkvRope || p.K == 4096 || p.K == 14336)),
+             "gemm_skinny: K-half tail tiles (sk_tail=%d) need the SwiGLU or QKV epilogue, K 4096 "
+             "or 14336, at most %d tiles, partials and counters",
+             p.sk_tail, kSkTailMax);
   switch (epi) {
     case kGemmSwiglu: return launch_s<kGemmSwiglu>(p, st);
     case kGemmQkvRope: return launch_s<kGemmQkvRope>(p, st);
