@@ -146,6 +146,61 @@ def test_multiply_by_weight_gemv(hip, ctx, k, n):
     assert_bf16_close(host(out), want, ulps=2, what="matmul")
 
 
+@pytest.mark.parametrize("waves,ppw", [(4, 1), (16, 1), (8, 3), (8, 7), (4, 5)])
+def test_gemv_tuning_knobs(hip, ctx, waves, ppw):
+    """The decode GEMV under forced waves per workgroup / row pairs per wave (the multi-pair loop
+    and the 4- and 16-wave instances; partial last waves at 3072 and 2048 pairs) computes the
+    default's values: bit-identical without RMSNorm (a pair's dot product does not depend on
+    where it runs), within tolerance of the oracle with it (the sum of squares is added over a
+    different number of waves)."""
+    say(f"gemv knobs waves={waves} pairs/wave={ppw}")
+    cases = [(14336, 4096), (4096, 6144)]
+    xs = {k: orc.synthetic((1, k), 21, k, 0.0, 1.0) for k, _ in cases}
+    ws = {(k, n): orc.synthetic((n, k), 21, n, 0.0, 0.02) for k, n in cases}
+
+    def run_plain():
+        outs = []
+        for k, n in cases:
+            out = bf16_empty(1, n)
+            hip.check(hip.lib.ie_multiply_by_weight(ctx.handle, 1, k, n, P(dev(xs[k])),
+                                                    P(dev(ws[(k, n)])), P(out)))
+            outs.append(out)
+        sync()
+        return [host(o) for o in outs]
+
+    wg, wu, wd = _ffn_weights(22)
+    x = orc.synthetic((1, H), 22, 10, 0.0, 1.0)
+    nw = orc.synthetic((H,), 22, 11, 1.0, 0.02)
+    wsp = torch.zeros(hip.lib.ie_ffn_workspace_size(1), dtype=torch.uint8, device="cuda")
+    dwg, dwu, dwd, dnw = dev(wg), dev(wu), dev(wd), dev(nw)
+
+    def run_ffn():
+        dx = dev(x)
+        hip.check(hip.lib.ie_ffn_block_decode(ctx.handle, P(dx), P(dnw), P(dwg), P(dwu), P(dwd),
+                                              P(wsp)))
+        sync()
+        return host(dx)
+
+    default = run_plain()
+    try:
+        hip.check(hip.lib.ie_tune_gemv_waves(waves))
+        hip.check(hip.lib.ie_tune_gemv_pairs_per_wave(ppw))
+        tuned = run_plain()
+        ffn = run_ffn()
+    finally:
+        hip.check(hip.lib.ie_tune_gemv_waves(0))
+        hip.check(hip.lib.ie_tune_gemv_pairs_per_wave(0))
+    for (k, n), a, b in zip(cases, default, tuned):
+        assert np.array_equal(a, b), f"gemv k={k} n={n} differs under waves={waves} ppw={ppw}"
+        assert_close(orc.bf16_to_f32(b), orc.bf16_to_f32(orc.matmul(xs[k], ws[(k, n)])),
+                     what=f"gemv k={k} n={n}")
+    want = orc.residual_add(x, orc.ffn(orc.rmsnorm(x, nw), wg, wu, wd))
+    assert_close(orc.bf16_to_f32(ffn), orc.bf16_to_f32(want), what="ffn block (tuned)")
+    assert_delta_close(x, ffn, want, what="ffn block delta (tuned)")
+    hip.check(hip.lib.ie_tune_gemv_waves(0))
+    assert np.array_equal(run_plain()[0], default[0]), "knobs reset"
+
+
 def test_lm_head_logits(hip, ctx):
     say("lm_head [1,4096] x [128256,4096] -> fp32")
     x = orc.synthetic((3, H), 10, 1, 0.0, 1.0)
