@@ -201,6 +201,55 @@ def test_gemv_tuning_knobs(hip, ctx, waves, ppw):
     assert np.array_equal(run_plain()[0], default[0]), "knobs reset"
 
 
+def test_rope_buffer_tables(hip, ctx):
+    """ie_init_rope_buffer (rope.cu:68-103; the [8192][64] tables continued by the same formula to
+    131072 rows) equals the oracle's tables bit for bit; ie_cleanup_rope_buffer frees them."""
+    from infengine_amd._lib import MAX_LONG_CONTEXT
+    from infengine_amd.engine import device_view
+    n = MAX_LONG_CONTEXT
+    say(f"init_rope_buffer [{n}][64] vs oracle")
+    cos, sin = C.c_void_p(), C.c_void_p()
+    hip.check(hip.lib.ie_init_rope_buffer(C.byref(cos), C.byref(sin)))
+    try:
+        want_cos, want_sin = orc.rope_tables(n)
+        sync()
+        assert torch.equal(device_view(cos.value, (n, 64), torch.float32).cpu(),
+                           torch.from_numpy(want_cos))
+        assert torch.equal(device_view(sin.value, (n, 64), torch.float32).cpu(),
+                           torch.from_numpy(want_sin))
+    finally:
+        hip.check(hip.lib.ie_cleanup_rope_buffer(cos, sin))
+
+
+def test_kv_cache_to_pages(hip, ctx):
+    """ie_kv_cache_to_pages: positions [37, 287) of every layer of a reference-layout cache
+    ([32][K|V][8][8192][128]) land in the pages the block table names ([page][32][K|V][8][64]
+    [128]), bit for bit; blocks whose id is outside the pool (-1, 9) are skipped and every
+    other page row keeps its contents."""
+    say("kv_cache_to_pages, 250 positions over 5 blocks")
+    Lr, KVH, MAXC, D, PP, n_pages = 32, 8, 8192, 128, 64, 6
+    g = torch.Generator(device="cuda").manual_seed(5)
+    cache = torch.randint(-32768, 32767, (Lr, 2, KVH, MAXC, D), dtype=torch.int16, device="cuda",
+                          generator=g)
+    pool = torch.randint(-32768, 32767, (n_pages, Lr, 2, KVH, PP, D), dtype=torch.int16,
+                         device="cuda", generator=g)
+    want = pool.clone()
+    tab = [3, -1, 0, 5, 1, 9]
+    table = torch.tensor(tab, dtype=torch.int32, device="cuda")
+    first, npos = 37, 250
+    hip.check(hip.lib.ie_kv_cache_to_pages(ctx.handle, P(cache), first, npos, P(pool), n_pages,
+                                           P(table)))
+    sync()
+    for blk in range(first // PP, (first + npos - 1) // PP + 1):
+        pg = tab[blk]
+        if not 0 <= pg < n_pages:
+            continue
+        lo, hi = max(first, blk * PP), min(first + npos, (blk + 1) * PP)
+        want[pg, :, :, :, lo - blk * PP:hi - blk * PP, :] = cache[:, :, :, lo:hi, :]
+    assert torch.equal(pool, want)
+    del cache
+
+
 def test_lm_head_logits(hip, ctx):
     say("lm_head [1,4096] x [128256,4096] -> fp32")
     x = orc.synthetic((3, H), 10, 1, 0.0, 1.0)
