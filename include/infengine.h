@@ -72,8 +72,8 @@ typedef struct ie_ffn_block_weights {
 } ie_ffn_block_weights;
 
 typedef struct ie_rope_weights {
-  float* cos; /* [131072, 64] fp32 (rows 0..8191: the reference's [8192, 64] table) */
-  float* sin; /* [131072, 64] fp32 */
+  float* cos; /* [rope_rows, 64] fp32 (rows 0..8191: the reference's [8192, 64] table) */
+  float* sin; /* [rope_rows, 64] fp32 */
 } ie_rope_weights;
 
 /* kernels/model_weights.cuh:11-19 */
@@ -86,7 +86,12 @@ typedef struct ie_layer {
 
 /* kernels/model_weights.cuh:21-34.  `storage` is the library-owned arena that
  * backs every pointer when the weights were made by ie_model_weights_random_init
- * or ie_model_weights_from_safetensors; NULL when the caller owns them. */
+ * or ie_model_weights_from_safetensors; NULL when the caller owns them.
+ * `rope_rows` (no reference counterpart) is the number of rows of rope.cos and
+ * rope.sin: 0 means IE_MAX_CONTEXT_LENGTH, the reference's 8192.  The library's
+ * constructors set IE_MAX_LONG_CONTEXT; a caller assembling its own weights with
+ * ie_init_rope_buffer's tables may set that too.  Every entry point refuses
+ * positions at or past it. */
 typedef struct ie_model_weights {
   ie_bf16* emb_lookup; /* [128256, 4096] */
   ie_layer layers[IE_NUM_LAYERS];
@@ -94,13 +99,16 @@ typedef struct ie_model_weights {
   ie_bf16* lm_head;    /* [128256, 4096] (untied) */
   ie_rope_weights rope;
   void* storage;
+  int rope_rows;
 } ie_model_weights;
 
 typedef struct ie_context ie_context;
 
 /* ---- context / errors (replaces cublasCreate/cublasDestroy, manager.cpp:58-59,107) ---- */
 /* stream: the hipStream_t every call on this context runs on; NULL means the
- * legacy default stream (the reference's implicit ordering). */
+ * legacy default stream (the reference's implicit ordering).  device: a device
+ * index, or IE_CURRENT_DEVICE for the calling thread's current device. */
+#define IE_CURRENT_DEVICE (-1)
 IE_API int ie_context_create(ie_context** out, int device, void* stream);
 IE_API int ie_context_destroy(ie_context* ctx);
 IE_API void* ie_context_stream(ie_context* ctx);
@@ -297,6 +305,25 @@ IE_API int ie_ffn_gate_up_decode(ie_context* ctx, const ie_bf16* d_x, const ie_b
 IE_API int ie_decoder_layer_decode(ie_context* ctx, const ie_model_weights* weights,
                                    int layer_idx, int seq_len, ie_bf16* d_x,
                                    ie_bf16* d_attn_out, void* workspace, void* kv_cache);
+/* One iteration of prefill.cu:17-38's layer loop: decoder layer layer_idx of ie_prefill over
+ * seq_len rows (positions 0 .. seq_len-1) of data_buffer [seq_len][4096], in place, writing
+ * that layer's K/V rows 0 .. seq_len-1 of kv_cache; aux/attn buffers and workspace
+ * (max(ie_attn_workspace_size, ie_ffn_workspace_size)(seq_len) bytes) as ie_prefill.
+ * ie_prefill is the embedding, these 32 calls, then final norm + lm_head on the last row and
+ * argmax, bit for bit. */
+IE_API int ie_decoder_layer_prefill(ie_context* ctx, const ie_model_weights* weights,
+                                    int layer_idx, int seq_len, ie_bf16* data_buffer,
+                                    ie_bf16* aux_buffer, ie_bf16* attn_buffer, void* workspace,
+                                    void* kv_cache);
+/* One decoder layer of ie_decode_step_batched (no reference counterpart: the reference decodes
+ * one sequence) over batch rows [batch][4096] of data_buffer, in place; row b is sequence b at
+ * position seq_lens[b]-1 of cache b (kv_caches as ie_decode_step_batched), workspace
+ * ie_batch_workspace_size(batch) bytes.  Synchronous.  The step's residual rows after its 32
+ * layers equal the embedding followed by these 32 calls, bit for bit. */
+IE_API int ie_decoder_layer_batched(ie_context* ctx, const ie_model_weights* weights,
+                                    int layer_idx, int batch, const int* seq_lens,
+                                    ie_bf16* data_buffer, ie_bf16* attn_buffer, void* workspace,
+                                    void* kv_caches);
 /* final RMSNorm + lm_head GEMV to fp32 logits for `rows` rows of [rows, 4096]. */
 IE_API int ie_final_norm_lm_head(ie_context* ctx, int rows, const ie_bf16* d_x,
                                  const ie_bf16* d_norm_w, const ie_bf16* d_lm_head,

@@ -110,3 +110,28 @@ inline void lm_head(IEHandle handle, int seq_len, bf16* d_input, bf16* d_weight,
 inline void sample_token_amax(IEHandle handle, const float* d_logits, int* d_output) {
   infengine_detail::checked(ie_sample_token_amax(handle, d_logits, d_output));
 }
+
+namespace infengine_detail {
+// The context behind the handle-free launchers: one per host thread, on the device current at
+// its first use and on the legacy default stream (where the reference's launchers run),
+// destroyed when the thread ends.
+inline IEHandle thread_default_handle() {
+  struct Holder {
+    IEHandle h = nullptr;
+    ~Holder() {
+      if (h) ie_context_destroy(h);
+    }
+  };
+  thread_local Holder holder;
+  if (!holder.h) checked(ie_context_create(&holder.h, IE_CURRENT_DEVICE, nullptr));
+  return holder.h;
+}
+}  // namespace infengine_detail
+
+// sampling.cuh:4, the reference's own spelling: no handle (the argmax's reduction state lives in
+// the calling thread's default context).  Asynchronous on the legacy default stream, like the
+// reference's launcher; the caller's copy of *d_output orders after it.
+inline void sample_token_amax(const float* d_logits, int* d_output) {
+  infengine_detail::checked(
+      ie_sample_token_amax(infengine_detail::thread_default_handle(), d_logits, d_output));
+}

@@ -218,6 +218,9 @@ int enqueue_decode(Context* c, hipStream_t st, const ie_model_weights& W, int se
   return IE_OK;
 }
 
+// Rows of the weights' RoPE tables (0: the reference's 8192).
+int rope_rows(const ie_model_weights& W) { return W.rope_rows > 0 ? W.rope_rows : kMaxCtx; }
+
 bool weights_complete(const ie_model_weights& W) {
   if (!W.emb_lookup || !W.final_norm || !W.lm_head || !W.rope.cos || !W.rope.sin) return false;
   for (int l = 0; l < kLayers; ++l) {
@@ -300,6 +303,7 @@ int ie_context_create(ie_context** out, int device, void* stream) {
   *out = nullptr;
   int n = 0;
   IE_CHECK_HIP(hipGetDeviceCount(&n));
+  if (device == IE_CURRENT_DEVICE) IE_CHECK_HIP(hipGetDevice(&device));
   IE_REQUIRE(device >= 0 && device < n, "ie_context_create: device %d of %d", device, n);
   IE_CHECK_HIP(hipSetDevice(device));
   ie_context* c = new ie_context;
@@ -351,6 +355,8 @@ int ie_context_destroy(ie_context* c) {
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+  for (auto& bg : c->bgraph)
+    if (bg.exec) (void)hipGraphExecDestroy(bg.exec);
   (void)hipFree(c->d_counters);
   (void)hipFree(c->d_slots);
   (void)hipFree(c->d_params);
@@ -543,6 +549,84 @@ int ie_generate(ie_context* c, const ie_model_weights* weights, const int* promp
 
 // ---------------------------------------------------------------- prefill
 namespace {
+// One decoder layer of the prefill (prefill.cu:17-38's loop body) over the S rows of
+// data_buffer at positions start_pos.., in place: RMSNorm, the Q/K/V product, RoPE and the K/V
+// write-out, causal attention, the O product + residual, RMSNorm, gate/up + SwiGLU, down +
+// residual.  The workspace holds q/k/v and the rotated q, then h.
+int prefill_layer(hipStream_t st, const ie_model_weights& W, int l, int start_pos, int S,
+                  ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
+                  void* workspace, void* kv_cache, const int* block_table, int n_pages) {
+  char* wsb = static_cast<char*>(workspace);
+  uint16_t* qkv = reinterpret_cast<uint16_t*>(wsb);
+  uint16_t* qrot = reinterpret_cast<uint16_t*>(wsb + align256((size_t)S * kQKVDim * 2));
+  uint16_t* h = reinterpret_cast<uint16_t*>(wsb);
+  const ie_layer& L = W.layers[l];
+  uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_cache) + (size_t)l * kPageLayer
+                              : kv_layer(kv_cache, l);
+  uint16_t* vpl = kvl + (size_t)kKVHeads * (block_table ? kPageHead : kKVPlane);
+  IE_TRY(launch_rmsnorm(S, data_buffer, L.input_layernorm, aux_buffer, st));
+  GemmParams g{};
+  g.x = aux_buffer;
+  g.w0 = L.transformer.w_q;
+  g.w1 = L.transformer.w_k;
+  g.w2 = L.transformer.w_v;
+  g.n0 = kHidden;
+  g.n1 = kKVDim;
+  g.y = qkv;
+  g.M = S;
+  g.N = kQKVDim;
+  g.K = kHidden;
+  g.ldy = kQKVDim;
+  // split K's partials after q/k/v and the rotated q (the rest of the workspace)
+  g.split_ws = reinterpret_cast<float*>(wsb + prefill_attn_bytes(S));
+  g.split_ws_bytes = (long long)(ie_attn_workspace_size(S) - prefill_attn_bytes(S));
+  IE_TRY(launch_gemm(kGemmBf16, g, st));
+  IE_TRY(launch_qkv_rope_scatter(S, start_pos, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl,
+                                 nullptr, 0, st, block_table, n_pages));
+  AttnPrefillParams a{qrot, kvl, vpl, attn_buffer, S, start_pos, block_table, n_pages};
+  IE_TRY(launch_attn_prefill(a, st));
+  GemmParams o{};
+  o.x = attn_buffer;
+  o.w0 = L.transformer.w_o;
+  o.n0 = kHidden;
+  o.y = data_buffer;
+  o.M = S;
+  o.N = kHidden;
+  o.K = kHidden;
+  o.ldy = kHidden;
+  o.split_ws = reinterpret_cast<float*>(wsb);  // q/k/v and rotated q are dead
+  o.split_ws_bytes = (long long)std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S));
+  IE_TRY(launch_gemm(kGemmResid, o, st));
+  IE_TRY(launch_rmsnorm(S, data_buffer, L.post_attention_layernorm, aux_buffer, st));
+  GemmParams gu{};
+  gu.x = aux_buffer;
+  gu.w0 = L.ffn_block.w_gate;
+  gu.w1 = L.ffn_block.w_up;
+  gu.y = h;
+  gu.M = S;
+  gu.N = kFFN;
+  gu.K = kHidden;
+  gu.ldy = kFFN;
+  gu.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
+  gu.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
+                                  align256((size_t)S * kFFN * 2));
+  IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
+  GemmParams dn{};
+  dn.x = h;
+  dn.w0 = L.ffn_block.w_down;
+  dn.n0 = kHidden;
+  dn.y = data_buffer;
+  dn.M = S;
+  dn.N = kHidden;
+  dn.K = kFFN;
+  dn.ldy = kHidden;
+  dn.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
+  dn.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
+                                  align256((size_t)S * kFFN * 2));
+  IE_TRY(launch_gemm(kGemmResid, dn, st));
+  return IE_OK;
+}
+
 // The prefill body over a reference-layout cache (block_table null) or over a page pool
 // (kv_cache = n_pages pages, block_table the sequence's page per 64-position block).  The
 // seq_len tokens sit at positions start_pos .. (tokenid_buff indexed by position); with pages,
@@ -557,84 +641,20 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int start_pos, 
              "prefill: start_pos %d needs the paged cache", start_pos);
   IE_REQUIRE(seq_len >= 1 && start_pos + seq_len <= cap,
              "prefill: positions [%d, %d) out of [0, %d]", start_pos, start_pos + seq_len, cap);
+  IE_REQUIRE(start_pos + seq_len <= rope_rows(*weights),
+             "prefill: position %d past the weights' %d RoPE table rows (rope_rows)",
+             start_pos + seq_len - 1, rope_rows(*weights));
   IE_REQUIRE(tokenid_buff && data_buffer && aux_buffer && attn_buffer && output_distr &&
                  output_token && workspace && kv_cache,
              "prefill: null buffer");
   const ie_model_weights& W = *weights;
   hipStream_t st = c->stream;
   const int S = seq_len;
-  char* wsb = static_cast<char*>(workspace);
-  uint16_t* qkv = reinterpret_cast<uint16_t*>(wsb);
-  uint16_t* qrot = reinterpret_cast<uint16_t*>(wsb + align256((size_t)S * kQKVDim * 2));
-  uint16_t* h = reinterpret_cast<uint16_t*>(wsb);
 
   IE_TRY(launch_emblookup(S, tokenid_buff + start_pos, W.emb_lookup, data_buffer, nullptr, 0, st));
-  for (int l = 0; l < kLayers; ++l) {
-    const ie_layer& L = W.layers[l];
-    uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_cache) + (size_t)l * kPageLayer
-                                : kv_layer(kv_cache, l);
-    uint16_t* vpl = kvl + (size_t)kKVHeads * (block_table ? kPageHead : kKVPlane);
-    IE_TRY(launch_rmsnorm(S, data_buffer, L.input_layernorm, aux_buffer, st));
-    GemmParams g{};
-    g.x = aux_buffer;
-    g.w0 = L.transformer.w_q;
-    g.w1 = L.transformer.w_k;
-    g.w2 = L.transformer.w_v;
-    g.n0 = kHidden;
-    g.n1 = kKVDim;
-    g.y = qkv;
-    g.M = S;
-    g.N = kQKVDim;
-    g.K = kHidden;
-    g.ldy = kQKVDim;
-    // split K's partials after q/k/v and the rotated q (the rest of the workspace)
-    g.split_ws = reinterpret_cast<float*>(wsb + prefill_attn_bytes(S));
-    g.split_ws_bytes = (long long)(ie_attn_workspace_size(S) - prefill_attn_bytes(S));
-    IE_TRY(launch_gemm(kGemmBf16, g, st));
-    IE_TRY(launch_qkv_rope_scatter(S, start_pos, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl,
-                                   nullptr, 0, st, block_table, n_pages));
-    AttnPrefillParams a{qrot, kvl, vpl, attn_buffer, S, start_pos, block_table, n_pages};
-    IE_TRY(launch_attn_prefill(a, st));
-    GemmParams o{};
-    o.x = attn_buffer;
-    o.w0 = L.transformer.w_o;
-    o.n0 = kHidden;
-    o.y = data_buffer;
-    o.M = S;
-    o.N = kHidden;
-    o.K = kHidden;
-    o.ldy = kHidden;
-    o.split_ws = reinterpret_cast<float*>(wsb);  // q/k/v and rotated q are dead
-    o.split_ws_bytes = (long long)std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S));
-    IE_TRY(launch_gemm(kGemmResid, o, st));
-    IE_TRY(launch_rmsnorm(S, data_buffer, L.post_attention_layernorm, aux_buffer, st));
-    GemmParams gu{};
-    gu.x = aux_buffer;
-    gu.w0 = L.ffn_block.w_gate;
-    gu.w1 = L.ffn_block.w_up;
-    gu.y = h;
-    gu.M = S;
-    gu.N = kFFN;
-    gu.K = kHidden;
-    gu.ldy = kFFN;
-    gu.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
-    gu.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
-                                    align256((size_t)S * kFFN * 2));
-    IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
-    GemmParams dn{};
-    dn.x = h;
-    dn.w0 = L.ffn_block.w_down;
-    dn.n0 = kHidden;
-    dn.y = data_buffer;
-    dn.M = S;
-    dn.N = kHidden;
-    dn.K = kFFN;
-    dn.ldy = kHidden;
-    dn.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
-    dn.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
-                                    align256((size_t)S * kFFN * 2));
-    IE_TRY(launch_gemm(kGemmResid, dn, st));
-  }
+  for (int l = 0; l < kLayers; ++l)
+    IE_TRY(prefill_layer(st, W, l, start_pos, S, data_buffer, aux_buffer, attn_buffer, workspace,
+                         kv_cache, block_table, n_pages));
   // prefill.cu:41-43: final norm, lm_head on the last row only, argmax
   IE_TRY(gemv_plain(kHidden, kEpiF32, data_buffer + (size_t)(S - 1) * kHidden, W.final_norm,
                     W.lm_head, nullptr, kVocab / 2, nullptr, output_distr, 1, kVocab, st));
@@ -677,8 +697,105 @@ int ie_prefill_paged_chunk(ie_context* c, const ie_model_weights* weights, int s
                       n_pages);
 }
 
+int ie_decoder_layer_prefill(ie_context* c, const ie_model_weights* weights, int layer_idx,
+                             int seq_len, ie_bf16* data_buffer, ie_bf16* aux_buffer,
+                             ie_bf16* attn_buffer, void* workspace, void* kv_cache) {
+  CTX_OK(c);
+  IE_REQUIRE(weights && weights_complete(*weights), "decoder_layer_prefill: incomplete weights");
+  IE_REQUIRE(layer_idx >= 0 && layer_idx < kLayers, "decoder_layer_prefill: layer %d", layer_idx);
+  IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx, "decoder_layer_prefill: seq_len %d out of [1, %d]",
+             seq_len, kMaxCtx);
+  IE_REQUIRE(data_buffer && aux_buffer && attn_buffer && workspace && kv_cache,
+             "decoder_layer_prefill: null buffer");
+  return prefill_layer(c->stream, *weights, layer_idx, 0, seq_len, data_buffer, aux_buffer,
+                       attn_buffer, workspace, kv_cache, nullptr, 0);
+}
+
 // ---------------------------------------------------------------- batched decode
 namespace {
+// One decoder layer of the batched step over the batch rows of data_buffer (in place), the
+// rows' partial sums of squares already in w.ss (from the previous layer's down projection or
+// the prep kernel); with ss_next the down projection leaves those of its output rows there.
+int batched_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, int batch,
+                  int len_class, ie_bf16* data_buffer, ie_bf16* attn_buffer, const DecodeWs& w,
+                  void* kv_caches, const int* block_table, int table_stride, int n_pages,
+                  bool ss_next) {
+  const int* d_sl = c->d_params + 1;
+  const long long cstride = (long long)kLayers * kKVLayer;
+  const ie_layer& L = W.layers[l];
+  uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_caches) + (size_t)l * kPageLayer
+                              : kv_layer(kv_caches, l);
+  GemmParams g{};
+  g.x = data_buffer;
+  g.w0 = L.transformer.w_q;
+  g.w1 = L.transformer.w_k;
+  g.w2 = L.transformer.w_v;
+  g.n0 = kHidden;
+  g.n1 = kKVDim;
+  g.y = w.q;  // q rotated; k rotated and v into each sequence's cache row
+  g.M = batch;
+  g.N = kQKVDim;
+  g.K = kHidden;
+  g.ldy = kQKVDim;
+  g.rope_cos = W.rope.cos;
+  g.rope_sin = W.rope.sin;
+  g.k_cache = kvl;
+  g.v_cache = kvl + (size_t)kKVHeads * (block_table ? kPageHead : kKVPlane);
+  g.cache_stride = cstride;
+  g.block_table = block_table;
+  g.table_stride = table_stride;
+  g.n_pages = n_pages;
+  g.d_seq_len = d_sl;
+  g.ss_in = w.ss;
+  g.ss_parts = kNormParts;
+  g.x_norm_w = L.input_layernorm;
+  g.sk_tail = gemm_skinny_tail(kQKVDim);
+  g.sk_part = w.sk_part;
+  g.sk_cnt = c->d_counters + kCntSkinny;
+  IE_TRY(launch_gemm(kGemmQkvRope, g, st));
+  IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, len_class, batch, cstride, true, st,
+                     block_table, table_stride, n_pages, true));
+  GemmParams o{};
+  o.x = attn_buffer;
+  o.w0 = L.transformer.w_o;
+  o.n0 = kHidden;
+  o.y = data_buffer;
+  o.M = batch;
+  o.N = kHidden;
+  o.K = kHidden;
+  o.ldy = kHidden;
+  o.ss_out = w.ss;
+  IE_TRY(launch_gemm(kGemmResid, o, st));
+  GemmParams gu{};
+  gu.x = data_buffer;
+  gu.w0 = L.ffn_block.w_gate;
+  gu.w1 = L.ffn_block.w_up;
+  gu.y = w.h;
+  gu.M = batch;
+  gu.N = kFFN;
+  gu.K = kHidden;
+  gu.ldy = kFFN;
+  gu.ss_in = w.ss;
+  gu.ss_parts = kNormParts;
+  gu.x_norm_w = L.post_attention_layernorm;
+  gu.sk_tail = gemm_skinny_tail(kFFN);
+  gu.sk_part = w.sk_part;
+  gu.sk_cnt = c->d_counters + kCntSkinny;
+  IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
+  GemmParams dn{};
+  dn.x = w.h;
+  dn.w0 = L.ffn_block.w_down;
+  dn.n0 = kHidden;
+  dn.y = data_buffer;
+  dn.M = batch;
+  dn.N = kHidden;
+  dn.K = kFFN;
+  dn.ldy = kHidden;
+  if (ss_next) dn.ss_out = w.ss;
+  IE_TRY(launch_gemm(kGemmResid, dn, st));
+  return IE_OK;
+}
+
 // The kernels of one batched step on stream st, the sequences' lengths already in
 // d_params[1 .. batch].  len_class bounds the longest context and picks the attention path:
 // kAttnDirectMaxCtx (one split per sequence and kv head, no merge launch), kAttnFusedMaxCtx or
@@ -690,87 +807,16 @@ int enqueue_batched(Context* c, hipStream_t st, const ie_model_weights& W, int b
                     int n_pages) {
   const int* d_sl = c->d_params + 1;
   const DecodeWs w = decode_ws(workspace, batch);
-  const long long cstride = (long long)kLayers * kKVLayer;
   IE_TRY(launch_emblookup(batch, tokenid_buffs, W.emb_lookup, data_buffer, d_sl, tokens_stride,
                           st));
   // RMSNorm inside the projections: the QKV and gate/up projections read the residual rows
-  // with partial sums of squares of them (layer 0: from this prep kernel, 4 per row; later:
-  // from the residual epilogue of the O / down projection, kNormParts partials per row) and
+  // with kNormParts partial sums of squares per row (layer 0: from this prep kernel; later:
+  // from the residual epilogue of the O / down projection, the same partials bit for bit) and
   // normalise the rows on their way in, with rmsnorm.cu:61's two roundings
   IE_TRY(launch_rmsnorm_prep(batch, data_buffer, w.ss, st));
-  for (int l = 0; l < kLayers; ++l) {
-    const ie_layer& L = W.layers[l];
-    uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_caches) + (size_t)l * kPageLayer
-                                : kv_layer(kv_caches, l);
-    GemmParams g{};
-    g.x = data_buffer;
-    g.w0 = L.transformer.w_q;
-    g.w1 = L.transformer.w_k;
-    g.w2 = L.transformer.w_v;
-    g.n0 = kHidden;
-    g.n1 = kKVDim;
-    g.y = w.q;  // q rotated; k rotated and v into each sequence's cache row
-    g.M = batch;
-    g.N = kQKVDim;
-    g.K = kHidden;
-    g.ldy = kQKVDim;
-    g.rope_cos = W.rope.cos;
-    g.rope_sin = W.rope.sin;
-    g.k_cache = kvl;
-    g.v_cache = kvl + (size_t)kKVHeads * (block_table ? kPageHead : kKVPlane);
-    g.cache_stride = cstride;
-    g.block_table = block_table;
-    g.table_stride = table_stride;
-    g.n_pages = n_pages;
-    g.d_seq_len = d_sl;
-    g.ss_in = w.ss;
-    g.ss_parts = kNormParts;
-    g.x_norm_w = L.input_layernorm;
-    g.sk_tail = gemm_skinny_tail(kQKVDim);
-    g.sk_part = w.sk_part;
-    g.sk_cnt = c->d_counters + kCntSkinny;
-    IE_TRY(launch_gemm(kGemmQkvRope, g, st));
-    IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, len_class, batch, cstride, true, st,
-                       block_table, table_stride, n_pages, true));
-    GemmParams o{};
-    o.x = attn_buffer;
-    o.w0 = L.transformer.w_o;
-    o.n0 = kHidden;
-    o.y = data_buffer;
-    o.M = batch;
-    o.N = kHidden;
-    o.K = kHidden;
-    o.ldy = kHidden;
-    o.ss_out = w.ss;
-    IE_TRY(launch_gemm(kGemmResid, o, st));
-    GemmParams gu{};
-    gu.x = data_buffer;
-    gu.w0 = L.ffn_block.w_gate;
-    gu.w1 = L.ffn_block.w_up;
-    gu.y = w.h;
-    gu.M = batch;
-    gu.N = kFFN;
-    gu.K = kHidden;
-    gu.ldy = kFFN;
-    gu.ss_in = w.ss;
-    gu.ss_parts = kNormParts;
-    gu.x_norm_w = L.post_attention_layernorm;
-    gu.sk_tail = gemm_skinny_tail(kFFN);
-    gu.sk_part = w.sk_part;
-    gu.sk_cnt = c->d_counters + kCntSkinny;
-    IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
-    GemmParams dn{};
-    dn.x = w.h;
-    dn.w0 = L.ffn_block.w_down;
-    dn.n0 = kHidden;
-    dn.y = data_buffer;
-    dn.M = batch;
-    dn.N = kHidden;
-    dn.K = kFFN;
-    dn.ldy = kHidden;
-    if (l + 1 < kLayers) dn.ss_out = w.ss;
-    IE_TRY(launch_gemm(kGemmResid, dn, st));
-  }
+  for (int l = 0; l < kLayers; ++l)
+    IE_TRY(batched_layer(c, st, W, l, batch, len_class, data_buffer, attn_buffer, w, kv_caches,
+                         block_table, table_stride, n_pages, l + 1 < kLayers));
   // prefill.cu:41-43 / decode.cu:41: final RMSNorm of the rows, then the lm_head product
   IE_TRY(launch_rmsnorm(batch, data_buffer, W.final_norm, w.xn, st));
   GemmParams lm{};
@@ -803,10 +849,14 @@ int batched_step(ie_context* c, const ie_model_weights* weights, int batch, cons
                  output_tokens && workspace && kv_caches,
              "decode_step_batched: null buffer");
   const int cap = block_table ? kMaxLongCtx : kMaxCtx;
-  for (int b = 0; b < batch; ++b)
+  for (int b = 0; b < batch; ++b) {
     IE_REQUIRE(seq_lens[b] >= 1 && seq_lens[b] <= cap && seq_lens[b] <= tokens_stride,
                "decode_step_batched: seq_lens[%d]=%d out of [1, %d] (token rows of %d)", b,
                seq_lens[b], cap, tokens_stride);
+    IE_REQUIRE(seq_lens[b] <= rope_rows(*weights),
+               "decode_step_batched: seq_lens[%d]=%d past the weights' %d RoPE table rows "
+               "(rope_rows)", b, seq_lens[b], rope_rows(*weights));
+  }
   hipStream_t st = c->stream;
   int max_len = 1;
   for (int b = 0; b < batch; ++b) {
@@ -883,6 +933,38 @@ int ie_decode_step_batched(ie_context* c, const ie_model_weights* weights, int b
   return batched_step(c, weights, batch, seq_lens, tokenid_buffs, kMaxCtx, data_buffer,
                       attn_buffer, output_distr, output_tokens, tokens_out, workspace, kv_caches,
                       nullptr, 0, 0);
+}
+
+int ie_decoder_layer_batched(ie_context* c, const ie_model_weights* weights, int layer_idx,
+                             int batch, const int* seq_lens, ie_bf16* data_buffer,
+                             ie_bf16* attn_buffer, void* workspace, void* kv_caches) {
+  CTX_OK(c);
+  IE_REQUIRE(weights && weights_complete(*weights), "decoder_layer_batched: incomplete weights");
+  IE_REQUIRE(layer_idx >= 0 && layer_idx < kLayers, "decoder_layer_batched: layer %d", layer_idx);
+  IE_REQUIRE(batch >= 1 && batch <= 16, "decoder_layer_batched: batch %d out of [1, 16]", batch);
+  IE_REQUIRE(seq_lens && data_buffer && attn_buffer && workspace && kv_caches,
+             "decoder_layer_batched: null buffer");
+  int max_len = 1;
+  for (int b = 0; b < batch; ++b) {
+    IE_REQUIRE(seq_lens[b] >= 1 && seq_lens[b] <= kMaxCtx,
+               "decoder_layer_batched: seq_lens[%d]=%d out of [1, %d]", b, seq_lens[b], kMaxCtx);
+    c->h_params[1 + b] = seq_lens[b];
+    max_len = std::max(max_len, seq_lens[b]);
+  }
+  hipStream_t st = c->stream;
+  IE_CHECK_HIP(hipMemcpyAsync(c->d_params + 1, c->h_params + 1, batch * sizeof(int),
+                              hipMemcpyHostToDevice, st));
+  // the attention path ie_decode_step_batched takes for these lengths
+  const int len_class = max_len <= kAttnDirectMaxCtx  ? kAttnDirectMaxCtx
+                        : max_len <= kAttnFusedMaxCtx ? kAttnFusedMaxCtx
+                                                      : kMaxCtx;
+  const DecodeWs w = decode_ws(workspace, batch);
+  IE_TRY(launch_rmsnorm_prep(batch, data_buffer, w.ss, st));
+  IE_TRY(batched_layer(c, st, *weights, layer_idx, batch, len_class, data_buffer, attn_buffer, w,
+                       kv_caches, nullptr, 0, 0, false));
+  // the lengths' pinned staging is reused by the next call
+  IE_CHECK_HIP(hipStreamSynchronize(st));
+  return IE_OK;
 }
 
 size_t ie_kv_page_size(void) { return kPageElems * sizeof(uint16_t); }
@@ -993,6 +1075,7 @@ void weights_arena_assign(ie_model_weights* w, void* arena) {
   w->lm_head = static_cast<ie_bf16*>(take(emb * 2));
   w->rope.cos = static_cast<float*>(take((size_t)kMaxLongCtx * 64 * 4));
   w->rope.sin = static_cast<float*>(take((size_t)kMaxLongCtx * 64 * 4));
+  w->rope_rows = kMaxLongCtx;
 }
 
 int weights_upload_rope(ie_model_weights* w) {

@@ -118,6 +118,17 @@ __device__ __forceinline__ float dot8(const uint4& w, const uint4& x, float acc)
   return acc;
 }
 
+// RoPE of the pair (a, b) = (x_j, x_{j+64}) by angle (c, s) = (cos, sin) (rope.cu:59-64):
+// a c - b s and a s + b c, each as one fused multiply-add over the other product, so the result
+// does not depend on which product the compiler would have contracted (nvcc, compiling the
+// reference, contracts a*b - c*d the same way by default).
+__host__ __device__ __forceinline__ float rope_lo(float a, float b, float c, float s) {
+  return fmaf(a, c, -(b * s));
+}
+__host__ __device__ __forceinline__ float rope_hi(float a, float b, float c, float s) {
+  return fmaf(a, s, b * c);
+}
+
 // Native 4 x u32 vector.  Register arrays use it instead of HIP's uint4 (a
 // struct with a union, which SROA does not split into registers).
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));

@@ -127,8 +127,8 @@ __global__ __launch_bounds__(64) void rope_kernel(int start_pos, int seq_len, co
   const int pos = start_pos + tok;
   const float c = cos_t[pos * 64 + j], s = sin_t[pos * 64 + j];
   const float a = bf2f(in[off + j]), b = bf2f(in[off + j + 64]);
-  out[off + j] = f2bf(a * c - b * s);
-  out[off + j + 64] = f2bf(a * s + b * c);
+  out[off + j] = f2bf(rope_lo(a, b, c, s));
+  out[off + j + 64] = f2bf(rope_hi(a, b, c, s));
 }
 
 // ---------------------------------------------------------------- prefill q/k/v scatter
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void qkv_rope_scatter_kernel(int start_pos, co
     float a = bf2f(hs[j]), b = bf2f(hs[j + 64]);
     if (head < kQHeads + kKVHeads) {
       const float c = cos_t[pos * 64 + j], s = sin_t[pos * 64 + j];
-      const float a2 = a * c - b * s, b2 = a * s + b * c;
+      const float a2 = rope_lo(a, b, c, s), b2 = rope_hi(a, b, c, s);
       a = a2;
       b = b2;
     }
@@ -257,31 +257,30 @@ int launch_emblookup(int rows, const int* ids, const uint16_t* table, uint16_t* 
   return IE_OK;
 }
 
-// One block per row of 16 (rows past `rows` write a zero sum); thread t writes partial t.
-static_assert(kNormParts == 256, "one partial per thread");
+// One block per row of 16 (rows past `rows` write zero sums); thread t writes partial t, the
+// sum of squares of columns 16t .. 16t+15 exactly as the skinny GEMM's residual epilogue forms
+// it for its 16-column tile t (lane group q's four columns 16t + 4q .. +3 as one fma chain, then
+// (q0 + q1) + (q2 + q3)), so a step's later layers, which read that epilogue's partials, and a
+// layer started from this kernel see the same bits.
+static_assert(kNormParts == 256 && kNormParts * 16 == kHidden, "one 16-column partial per thread");
 __global__ __launch_bounds__(256) void rmsnorm_prep_kernel(int rows, const uint16_t* x,
                                                            float* ss) {
-  __shared__ float red[4];
-  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float s = 0.f;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  float part = 0.f;
   if (row < rows) {
-    const uint4* x4 = reinterpret_cast<const uint4*>(x + (size_t)row * kHidden);
+    const uint4* x4 = reinterpret_cast<const uint4*>(x + (size_t)row * kHidden + 16 * tid);
+    const uint4 a = x4[0], b = x4[1];
+    const uint32_t e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float sq[4];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const uint4 v = x4[tid + k * 256];
-      const uint32_t e[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        s = fmaf(bf_lo(e[q]), bf_lo(e[q]), s);
-        s = fmaf(bf_hi(e[q]), bf_hi(e[q]), s);
-      }
+    for (int q = 0; q < 4; ++q) {
+      const float v0 = bf_lo(e[2 * q]), v1 = bf_hi(e[2 * q]), v2 = bf_lo(e[2 * q + 1]),
+                  v3 = bf_hi(e[2 * q + 1]);
+      sq[q] = fmaf(v0, v0, fmaf(v1, v1, fmaf(v2, v2, v3 * v3)));
     }
+    part = (sq[0] + sq[1]) + (sq[2] + sq[3]);
   }
-  s = wave_sum(s);
-  if (lane == 0) red[wave] = s;
-  __syncthreads();
-  // the layout of the skinny GEMM's residual epilogue: kNormParts partials per row
-  ss[row * kNormParts + tid] = tid == 0 ? (red[0] + red[1]) + (red[2] + red[3]) : 0.f;
+  ss[row * kNormParts + tid] = part;
 }
 
 int launch_rmsnorm_prep(int rows, const uint16_t* x, float* ss, hipStream_t st) {

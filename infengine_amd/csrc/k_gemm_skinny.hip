@@ -433,7 +433,7 @@ void gemm_skinny_kernel(GemmParams p) {
     for (int i = 0; i < 4; ++i) {
       if (head < kQHeads + kKVHeads) {
         const float c = ecos[i], sn = esin[i];
-        v[i] = hi ? a[i] * sn + b[i] * c : a[i] * c - b[i] * sn;
+        v[i] = hi ? rope_hi(a[i], b[i], c, sn) : rope_lo(a[i], b[i], c, sn);
       } else {
         v[i] = hi ? b[i] : a[i];
       }

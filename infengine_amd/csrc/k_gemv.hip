@@ -113,8 +113,8 @@ __device__ __forceinline__ void gemv_epilogue(const GemvParams& p, int pair, int
     if (head < kQHeads + kKVHeads) {
       const float c = e.have ? e.c : p.rope_cos[pos * (kHeadDim / 2) + j];
       const float s = e.have ? e.s : p.rope_sin[pos * (kHeadDim / 2) + j];
-      const float o0 = y0 * c - y1 * s;
-      const float o1 = y0 * s + y1 * c;
+      const float o0 = rope_lo(y0, y1, c, s);
+      const float o1 = rope_hi(y0, y1, c, s);
       y0 = o0;
       y1 = o1;
     }

@@ -49,6 +49,7 @@ def _load() -> C.CDLL:
     P, I, U64, F, SZ = C.c_void_p, C.c_int, C.c_uint64, C.c_float, C.c_size_t
     sig = {
         "orc_set_sum_order": (None, [I]),
+        "orc_set_prob_round": (None, [I]),
         "orc_fill_synthetic": (None, [P, SZ, U64, U64, F, F]),
         "orc_tensor_id": (U64, [I, I]),
         "orc_rope_freqs": (None, [P]),
@@ -100,6 +101,29 @@ class reversed_summation:
 
     def __exit__(self, *exc):
         _lib.orc_set_sum_order(0)
+        return False
+
+
+PROB_FP32, PROB_REFERENCE, PROB_FLASH = 0, 1, 2
+
+
+class prob_rounding:
+    """Context manager: the rounding point of the attention probabilities before P.V.
+    PROB_FP32 (the default) keeps them in fp32; PROB_REFERENCE rounds the normalised
+    probabilities to bf16 as the reference's softmax stores them (softmax.cu:105,158) before
+    its A.V GEMM (attn.cu:167-204); PROB_FLASH rounds exp2((s - m) c) to bf16 against the
+    running max m of 64-key tiles and divides by the sum of the rounded values at the end,
+    the form of an MFMA flash attention whose P.V operand is bf16."""
+
+    def __init__(self, mode: int):
+        self.mode = mode
+
+    def __enter__(self):
+        _lib.orc_set_prob_round(self.mode)
+        return self
+
+    def __exit__(self, *exc):
+        _lib.orc_set_prob_round(PROB_FP32)
         return False
 
 

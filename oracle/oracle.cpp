@@ -56,6 +56,17 @@ constexpr double kSynthStd = 37837.22627754049;  // sqrt(4 * (65536^2 - 1) / 12)
 // rounding-noise floor that any fp32-accumulating implementation sits inside.
 int g_sum_reverse = 0;
 
+// Rounding point of the attention probabilities before P.V (orc_set_prob_round):
+//   0  fp32 throughout: out = bf16(sum_t p_t v_t), p = softmax in fp32 (the exact math);
+//   1  the reference's point: the softmax kernel stores the normalised probabilities in the
+//      storage type (softmax.cu:105,158) and the A.V GEMM multiplies those
+//      (attn.cu:167-204): p_t = bf16(exp(s_t - max) / sum), out = bf16(sum_t p_t v_t);
+//   2  the flash form: keys in 64-key tiles from key 0, a running max m of the raw scores,
+//      p_t = bf16(exp2((s_t - m) c)) with c = log2(e)/sqrt(128), o and the row sum l of the
+//      rounded p rescaled by exp2((m_old - m_new) c) when m grows, out = bf16(o * (1 / l)):
+//      the rounding the MFMA prefill attention applies (its P.V operand is bf16).
+int g_prob_round = 0;
+
 // fp32 dot product of two bf16 vectors, 8 running partial sums.
 inline float dot_bf16(const uint16_t* a, const uint16_t* b, int k) {
   float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -85,6 +96,7 @@ inline float silu_mul(float g, float u) {  // swiglu.cu:24-29
 extern "C" {
 
 void orc_set_sum_order(int reverse) { g_sum_reverse = reverse ? 1 : 0; }
+void orc_set_prob_round(int mode) { g_prob_round = mode < 0 || mode > 2 ? 0 : mode; }
 
 // ---------------------------------------------------------------- synthetic data
 // Deterministic approximate normal keyed by (seed, tensor_id, index): centred
@@ -206,8 +218,9 @@ void orc_apply_rope(int start_pos, int heads, int seq_len, int head_rows, const 
       for (int j = 0; j < 64; ++j) {
         const float c = cos_t[(size_t)pos * 64 + j], s = sin_t[(size_t)pos * 64 + j];
         const float a = bf2f(in[off + j]), b = bf2f(in[off + j + 64]);
-        out[off + j] = f2bf(a * c - b * s);
-        out[off + j + 64] = f2bf(a * s + b * c);
+        // one rounding over the second product, as nvcc contracts rope.cu:63-64 by default
+        out[off + j] = f2bf(std::fma(a, c, -(b * s)));
+        out[off + j + 64] = f2bf(std::fma(a, s, b * c));
       }
     }
 }
@@ -236,12 +249,15 @@ void orc_softmax_scaled(int rows, int len, int causal, const uint16_t* in, uint1
 // ---------------------------------------------------------------- attention
 // attn.cu:355-363 (prefill) / :423-431 (decode): for q row i (absolute position
 // q_start + i) and q head h, scores s_t = (q_h . k_{h/4, t}) / sqrt(128) for
-// t = 0..q_start+i, p = softmax(s) (fp32), out = sum_t p_t v_{h/4, t}, rounded
-// to bf16.  GQA mapping h -> h/4 is attn.cu:51-53 / HF repeat_kv.
+// t = 0..q_start+i, p = softmax(s), out = sum_t p_t v_{h/4, t}, rounded to bf16,
+// with p rounded as g_prob_round says (fp32 by default).  GQA mapping h -> h/4 is
+// attn.cu:51-53 / HF repeat_kv.
 // q: [n_q][32][128]; k/v planes: [8][ctx_stride][128]; out: [n_q][4096].
 void orc_attention(int n_q, int q_start, const uint16_t* q, const uint16_t* kplane,
                    const uint16_t* vplane, int ctx_stride, uint16_t* out) {
   const float scale = 0.08838834764831845f;
+  const float c2 = 0.08838834764831845f * 1.4426950408889634f;  // scale * log2(e)
+  const int mode = g_prob_round;
 #pragma omp parallel for schedule(dynamic) collapse(2)
   for (int i = 0; i < n_q; ++i)
     for (int h = 0; h < kQHeads; ++h) {
@@ -249,7 +265,33 @@ void orc_attention(int n_q, int q_start, const uint16_t* q, const uint16_t* kpla
       const uint16_t* qh = q + ((size_t)i * kQHeads + h) * kHeadDim;
       const uint16_t* K = kplane + (size_t)g * ctx_stride * kHeadDim;
       const uint16_t* V = vplane + (size_t)g * ctx_stride * kHeadDim;
+      uint16_t* o = out + (size_t)i * kHidden + h * kHeadDim;
       std::vector<float> s(S);
+      float acc[kHeadDim] = {};
+      if (mode == 2) {
+        for (int t = 0; t < S; ++t) s[t] = dot_bf16(qh, K + (size_t)t * kHeadDim, kHeadDim);
+        float m = -INFINITY, l = 0.f;
+        for (int t0 = 0; t0 < S; t0 += 64) {
+          const int t1 = std::min(S, t0 + 64);
+          float mt = -INFINITY;
+          for (int t = t0; t < t1; ++t) mt = std::max(mt, s[t]);
+          const float mn = std::max(m, mt);
+          const float nb = -(mn * c2);
+          const float alpha = m == -INFINITY ? 0.f : std::exp2(std::fma(m, c2, nb));
+          l *= alpha;
+          for (int d = 0; d < kHeadDim; ++d) acc[d] *= alpha;
+          for (int t = t0; t < t1; ++t) {
+            const float p = bf2f(f2bf(std::exp2(std::fma(s[t], c2, nb))));
+            l += p;
+            const uint16_t* vt = V + (size_t)t * kHeadDim;
+            for (int d = 0; d < kHeadDim; ++d) acc[d] += p * bf2f(vt[d]);
+          }
+          m = mn;
+        }
+        const float inv = 1.0f / l;
+        for (int d = 0; d < kHeadDim; ++d) o[d] = f2bf(acc[d] * inv);
+        continue;
+      }
       float mx = -INFINITY;
       for (int t = 0; t < S; ++t) {
         s[t] = dot_bf16(qh, K + (size_t)t * kHeadDim, kHeadDim) * scale;
@@ -260,12 +302,19 @@ void orc_attention(int n_q, int q_start, const uint16_t* q, const uint16_t* kpla
         s[t] = std::exp(s[t] - mx);
         sum += s[t];
       }
-      float acc[kHeadDim] = {};
+      if (mode == 1) {
+        for (int t = 0; t < S; ++t) {
+          const float p = bf2f(f2bf(s[t] / sum));
+          const uint16_t* vt = V + (size_t)t * kHeadDim;
+          for (int d = 0; d < kHeadDim; ++d) acc[d] += p * bf2f(vt[d]);
+        }
+        for (int d = 0; d < kHeadDim; ++d) o[d] = f2bf(acc[d]);
+        continue;
+      }
       for (int t = 0; t < S; ++t) {
         const uint16_t* vt = V + (size_t)t * kHeadDim;
         for (int d = 0; d < kHeadDim; ++d) acc[d] += s[t] * bf2f(vt[d]);
       }
-      uint16_t* o = out + (size_t)i * kHidden + h * kHeadDim;
       for (int d = 0; d < kHeadDim; ++d) o[d] = f2bf(acc[d] / sum);
     }
 }

@@ -84,19 +84,34 @@ def assert_bf16_close(got: np.ndarray, want: np.ndarray, ulps: int = 2, what: st
     assert err.max() <= 1e-2 * scale, msg
 
 
-def assert_delta_close(x_in: np.ndarray, got: np.ndarray, want: np.ndarray, tol: float = 2e-2,
+def assert_delta_close(x_in: np.ndarray, got: np.ndarray, want: np.ndarray, tol: float = 1e-2,
                        what: str = ""):
     """A residual layer's own contribution (out - in) matches: per element
     |got - want| <= 2 ulp(want) + tol * max|want - x_in|, i.e. the output is
     right to its own bf16 rounding plus a small fraction of what the layer added
-    (a bare delta comparison is ill-conditioned where |x_in| >> |delta|)."""
+    (a bare delta comparison is ill-conditioned where |x_in| >> |delta|), and the
+    mean error is within tol of the mean |delta|.  Prints the worst element's share
+    of its allowance and the mean ratio."""
     g, w, x = (bf16_f32(a).astype(np.float64) for a in (got, want, x_in))
     ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(w), 1e-38))) - 7)
     allowed = 2 * ulp + tol * np.abs(w - x).max()
     err = np.abs(g - w)
     bad = err > allowed
+    mean_ratio = err.mean() / max(np.abs(w - x).mean(), 1e-30)
+    print(f"  {what}: worst {float((err / allowed).max()):.2f} of its allowance, "
+          f"mean error / mean |delta| {mean_ratio:.3e} (bar {tol:.0e})", flush=True)
     assert not bad.any(), f"{what}: {int(bad.sum())} elements off; worst {err.max():.3e}"
-    assert err.mean() <= tol * np.abs(w - x).mean(), f"{what}: mean error {err.mean():.3e}"
+    assert mean_ratio <= tol, f"{what}: mean error {err.mean():.3e}"
+
+
+def report_close(got, want, tol: float | None = None, what: str = ""):
+    """tolerance.assert_close (default bar 1e-2), printing the measured errors first so a run's
+    log shows each check's margin."""
+    from tolerance import TOL, assert_close, rel_errors
+    tol = TOL if tol is None else tol
+    mx, mean = rel_errors(got, want)
+    print(f"  {what}: max-abs/scale {mx:.3e}, mean-rel {mean:.3e} (bar {tol:.0e})", flush=True)
+    assert_close(got, want, tol=tol, what=what)
 
 
 def e2e_tol(noise: float) -> float:

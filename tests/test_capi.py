@@ -41,10 +41,26 @@ def test_ctypes_signatures_cover_the_header(hip):
     assert sorted(SIGNATURES) == declared_symbols()
 
 
-def test_model_weights_struct_layout_matches_header(hip):
-    # ie_model_weights: emb + 32 layers x 9 pointers + final_norm + lm_head + rope(2) + storage
-    assert C.sizeof(hip.ModelWeightsStruct) == 8 * (1 + 32 * 9 + 2 + 2 + 1)
-    assert hip.ModelWeightsStruct.layers.offset == 8
+def test_model_weights_struct_layout_matches_header(hip, tmp_path):
+    """The ctypes mirror has the C compiler's size and offsets of ie_model_weights."""
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "infengine.h"\n'
+                   'int main(void) { printf("%zu %zu %zu %zu %zu\\n", sizeof(ie_model_weights), '
+                   'offsetof(ie_model_weights, layers), offsetof(ie_model_weights, rope), '
+                   'offsetof(ie_model_weights, storage), offsetof(ie_model_weights, rope_rows)); '
+                   'return 0; }\n')
+    exe = tmp_path / "layout"
+    import pathlib
+    import subprocess
+    inc = pathlib.Path(__file__).resolve().parent.parent / "include"
+    subprocess.run(["gcc", f"-I{inc}", str(src), "-o", str(exe)], check=True)
+    want = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
+                                           check=True).stdout.split()]
+    S = hip.ModelWeightsStruct
+    assert [C.sizeof(S), S.layers.offset, S.rope.offset, S.storage.offset,
+            S.rope_rows.offset] == want
+    # emb + 32 layers x 9 pointers + final_norm + lm_head + rope(2) + storage, then rope_rows
+    assert want[4] == 8 * (1 + 32 * 9 + 2 + 2 + 1)
 
 
 def test_sizes(hip):
@@ -77,6 +93,8 @@ BOGUS = C.c_void_p(0x1000)   # never dereferenced: every call below fails valida
     lambda l: l.ie_prefill_paged_chunk(None, None, 0, 1, *[BOGUS] * 8, 1, BOGUS),
     lambda l: l.ie_attn_prefill_core_paged(None, 1, 9000, BOGUS, BOGUS, 1, BOGUS, 0, BOGUS),
     lambda l: l.ie_decoder_layer_decode(None, None, 0, 1, BOGUS, BOGUS, BOGUS, BOGUS),
+    lambda l: l.ie_decoder_layer_prefill(None, None, 0, 1, *[BOGUS] * 5),
+    lambda l: l.ie_decoder_layer_batched(None, None, 0, 1, None, *[BOGUS] * 4),
 ])
 def test_host_side_validation(hip, call):
     assert call(hip.lib) == IE_ERR_INVALID_ARG

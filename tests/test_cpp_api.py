@@ -23,7 +23,7 @@ def build_manager(out_dir: pathlib.Path, name: str = "manager_main") -> pathlib.
     return exe
 
 
-@pytest.mark.parametrize("name", ["manager_main", "batcher_main"])
+@pytest.mark.parametrize("name", ["manager_main", "batcher_main", "sampling_main"])
 def test_cpp_api_compiles_and_links(tmp_path, hip, name):
     exe = build_manager(tmp_path, name)
     assert exe.exists()
@@ -77,3 +77,20 @@ def test_cpp_manager_matches_python_driver(tmp_path, hip):
                          timeout=300)
     assert res.returncode == 0, res.stderr
     assert [int(t) for t in res.stdout.splitlines()[0].split()[1:]] == toks[:stop]
+
+
+@pytest.mark.gpu
+def test_cpp_handle_free_sample_token_amax(tmp_path, hip):
+    """The reference's argmax test (tests/test_sampling.cu) in C++: runtime-allocated buffers and
+    the handle-free sample_token_amax(d_logits, d_output) (sampling.cuh:4) on the torch.argmax
+    fixture rows (ties, NaN, signed zeros), each id bit-exact."""
+    from gpu_util import say
+    exe = build_manager(tmp_path, "sampling_main")
+    g = np.load(ROOT / "tests/golden/argmax_torch.npz")
+    for i, (row, want) in enumerate(zip(g["logits"], g["expect"])):
+        f = tmp_path / f"logits{i}.f32"
+        np.ascontiguousarray(row, dtype=np.float32).tofile(f)
+        say(f"C++ sample_token_amax, fixture row {i}")
+        res = subprocess.run([str(exe), str(f)], capture_output=True, text=True, timeout=120)
+        assert res.returncode == 0, res.stderr
+        assert int(res.stdout.split()[0]) == int(want), (i, res.stdout)

@@ -340,6 +340,42 @@ def test_batched_graph_replays_equal_eager(hip, ctx, model):
     torch.cuda.set_stream(ctx.stream)
 
 
+def test_closing_graphed_contexts_frees_their_batched_graphs(hip, ctx, model):
+    """Contexts that captured batched-step graphs (two batch compositions each) are created and
+    closed six times: the device memory in use returns to where it started (ie_context_destroy
+    destroys the cached graph executables with the context)."""
+    from infengine_amd.engine import Context, ptr
+    B, L = 4, 200
+    say("graphed batched contexts: create, step (2 captures), close x6")
+    kvs = torch.zeros(B * hip.lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+    toks = torch.zeros(B, 8192, dtype=torch.int32, device="cuda")
+    ws = torch.zeros(hip.lib.ie_batch_workspace_size(B), dtype=torch.uint8, device="cuda")
+    data = torch.zeros(B, 4096, dtype=torch.bfloat16, device="cuda")
+    attn = torch.zeros_like(data)
+    logits = torch.zeros(B, 128256, dtype=torch.float32, device="cuda")
+    out = torch.zeros(B, dtype=torch.int32, device="cuda")
+
+    def cycle():
+        c = Context(0, graph=True)
+        for nb in (B, 2, B):
+            seq = (C.c_int * nb)(*[L] * nb)
+            hip.check(hip.lib.ie_decode_step_batched(c.handle, model.ref(), nb, seq, ptr(toks),
+                                                     ptr(data), ptr(attn), ptr(logits), ptr(out),
+                                                     None, ptr(ws), ptr(kvs)))
+        torch.cuda.synchronize()
+        c.close()
+        torch.cuda.synchronize()
+
+    cycle()                                  # first-use allocations (module loads, pools)
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(6):
+        cycle()
+    grown = free0 - torch.cuda.mem_get_info()[0]
+    say(f"  device memory in use grew by {grown / 2**20:.2f} MiB over 6 cycles")
+    assert grown <= 4 << 20
+    torch.cuda.set_stream(ctx.stream)
+
+
 @pytest.mark.parametrize("lens", [[101, 257, 64], [2100, 257, 64], LENS16, LENS16_LONG])
 def test_batched_paged_equals_contiguous(hip, model, lens):
     """ie_decode_step_batched_paged on a page pool (the sequences' 64-position blocks scattered

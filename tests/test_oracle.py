@@ -231,6 +231,119 @@ def test_attention_matches_hf_repeat_kv():
     assert_close(out, ref, what="attention vs repeat_kv")
 
 
+def _attn_scores(q, kp, q_start, ctx, n_q):
+    """fp32 scores [32, n_q, ctx] (raw q.k, unscaled) with the causal mask as -inf."""
+    from transformers.models.llama.modeling_llama import repeat_kv
+    qt = t_bf16(q).float().permute(1, 0, 2)                          # [32, n_q, 128]
+    kt = repeat_kv(t_bf16(kp).float()[None], 4)[0]                   # [32, ctx, 128]
+    sc = qt @ kt.transpose(-1, -2)
+    pos = torch.arange(n_q)[:, None] + q_start
+    return sc.masked_fill(torch.arange(ctx)[None, :] > pos, float("-inf"))
+
+
+def _vrep(vp):
+    from transformers.models.llama.modeling_llama import repeat_kv
+    return repeat_kv(t_bf16(vp).float()[None], 4)[0]                 # [32, ctx, 128]
+
+
+def _heads_out(o, n_q):
+    return o.permute(1, 0, 2).reshape(n_q, 4096).numpy()
+
+
+def _assert_rounding_equal(got, ref, sc, vp, n_q, what):
+    """Equal up to rare flips of one probability's bf16 rounding: > 99% of elements bit-identical,
+    and every element within one ulp of the reference plus 2 x 2^-8 max_t p_t |v_t| (the shift one
+    flipped probability causes; the fp32 scores of two implementations differ in the last bits)."""
+    p = torch.softmax(sc.double() / np.sqrt(128.0), -1)                       # [32, n_q, ctx]
+    flip = _heads_out((p[..., None] * _vrep(vp).double().abs()[:, None]).amax(2), n_q)
+    g, w = orc.bf16_to_f32(got).astype(np.float64), orc.bf16_to_f32(ref).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(w), 1e-30))) - 7)
+    err = np.abs(g - w)
+    assert (err <= ulp + 2.0 ** -7 * flip).all(), f"{what}: worst {err.max():.3e}"
+    assert (got == ref).mean() > 0.99, f"{what}: {(got == ref).mean():.4f} exact"
+
+
+def test_attention_reference_rounding_point_matches_torch():
+    """PROB_REFERENCE: softmax in fp32, probabilities stored as bf16 (softmax.cu:105,158), then
+    the fp32 A.V product (attn.cu:167-204) rounded to bf16 -- torch's softmax, .to(bfloat16),
+    fp32 matmul.  The fp32 mode is measurably further from that reference than the rounded mode
+    is, so a mode that skipped the rounding would fail."""
+    ctx, q_start, n_q = 160, 130, 24
+    q = orc.synthetic((n_q, 32, 128), 81, 1, 0.0, 1.0)
+    kp = orc.synthetic((8, ctx, 128), 81, 2, 0.0, 1.0)
+    vp = orc.synthetic((8, ctx, 128), 81, 3, 0.0, 1.0)
+    sc = _attn_scores(q, kp, q_start, ctx, n_q)
+    p = torch.softmax(sc / np.sqrt(128.0), -1).to(torch.bfloat16).float()
+    ref = bits(torch.from_numpy(_heads_out(p @ _vrep(vp), n_q)))
+    with orc.prob_rounding(orc.PROB_REFERENCE):
+        got = orc.attention(q, kp, vp, q_start, ctx)
+    exact = orc.attention(q, kp, vp, q_start, ctx)
+    _assert_rounding_equal(got, ref, sc, vp, n_q, "reference rounding point")
+    assert (exact != ref).sum() > 5 * max(1, (got != ref).sum())
+
+
+def test_attention_flash_rounding_single_tile_closed_form():
+    """PROB_FLASH with every row's keys in one 64-key tile: out = bf16(sum_t p_t v_t * (1 / sum_t
+    p_t)), p_t = bf16(exp2((s_t - max s) log2(e) / sqrt(128))) (one max, no rescaling)."""
+    ctx, q_start, n_q = 64, 40, 24
+    q = orc.synthetic((n_q, 32, 128), 82, 1, 0.0, 1.0)
+    kp = orc.synthetic((8, ctx, 128), 82, 2, 0.0, 1.0)
+    vp = orc.synthetic((8, ctx, 128), 82, 3, 0.0, 1.0)
+    c = np.float32(np.log2(np.e) / np.sqrt(128.0))
+    sc = _attn_scores(q, kp, q_start, ctx, n_q)
+    e = torch.exp2((sc - sc.amax(-1, keepdim=True)) * c).to(torch.bfloat16).float()
+    ref = bits(torch.from_numpy(_heads_out((e @ _vrep(vp)) * (1.0 / e.sum(-1, keepdim=True)), n_q)))
+    with orc.prob_rounding(orc.PROB_FLASH):
+        got = orc.attention(q, kp, vp, q_start, ctx)
+    _assert_rounding_equal(got, ref, sc, vp, n_q, "flash rounding, one tile")
+
+
+def test_attention_flash_rounding_fixed_max_closed_form():
+    """PROB_FLASH over many tiles where key 0 holds every row's maximum score (k_0 = 8 q-ish):
+    the running max never moves after the first tile, so the tiled sums equal the one-max closed
+    form over all keys -- pins the accumulation across tiles and the causal extent."""
+    ctx, q_start, n_q = 300, 260, 16
+    q = orc.synthetic((n_q, 32, 128), 83, 1, 0.0, 0.5)
+    kp = orc.synthetic((8, ctx, 128), 83, 2, 0.0, 0.2)
+    vp = orc.synthetic((8, ctx, 128), 83, 3, 0.0, 1.0)
+    # dim 0 of every q row is 4 and key 0 is 3 e_0: its score 12 tops every row (others ~N(0, 1.4))
+    q[..., 0] = orc.f32_to_bf16(np.float32([4.0]))[0]
+    kp[:, 0] = 0
+    kp[:, 0, 0] = orc.f32_to_bf16(np.float32([3.0]))[0]
+    c = np.float32(np.log2(np.e) / np.sqrt(128.0))
+    sc = _attn_scores(q, kp, q_start, ctx, n_q)
+    assert torch.equal(sc.amax(-1), sc[..., 0]), "key 0 must hold every row's maximum"
+    e = torch.exp2((sc - sc[..., :1]) * c).to(torch.bfloat16).float()
+    ref = bits(torch.from_numpy(_heads_out((e @ _vrep(vp)) * (1.0 / e.sum(-1, keepdim=True)), n_q)))
+    with orc.prob_rounding(orc.PROB_FLASH):
+        got = orc.attention(q, kp, vp, q_start, ctx)
+    _assert_rounding_equal(got, ref, sc, vp, n_q, "flash rounding, fixed max")
+
+
+def test_attention_flash_rounding_within_its_error_bound():
+    """PROB_FLASH with growing maxima (rescaling on most tiles) stays within the bound that bf16
+    probabilities allow around the exact (fp32) attention: each p_t carries a relative error
+    <= 2^-9 in numerator and denominator alike, so |out - exact| <= 2^-8 sum p|v| / sum p plus
+    the two outputs' bf16 roundings; and it differs from the fp32 mode (the rounding is on)."""
+    ctx, q_start, n_q = 400, 330, 16
+    q = orc.synthetic((n_q, 32, 128), 84, 1, 0.0, 1.0)
+    kp = orc.synthetic((8, ctx, 128), 84, 2, 0.0, 1.0)
+    ramp = np.linspace(0.5, 3.0, ctx, dtype=np.float32)[None, :, None]   # scores grow with t
+    kp = orc.f32_to_bf16(orc.bf16_to_f32(kp) * ramp)
+    vp = orc.synthetic((8, ctx, 128), 84, 3, 0.0, 1.0)
+    sc = _attn_scores(q, kp, q_start, ctx, n_q).double() / np.sqrt(128.0)
+    p = torch.softmax(sc, -1)
+    va = _vrep(vp).double()
+    bound = _heads_out(2.0 ** -8 * (p @ va.abs()), n_q)
+    exact64 = _heads_out(p @ va, n_q)
+    with orc.prob_rounding(orc.PROB_FLASH):
+        got = orc.bf16_to_f32(orc.attention(q, kp, vp, q_start, ctx)).astype(np.float64)
+    fp32 = orc.attention(q, kp, vp, q_start, ctx)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact64), 1e-30))) - 7)
+    assert (np.abs(got - exact64) <= bound + ulp).all()
+    assert (orc.f32_to_bf16(got.astype(np.float32)) != fp32).mean() > 0.05
+
+
 # ---------------------------------------------------------------- decoder layer
 def _hf_layer(w):
     from transformers import LlamaConfig
