@@ -118,6 +118,7 @@ SIGNATURES: dict[str, tuple] = {
     "ie_attn_prefill_core_paged": (_i, [_p, _i, _i, _p, _p, _i, _p, _i, _p]),
     "ie_tune_gemv_waves": (_i, [_i]),
     "ie_tune_gemv_pairs_per_wave": (_i, [_i]),
+    "ie_tune_gemm_schedule": (_i, [_i]),
 }
 
 

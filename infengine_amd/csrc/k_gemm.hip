@@ -273,8 +273,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t w_group(const GemmParams& p, i
   const uint16_t* base;
   long long rows;
   if constexpr (EPI == kGemmSwiglu) {
-    // local row r -> [32 gate | 32 up] x 4; output column ntile*128 + (r/64)*32 + r%32
-    const int col = ntile * 128 + (r >> 6) * 32 + (r & 31);
+    // local row r -> [32 gate | 32 up] x (BN / 64); output column ntile*BN/2 + (r/64)*32 + r%32
+    const int col = ntile * (BN / 2) + (r >> 6) * 32 + (r & 31);
     base = ((r & 63) < 32 ? p.w0 : p.w1) + (size_t)col * p.K;
     rows = p.N - col;
   } else {
@@ -454,6 +454,123 @@ __device__ __forceinline__ int swz_out(int u, int r) {
   return u ^ (r & 31);
 }
 
+// The epilogue of a 256- or 192-row W tile: wave (wn, wm) of k-group kg holds accumulator element
+// 4*g + q of tile (i, j) = W row wn*WTN + 32*i + 8*g + 4*(lane/32) + q, X row m0 + wm*64 + 32*j +
+// lane%32 (k-group 0 holds the sums).  fp32 results go straight to global memory; bf16 ones are
+// staged through the LDS ring as a [BM][OUTN] tile and stored as whole row segments.
+// Copy-out of a bf16 output tile staged in LDS as [BM][UPR] 8-byte units (unit u of row r at
+// swz(u, r)): 16 bytes (8 columns) per thread, consecutive threads along a row; the residual
+// epilogue adds the tile to y.
+template <int THREADS, int BM, int UPR, int EPI, class SW>
+__device__ __forceinline__ void tile_copy_out(const GemmParams& p, const uint2* ot, uint16_t* y,
+                                              int m0, int n_base, int tid, SW swz) {
+  const bool ld16 = (p.ldy & 7) == 0;  // rows 16-byte aligned: one 16-byte store per thread
+#pragma unroll 4
+  for (int P = tid; P < BM * UPR / 2; P += THREADS) {
+    const int r = P / (UPR / 2), c2 = P % (UPR / 2);
+    const int m = m0 + r, n = n_base + 8 * c2;
+    if (m >= p.M || n >= p.N) continue;
+    const uint2 lo = ot[r * UPR + swz(2 * c2, r)], hi = ot[r * UPR + swz(2 * c2 + 1, r)];
+    uint16_t* dst = y + (size_t)m * p.ldy + n;
+    if constexpr (EPI == kGemmResid) {
+      // y = bf16(y + bf16(acc)) (residual_add.cu:17-19); the LDS tile holds bf16(acc)
+      const uint2 a = *reinterpret_cast<const uint2*>(dst);
+      const uint2 o0 = make_uint2(pack_bf2(bf_lo(a.x) + bf_lo(lo.x), bf_hi(a.x) + bf_hi(lo.x)),
+                                  pack_bf2(bf_lo(a.y) + bf_lo(lo.y), bf_hi(a.y) + bf_hi(lo.y)));
+      if (n + 8 <= p.N) {
+        const uint2 b = *reinterpret_cast<const uint2*>(dst + 4);
+        const uint2 o1 = make_uint2(pack_bf2(bf_lo(b.x) + bf_lo(hi.x), bf_hi(b.x) + bf_hi(hi.x)),
+                                    pack_bf2(bf_lo(b.y) + bf_lo(hi.y), bf_hi(b.y) + bf_hi(hi.y)));
+        store16(dst, o0, o1, ld16);
+      } else {
+        *reinterpret_cast<uint2*>(dst) = o0;
+      }
+    } else {
+      if (n + 8 <= p.N) store16(dst, lo, hi, ld16);
+      else *reinterpret_cast<uint2*>(dst) = lo;
+    }
+  }
+}
+
+template <int UPR>
+struct WideOutSwz {
+  __device__ __forceinline__ int operator()(int u, int r) const { return swz_out<UPR>(u, r); }
+};
+
+template <class C, int EPI>
+__device__ __forceinline__ void wide_epilogue(const GemmParams& p, f32x16_t (&acc)[C::NI][2],
+                                              u32x4_t* lds, uint16_t* y, float* yf, int m0,
+                                              int ntile, int kg, int wn, int wm, int lane,
+                                              int tid) {
+  constexpr int BM = C::BM, BN = C::BN, STAGES = C::STAGES;
+  const int fr = lane & 31, fh = lane >> 5;
+  if constexpr (EPI == kGemmF32) {
+    if (kg != 0) return;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int m = m0 + wm * 64 + j * 32 + fr;
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = ntile * BN + wn * C::WTN + i * 32 + 8 * g + 4 * fh;
+          if (n < p.N)
+            *reinterpret_cast<float4*>(yf + (size_t)m * p.ldy + n) =
+                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        }
+    }
+  } else {
+    // bf16 results go through LDS so that the global stores are whole, coalesced row segments
+    // (a lane's accumulators are 4 columns of 32 different rows; storing them directly writes
+    // every 128-byte line in eight 16-byte pieces).  The tile is [BM][OUTN] bf16 held as
+    // 8-byte units; unit u of row r sits at swz_out(u, r), which spreads the 32 rows one
+    // write instruction touches over distinct banks without padding.
+    constexpr int OUTN = (EPI == kGemmSwiglu) ? 128 : BN;  // output columns per tile
+    constexpr int UPR = OUTN / 4;                            // 8-byte units per row
+    static_assert(BM * OUTN * 2 <= STAGES * C::STAGE * 16, "output tile must fit the LDS ring");
+    uint2* ot = reinterpret_cast<uint2*>(lds);
+    __syncthreads();  // every wave is done reading the ring
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (kg != 0) break;
+      const int r = wm * 64 + j * 32 + fr;
+      if constexpr (EPI == kGemmSwiglu) {
+#pragma unroll
+        for (int i = 0; i < 4; i += 2)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            uint32_t o[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              float v[2];
+#pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const float gt = bf2f(f2bf(acc[i][j][4 * g + 2 * q + e]));
+                const float up = bf2f(f2bf(acc[i + 1][j][4 * g + 2 * q + e]));
+                v[e] = gt * (1.0f / (1.0f + expf(-gt))) * up;
+              }
+              o[q] = pack_bf2(v[0], v[1]);
+            }
+            const int u = (2 * wn + i / 2) * 8 + 2 * g + fh;
+            ot[r * UPR + swz_out<UPR>(u, r)] = make_uint2(o[0], o[1]);
+          }
+      } else {
+#pragma unroll
+        for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int u = wn * (C::WTN / 4) + i * 8 + 2 * g + fh;
+            ot[r * UPR + swz_out<UPR>(u, r)] = make_uint2(pack_bf2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+                                                pack_bf2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]));
+          }
+      }
+    }
+    __syncthreads();
+    tile_copy_out<C::THREADS, BM, UPR, EPI>(p, ot, y, m0, ntile * OUTN, tid, WideOutSwz<UPR>{});
+  }
+}
+
 template <int EPI, int BM, int BK, int STAGES, int MAPG, int BN, int KG>
 __global__ __launch_bounds__(2 * BM * KG) __attribute__((amdgpu_waves_per_eu(BM * KG / 128, BM * KG / 128)))
 void gemm_wide_kernel(GemmParams p, int m_tiles) {
@@ -559,101 +676,331 @@ void gemm_wide_kernel(GemmParams p, int m_tiles) {
     }
   }
 
-  // ---- epilogue: accumulator element 4*g + q of tile (i, j) is
-  //      W row wn*WTN + 32*i + 8*g + 4*(lane/32) + q,  X row m0 + wm*64 + 32*j + lane%32
-  if constexpr (EPI == kGemmF32) {
-    if (kg != 0) return;
+  wide_epilogue<C, EPI>(p, acc, lds, y, yf, m0, ntile, kg, wn, wm, lane, tid);
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong kernel for the 256 x 256 (or 192 W x 256 X) tile on v_mfma_f32_16x16x32_bf16.
+//
+// The part runs these GEMMs power-limited: the same kernels on all-zero operands run 25-35%
+// faster, and on random data a stream of 32x32x16 MFMAs alone (no LDS reads, loads or
+// barriers) reached 0.58-0.61 of the nominal peak where the same flops as 16x16x32 MFMAs
+// reached 0.61-0.66 (a 16x16x32 MFMA reads and writes a quarter of the accumulators for half
+// the flops).  So this kernel runs 16x16x32 MFMAs, and keeps every SIMD's matrix core fed from
+// registers:
+//
+// The two waves that share a SIMD (wave w and w + 4) alternate between a compute phase -- one
+// k-step (64 k) of MFMAs from fragments already in registers, 64 (48) back to back -- and a
+// memory phase -- the 24 (20) ds_read_b128 of their next k-step's fragments plus their share
+// of the direct-to-LDS loads of a later stage.  Group 0 (waves 0-3) owns W rows 0 .. WTN-1 of
+// the tile and loads the W half of every stage; group 1 (waves 4-7) owns W rows WTN .. and
+// loads the X half; wave 4 g + q owns X rows 64 q .. +63.  Group 1 runs one phase behind group
+// 0, and every phase ends at a workgroup barrier:
+//   phase 2k+1: group 0 multiplies k-step k; group 1 reads k-step k's fragments (ring slot k%2);
+//               every wave waits for its loads of stage k+1 (issued in phase 2k) first
+//   phase 2k+2: group 0 reads k-step k+1's fragments (slot (k+1)%2), then issues the W half of
+//               stage k+2 into slot k%2; group 1 issues the X half of stage k+2 into slot k%2
+//               between its first MFMAs of k-step k
+// Slot k%2 is free in phase 2k+2: its last readers (group 1, phase 2k+1) waited for their reads
+// before the barrier that ended that phase; a memory phase reads a stage every wave waited for
+// before the barrier that started the phase.  Each group runs a loop of its own (s_barrier
+// syncs the workgroup wherever each wave executes it), so each role's registers are allocated
+// on their own.
+//
+// MFMA operands: A = 16 W rows, B = 16 X rows, k 32: lane l supplies row l % 16 at k chunk
+// 4 ks + l / 16 of the 64-k stage (ks = 0, 1), so D[w][x] puts output row x = l % 16 and output
+// columns w = 4 (l / 16) .. +3 in a lane: an 8-byte unit.  LDS chunk slot s of row r holds
+// global chunk s ^ swz(r), swz(r) = (r >> 1) & 7: the 16 rows of one chunk a fragment read
+// touches fall in 16 distinct 16-byte bank groups (and, with the next chunk's 16, in 32 of a
+// 512-byte LDS line).  swz does not depend on a fragment's 16-row block, so a lane's fragment
+// offsets are base ^ (ks << 6) plus immediates of 2048 bytes per block.
+namespace pp {
+
+// Tile: BN W rows x BM X rows x 64 k per stage.  BM = 256 (KG = 1): the two wave groups split the
+// W rows.  BM = 128 (KG = 2): each group owns the whole tile and multiplies one k32 half of every
+// stage, and group 1's sums are added to group 0's through LDS at the end.
+template <int BN_, int BM_>
+struct PC {
+  static constexpr int BN = BN_, BM = BM_, BK = 64;
+  static constexpr int KG = BM == 256 ? 1 : 2;
+  static constexpr int KS = 2 / KG;            // k32 sub-steps a wave multiplies per stage
+  static constexpr int WTN = BN / 2;           // W rows per wave
+  static constexpr int NA = WTN / 16;          // 16-row W blocks per wave (8 or 6)
+  static constexpr int NB = 4;                 // 16-row X blocks per wave (64 X rows)
+  static constexpr int CPR = 8;                // 16-byte chunks per tile row
+  static constexpr int W_CHUNKS = BN * CPR;    // one stage's W half
+  static constexpr int X_CHUNKS = BM * CPR;    // one stage's X half
+  static constexpr int WL = W_CHUNKS / 64 / 4; // W loads per group-0 wave per stage
+  static constexpr int XL = X_CHUNKS / 64 / 4; // X loads per group-1 wave per stage
+  static constexpr int PL = WL > XL ? WL : XL;
+  // The W and X halves have rings of their own: 3 W slots (the W rows come from HBM; stage
+  // k + 3 is issued four phases before it is read), and 3 X slots where they fit beside them
+  // in the 160 KiB of LDS, else 2.  X slots follow the W slots.
+  static constexpr int NW = 3;
+  static constexpr int NX = (NW * W_CHUNKS + 3 * X_CHUNKS) * 16 <= 160 * 1024 ? 3 : 2;
+  static constexpr int X_BASE = NW * W_CHUNKS;  // chunk offset of X slot 0
+  static constexpr int TOTAL = NW * W_CHUNKS + NX * X_CHUNKS;
+  static_assert(BM == 256 || (BM == 128 && BN == 256), "tile shapes");
+  static_assert(TOTAL * 16 <= 160 * 1024, "LDS");
+  static __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+};
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Load j of a wave's stage share (8 tile rows) into LDS chunk base + 256 j (base: the ring slot's
+// first chunk plus the wave's first 8-row group).
+template <int NL>
+__device__ __forceinline__ void issue(u32x4_t* lds, const __amdgpu_buffer_rsrc_t* rs,
+                                      const uint32_t* vo, int base, int kt) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int m = m0 + wm * 64 + j * 32 + fr;
-      if (m >= p.M) continue;
+  for (int j = 0; j < NL; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs[j], (lds_void*)&lds[base + 256 * j], 16, vo[j],
+                                             (uint32_t)(kt * 128), 0, 0);
+}
+
+// All fragments of one k-step: the W half at LDS byte offset sa, the X half at sb.
+template <class C>
+__device__ __forceinline__ void read(const u32x4_t* lds, uint32_t sa, uint32_t sb, uint32_t aA,
+                                     uint32_t aB, bf16x8_t (&fa)[C::KS][C::NA],
+                                     bf16x8_t (&fb)[C::KS][C::NB]) {
+  const char* base = reinterpret_cast<const char*>(lds);
+  uint32_t a0 = sa + aA, b0 = sb + aB;
+  // (computed here, at the reads: hoisted out of the k loop the offsets of both ring slots
+  // would stay live through the MFMAs)
+  asm volatile("" : "+v"(a0), "+v"(b0));
 #pragma unroll
-      for (int i = 0; i < C::NI; ++i)
+  for (int ks = 0; ks < C::KS; ++ks) {
+    const char* pa = base + (a0 ^ (uint32_t)(ks << 6));
+    const char* pb = base + (b0 ^ (uint32_t)(ks << 6));
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = ntile * BN + wn * C::WTN + i * 32 + 8 * g + 4 * fh;
-          if (n < p.N)
-            *reinterpret_cast<float4*>(yf + (size_t)m * p.ldy + n) =
-                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-        }
+    for (int i = 0; i < C::NA; ++i) fa[ks][i] = *reinterpret_cast<const bf16x8_t*>(pa + i * 2048);
+#pragma unroll
+    for (int j = 0; j < C::NB; ++j) fb[ks][j] = *reinterpret_cast<const bf16x8_t*>(pb + j * 2048);
+  }
+}
+
+// One k-step of MFMAs at raised wave priority; with DMA this wave's loads of stage kt into
+// `slot` go out one after each of the first NL MFMAs.
+template <class C, int NL, bool DMA>
+__device__ __forceinline__ void compute(f32x4_t (&acc)[C::NA][C::NB], const bf16x8_t (&fa)[C::KS][C::NA],
+                                        const bf16x8_t (&fb)[C::KS][C::NB], u32x4_t* lds,
+                                        const __amdgpu_buffer_rsrc_t* rs, const uint32_t* vo,
+                                        int base, int kt) {
+  asm volatile("s_setprio 2" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks)
+#pragma unroll
+    for (int i = 0; i < C::NA; ++i)
+#pragma unroll
+      for (int j = 0; j < C::NB; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+        const int n = (ks * C::NA + i) * C::NB + j;
+        if (DMA && n < NL)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs[n], (lds_void*)&lds[base + 256 * n], 16, vo[n],
+                                                   (uint32_t)(kt * 128), 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  asm volatile("s_setprio 0" ::: "memory");
+}
+
+// Output staging swizzle (a bijection of a row's units): 8-byte unit u of row r at
+// u ^ ((r & 15) << 2) (64 units a row), u ^ ((r & 7) << 2) (32), u ^ ((r & 3) << 2) (16), and for
+// 48 the 32-unit form within the first 32 units and the 16-unit form in the last 16; a write
+// instruction covers 16 rows x 4 consecutive units.
+template <int UPR>
+struct OutSwz {
+  static_assert(UPR == 64 || UPR == 48 || UPR == 32 || UPR == 16, "units per row");
+  __device__ __forceinline__ int operator()(int u, int r) const {
+    if constexpr (UPR == 64) return u ^ ((r & 15) << 2);
+    else if constexpr (UPR == 32) return u ^ ((r & 7) << 2);
+    else if constexpr (UPR == 16) return u ^ ((r & 3) << 2);
+    else return u < 32 ? u ^ ((r & 7) << 2) : u ^ ((r & 3) << 2);
+  }
+};
+
+template <int EPI, int BN, int BM>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_pp_kernel(GemmParams p, int m_tiles) {
+  using C = PC<BN, BM>;
+  constexpr int NA = C::NA, NB = C::NB, WL = C::WL, XL = C::XL, PL = C::PL, KS = C::KS;
+  static_assert(EPI == kGemmBf16 || EPI == kGemmResid || EPI == kGemmSwiglu, "bf16 epilogues");
+  static_assert(EPI != kGemmSwiglu || BN == 256, "SwiGLU tiles are 256 W rows");
+  __shared__ u32x4_t lds[C::TOTAL];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wv >> 2, gw = wv & 3;
+  // the wave's output block: W rows wn * WTN .., X rows wm * 64 ..; with KG = 2 its k32 half grp
+  const int wn = C::KG == 1 ? grp : gw >> 1, wm = C::KG == 1 ? gw : gw & 1;
+  int mtile, ntile;
+  tile_of<1>(blockIdx.x, gridDim.x, m_tiles, mtile, ntile);
+  const int m0 = mtile * BM;
+  const int KT = p.K / 64;
+
+  // this wave's share of a stage: 8-row groups gw + 4 j of its half (W or X); lane i fills LDS
+  // slot (row 8 g + i / 8, chunk i % 8) from global chunk (i % 8) ^ swz(row)
+  __amdgpu_buffer_rsrc_t rs[PL];
+  uint32_t vo[PL];
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int g = gw + 4 * j;
+    rs[j] = grp == 0 ? w_group<EPI, BN>(p, ntile, min(g, BN / 8 - 1) * 8) : x_group(p, m0, g * 8);
+    const int rl = lane / 8, c = (lane % 8) ^ C::swz(g * 8 + rl);
+    vo[j] = (uint32_t)((rl * p.K + c * 8) * 2);
+  }
+  const int dst0 = (grp == 0 ? 0 : C::X_BASE) + gw * 64;  // the wave's first row group, slot 0
+  const int slot_chunks = grp == 0 ? C::W_CHUNKS : C::X_CHUNKS;
+
+  f32x4_t acc[NA][NB];
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // fragment byte offsets within a stage (ks = 0, block 0): lane l reads row base + l % 16 at
+  // chunk (l / 16) ^ swz(row)
+  const int fr = lane & 15, fq = lane >> 4;
+  const uint32_t chunk0 = (uint32_t)((fq ^ C::swz(fr)) * 16) ^ (C::KG == 2 ? (uint32_t)(grp << 6) : 0u);
+  const uint32_t aA = (uint32_t)((wn * C::WTN + fr) * C::CPR * 16) + chunk0;
+  const uint32_t aB = (uint32_t)((wm * 64 + fr) * C::CPR * 16) + chunk0;
+  bf16x8_t fa[KS][NA], fb[KS][NB];
+
+  uint16_t* const y = p.y;
+  asm volatile("" ::"s"(y), "s"(p.ldy), "s"(p.M), "s"(p.N));
+
+  // stage k's W half lives in W slot k % NW, its X half in X slot k % NX.  The wait that ends
+  // phase 2k+1 leaves in flight only this wave's loads of stages issued after k+1.
+  constexpr int NW = C::NW, NX = C::NX;
+  constexpr uint32_t WSB = C::W_CHUNKS * 16, XSB = C::X_CHUNKS * 16, XB0 = C::X_BASE * 16;
+  if (grp == 0) {
+#pragma unroll
+    for (int t = 0; t < NW; ++t)
+      if (t < KT) issue<WL>(lds, rs, vo, dst0 + t * C::W_CHUNKS, t);
+    if (KT >= NW) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NW - 1) * WL) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    // phase 0: fragments of k-step 0
+    read<C>(lds, 0, XB0, aA, aB, fa, fb);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    int sw = 0, sx = 0;  // W and X slots of stage k
+#pragma unroll 1
+    for (int k = 0; k < KT; ++k) {
+      const int swn = sw + 1 == NW ? 0 : sw + 1, sxn = sx + 1 == NX ? 0 : sx + 1;
+      // phase 2k+1: multiply k-step k
+      compute<C, WL, false>(acc, fa, fb, lds, rs, vo, 0, 0);
+      if (k + 2 < KT) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NW - 2) * WL) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      // phase 2k+2: fragments of k-step k+1, then the W half of stage k+NW into W slot sw
+      if (k + 1 < KT) read<C>(lds, swn * WSB, XB0 + sxn * XSB, aA, aB, fa, fb);
+      if (k + NW < KT) issue<WL>(lds, rs, vo, dst0 + sw * C::W_CHUNKS, k + NW);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      sw = swn;
+      sx = sxn;
     }
   } else {
-    // bf16 results go through LDS so that the global stores are whole, coalesced row segments
-    // (a lane's accumulators are 4 columns of 32 different rows; storing them directly writes
-    // every 128-byte line in eight 16-byte pieces).  The tile is [BM][OUTN] bf16 held as
-    // 8-byte units; unit u of row r sits at swz_out(u, r), which spreads the 32 rows one
-    // write instruction touches over distinct banks without padding.
-    constexpr int OUTN = (EPI == kGemmSwiglu) ? 128 : BN;  // output columns per tile
-    constexpr int UPR = OUTN / 4;                            // 8-byte units per row
-    static_assert(BM * OUTN * 2 <= STAGES * C::STAGE * 16, "output tile must fit the LDS ring");
-    uint2* ot = reinterpret_cast<uint2*>(lds);
-    __syncthreads();  // every wave is done reading the ring
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (kg != 0) break;
-      const int r = wm * 64 + j * 32 + fr;
-      if constexpr (EPI == kGemmSwiglu) {
-#pragma unroll
-        for (int i = 0; i < 4; i += 2)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            uint32_t o[2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              float v[2];
-#pragma unroll
-              for (int e = 0; e < 2; ++e) {
-                const float gt = bf2f(f2bf(acc[i][j][4 * g + 2 * q + e]));
-                const float up = bf2f(f2bf(acc[i + 1][j][4 * g + 2 * q + e]));
-                v[e] = gt * (1.0f / (1.0f + expf(-gt))) * up;
-              }
-              o[q] = pack_bf2(v[0], v[1]);
-            }
-            const int u = (2 * wn + i / 2) * 8 + 2 * g + fh;
-            ot[r * UPR + swz_out<UPR>(u, r)] = make_uint2(o[0], o[1]);
-          }
-      } else {
-#pragma unroll
-        for (int i = 0; i < C::NI; ++i)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int u = wn * (C::WTN / 4) + i * 8 + 2 * g + fh;
-            ot[r * UPR + swz_out<UPR>(u, r)] = make_uint2(pack_bf2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
-                                                pack_bf2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]));
-          }
-      }
+    for (int t = 0; t < NX; ++t)
+      if (t < KT) issue<XL>(lds, rs, vo, dst0 + t * C::X_CHUNKS, t);
+    if (KT >= NX) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NX - 1) * XL) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    int k = 0, sw = 0, sx = 0;
+#pragma unroll 1
+    for (; k + NX < KT; ++k) {
+      // phase 2k+1: fragments of k-step k
+      read<C>(lds, sw * WSB, XB0 + sx * XSB, aA, aB, fa, fb);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NX - 2) * XL) : "memory");
+      // phase 2k+2: the X half of stage k+NX into X slot sx while multiplying k-step k
+      compute<C, XL, true>(acc, fa, fb, lds, rs, vo, dst0 + sx * C::X_CHUNKS, k + NX);
+      asm volatile("s_barrier" ::: "memory");
+      sw = sw + 1 == NW ? 0 : sw + 1;
+      sx = sx + 1 == NX ? 0 : sx + 1;
     }
-    __syncthreads();
-    // copy-out: 16 bytes (8 columns) per thread, consecutive threads along a row
-    const int n_base = ntile * OUTN;
-    const bool ld16 = (p.ldy & 7) == 0;  // rows 16-byte aligned: one 16-byte store per thread
-#pragma unroll 4
-    for (int P = tid; P < BM * UPR / 2; P += C::THREADS) {
-      const int r = P / (UPR / 2), c2 = P % (UPR / 2);
-      const int m = m0 + r, n = n_base + 8 * c2;
-      if (m >= p.M || n >= p.N) continue;
-      const uint2 lo = ot[r * UPR + swz_out<UPR>(2 * c2, r)], hi = ot[r * UPR + swz_out<UPR>(2 * c2 + 1, r)];
-      uint16_t* dst = y + (size_t)m * p.ldy + n;
-      if constexpr (EPI == kGemmResid) {
-        // y = bf16(y + bf16(acc)) (residual_add.cu:17-19); the LDS tile holds bf16(acc)
-        const uint2 a = *reinterpret_cast<const uint2*>(dst);
-        const uint2 o0 = make_uint2(pack_bf2(bf_lo(a.x) + bf_lo(lo.x), bf_hi(a.x) + bf_hi(lo.x)),
-                                    pack_bf2(bf_lo(a.y) + bf_lo(lo.y), bf_hi(a.y) + bf_hi(lo.y)));
-        if (n + 8 <= p.N) {
-          const uint2 b = *reinterpret_cast<const uint2*>(dst + 4);
-          const uint2 o1 = make_uint2(pack_bf2(bf_lo(b.x) + bf_lo(hi.x), bf_hi(b.x) + bf_hi(hi.x)),
-                                      pack_bf2(bf_lo(b.y) + bf_lo(hi.y), bf_hi(b.y) + bf_hi(hi.y)));
-          store16(dst, o0, o1, ld16);
-        } else {
-          *reinterpret_cast<uint2*>(dst) = o0;
-        }
-      } else {
-        if (n + 8 <= p.N) store16(dst, lo, hi, ld16);
-        else *reinterpret_cast<uint2*>(dst) = lo;
+#pragma unroll 1
+    for (; k < KT; ++k) {
+      read<C>(lds, sw * WSB, XB0 + sx * XSB, aA, aB, fa, fb);
+      if (k + 2 < KT)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NX - 2) * XL) : "memory");
+      else
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      compute<C, XL, false>(acc, fa, fb, lds, rs, vo, 0, 0);
+      asm volatile("s_barrier" ::: "memory");
+      sw = sw + 1 == NW ? 0 : sw + 1;
+      sx = sx + 1 == NX ? 0 : sx + 1;
+    }
+  }
+  (void)slot_chunks;
+
+  // ---- epilogue: acc[i][j][r] = D[W row wn*WTN + 16 i + 4 (lane/16) + r][X row wm*64 + 16 j +
+  //      lane%16]; staged in the ring as [256][OUTN] bf16 (8-byte units), then stored as rows
+  if constexpr (C::KG == 2) {
+    // group 1 hands its sums to group 0 through the ring, half the W blocks at a time (a lane's
+    // 16-byte accumulators lane-contiguous: conflict-free)
+    constexpr int HALF = NA / 2 * NB;
+    static_assert(4 * HALF * 64 * 16 <= C::TOTAL * 16, "reduction fits the ring");
+    f32x4_t* red = reinterpret_cast<f32x4_t*>(lds) + (size_t)gw * HALF * 64 + lane;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      __syncthreads();  // the ring (or the previous half) is free
+      if (grp == 1) {
+#pragma unroll
+        for (int i = 0; i < NA / 2; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j) red[(i * NB + j) * 64] = acc[h * NA / 2 + i][j];
+      }
+      __syncthreads();
+      if (grp == 0) {
+#pragma unroll
+        for (int i = 0; i < NA / 2; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j) acc[h * NA / 2 + i][j] += red[(i * NB + j) * 64];
       }
     }
   }
+  constexpr int OUTN = (EPI == kGemmSwiglu) ? BN / 2 : BN;
+  constexpr int UPR = OUTN / 4;
+  static_assert(BM * OUTN * 2 <= C::TOTAL * 16, "output tile must fit the LDS ring");
+  const OutSwz<UPR> swz;
+  uint2* ot = reinterpret_cast<uint2*>(lds);
+  __syncthreads();  // every wave is done reading the ring
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    if (C::KG == 2 && grp != 0) break;
+    const int r = wm * 64 + 16 * j + fr;
+    if constexpr (EPI == kGemmSwiglu) {
+      // W rows of the wave: [32 gate | 32 up] x 2, so block i (gate) pairs with i + 2 (up)
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        if ((i & 2) != 0) continue;
+        uint32_t o[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          float v[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float gt = bf2f(f2bf(acc[i][j][2 * q + e]));
+            const float up = bf2f(f2bf(acc[i + 2][j][2 * q + e]));
+            v[e] = gt * (1.0f / (1.0f + expf(-gt))) * up;
+          }
+          o[q] = pack_bf2(v[0], v[1]);
+        }
+        const int u = (wn * (C::WTN / 64) + i / 4) * 8 + (i & 1) * 4 + fq;
+        ot[r * UPR + swz(u, r)] = make_uint2(o[0], o[1]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int u = wn * (C::WTN / 4) + 4 * i + fq;
+        ot[r * UPR + swz(u, r)] = make_uint2(pack_bf2(acc[i][j][0], acc[i][j][1]),
+                                             pack_bf2(acc[i][j][2], acc[i][j][3]));
+      }
+    }
+  }
+  __syncthreads();
+  tile_copy_out<512, BM, UPR, EPI>(p, ot, y, m0, ntile * OUTN, tid, swz);
 }
+
+}  // namespace pp
 
 }  // namespace wide
 
@@ -665,6 +1012,18 @@ int launch_wide(const GemmParams& p, hipStream_t st) {
   IE_REQUIRE(blocks <= 0x7fffffff, "gemm: too many tiles");
   hipLaunchKernelGGL((wide::gemm_wide_kernel<EPI, BM, BK, STAGES, MAPG, WBN, KG>), dim3((unsigned)blocks),
                      dim3(wide::Cfg<BM, BK, STAGES, WBN, KG>::THREADS), 0, st, p, m_tiles);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+template <int EPI, int WBN, int XBM = 256>
+int launch_pp(const GemmParams& p, hipStream_t st) {
+  const int m_tiles = (p.M + XBM - 1) / XBM;
+  const int n_tiles = (EPI == kGemmSwiglu) ? (p.N + WBN / 2 - 1) / (WBN / 2) : (p.N + WBN - 1) / WBN;
+  const long long blocks = (long long)m_tiles * n_tiles;
+  IE_REQUIRE(blocks <= 0x7fffffff && p.k_splits <= 1, "gemm: ping-pong tiles");
+  hipLaunchKernelGGL((wide::pp::gemm_pp_kernel<EPI, WBN, XBM>), dim3((unsigned)blocks), dim3(512), 0,
+                     st, p, m_tiles);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
@@ -687,6 +1046,11 @@ int launch_e(const GemmParams& p, hipStream_t st) {
 // chip; at small S the 128 x 128 tile keeps more CUs busy.  192 W rows x 256 X rows gives
 // exactly 256 tiles for the QKV projection at S = 2048 (N = 6144).
 enum { kTileSmall, kTileWide, kTileBig, kTileBig192, kTileKinds };
+
+// Kernel of the bf16 wide tiles: 0 = the DMA-ring wide kernels; 1 = the ping-pong kernel for
+// the 256-row X tiles; 2 (default) = the ping-pong kernel for those and for the 128-row X tiles.
+// Outputs are bit-identical across the three (same per-accumulator MFMA order).
+int g_gemm_schedule = 2;
 
 struct TileKind {
   int tm, tn, tn_swiglu;  // X rows, output columns (plain / SwiGLU) per tile
@@ -718,6 +1082,13 @@ double tile_cost(int kind, int epi, int M, int N) {
 }
 
 int launch_kind(int kind, int epi, const GemmParams& p, hipStream_t st) {
+  if (g_gemm_schedule == 2 && kind == kTileWide && epi != kGemmF32) {
+    switch (epi) {
+      case kGemmBf16: return launch_pp<kGemmBf16, 256, 128>(p, st);
+      case kGemmResid: return launch_pp<kGemmResid, 256, 128>(p, st);
+      case kGemmSwiglu: return launch_pp<kGemmSwiglu, 256, 128>(p, st);
+    }
+  }
   switch (kind * 4 + epi) {
     case kTileSmall * 4 + kGemmBf16: return launch_e<kGemmBf16>(p, st);
     case kTileSmall * 4 + kGemmResid: return launch_e<kGemmResid>(p, st);
@@ -727,6 +1098,17 @@ int launch_kind(int kind, int epi, const GemmParams& p, hipStream_t st) {
     case kTileWide * 4 + kGemmResid: return launch_wide<kGemmResid, 128, 64, 3, 1, 256, 2>(p, st);
     case kTileWide * 4 + kGemmF32: return launch_wide<kGemmF32, 128, 64, 3, 1, 256, 2>(p, st);
     case kTileWide * 4 + kGemmSwiglu: return launch_wide<kGemmSwiglu, 128, 64, 3, 1, 256, 2>(p, st);
+  }
+  if (g_gemm_schedule >= 1) {
+    switch (kind * 4 + epi) {
+      case kTileBig * 4 + kGemmBf16: return launch_pp<kGemmBf16, 256>(p, st);
+      case kTileBig * 4 + kGemmResid: return launch_pp<kGemmResid, 256>(p, st);
+      case kTileBig * 4 + kGemmSwiglu: return launch_pp<kGemmSwiglu, 256>(p, st);
+      case kTileBig192 * 4 + kGemmBf16: return launch_pp<kGemmBf16, 192>(p, st);
+      case kTileBig192 * 4 + kGemmResid: return launch_pp<kGemmResid, 192>(p, st);
+    }
+  }
+  switch (kind * 4 + epi) {
     case kTileBig * 4 + kGemmBf16: return launch_wide<kGemmBf16, 256, 64, 2>(p, st);
     case kTileBig * 4 + kGemmResid: return launch_wide<kGemmResid, 256, 64, 2>(p, st);
     case kTileBig * 4 + kGemmSwiglu: return launch_wide<kGemmSwiglu, 256, 64, 2>(p, st);
@@ -931,3 +1313,9 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
 }
 
 }  // namespace ie
+
+extern "C" int ie_tune_gemm_schedule(int schedule) {
+  IE_REQUIRE(schedule >= 0 && schedule <= 2, "tune_gemm_schedule: %d not in [0, 2]", schedule);
+  ie::g_gemm_schedule = schedule;
+  return IE_OK;
+}

@@ -346,6 +346,36 @@ def test_gemm_epilogues(hip, ctx, epi, m, n):
                       outlier_frac=1e-3 if epi == "resid" else 0.0)
 
 
+# ragged rows and columns on every tile kind: 256 x 256 and 192 x 256 (QKV split points at
+# 4096 / 5120), 256 x 128 (two k-groups), SwiGLU with a column-split launch
+@pytest.mark.parametrize("epi,m,k,n", [("bf16", 300, 4096, 6144), ("resid", 1300, 4096, 4096),
+                                       ("resid", 2048, 14336, 4096), ("swiglu", 700, 4096, 14336),
+                                       ("swiglu", 2048, 4096, 14336), ("bf16", 2048, 4096, 6144),
+                                       ("bf16", 555, 4096, 1000)])
+def test_gemm_schedules_bit_identical(hip, ctx, epi, m, k, n):
+    """The prefill GEMM's three tile schedules (ie_tune_gemm_schedule: the DMA-ring kernels, the
+    ping-pong kernel for 256-row tiles, for all bf16 tiles) give identical bits: the MFMAs of every
+    accumulator run in the same k order."""
+    say(f"gemm schedules {epi} m={m} k={k} n={n}")
+    x = dev(orc.synthetic((m, k), 31, m, 0.0, 1.0))
+    w0 = dev(orc.synthetic((n, k), 31, n + 1, 0.0, 0.02))
+    w1 = dev(orc.synthetic((n, k), 31, n + 2, 0.0, 0.02))
+    y0 = dev(orc.synthetic((m, n), 31, n + 3, 0.0, 1.0))
+    outs = []
+    try:
+        for sched in (0, 1, 2):
+            hip.check(hip.lib.ie_tune_gemm_schedule(sched))
+            out = y0.clone()
+            hip.check(hip.lib.ie_gemm_ex(ctx.handle, GEMM_EPI[epi], m, k, n, P(x), P(w0), P(w1),
+                                         P(out)))
+            sync()
+            outs.append(host(out))
+    finally:
+        hip.check(hip.lib.ie_tune_gemm_schedule(2))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert np.isfinite(orc.bf16_to_f32(outs[2])).all() and outs[2][[0, m // 2, m - 1]].any()
+
+
 @pytest.mark.parametrize("epi", ["bf16", "resid"])
 @pytest.mark.parametrize("m", [17, 24, 40, 64, 2048])
 def test_gemm_down_projection_shapes(hip, ctx, epi, m):
