@@ -95,6 +95,68 @@ def cpu_baseline(prompt: int, budget_s: float = 10.0) -> dict:
                       f"{threads} threads"}
 
 
+def cpu_config_legs(budget_s: float = 2.0) -> dict:
+    """The oracle on configs 1-4 on this host (same thread count as cpu_baseline), each repeated
+    for about budget_s seconds after one untimed call; inputs generated beforehand, not timed.
+    Configs 1-3 in full; config 4 (2048-token prefill of 32 layers) from one layer at 256 rows,
+    extrapolated by flop count (linear products, causal attention, the last row's lm_head).
+    Threads: OpenMP's default (the host's cores available to this process)."""
+    import numpy as np
+
+    import oracle as orc
+    seed = 0
+    cos, sin = orc.rope_tables()
+    w = orc.layer_weights(seed, 5)
+    x = orc.synthetic((1, HIDDEN), seed, 77, 0.0, 1.0)
+
+    def timed(fn, min_n: int = 2) -> float:
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while n < min_n or time.perf_counter() - t0 < budget_s:
+            fn()
+            n += 1
+        return (time.perf_counter() - t0) / n
+
+    def c1() -> None:
+        xn = orc.rmsnorm(x, w["post_attention_layernorm"])
+        orc.residual_add(x, orc.ffn(xn, w["w_gate"], w["w_up"], w["w_down"]))
+
+    P = 2047
+    planes = np.zeros((2, 8, P + 1, 128), np.uint16)
+    planes[:, :, :P] = orc.synthetic((2, 8, P, 128), seed, 78, 0.0, 1.0)
+
+    def c2() -> None:
+        orc.decoder_layer(x.copy(), w, P, cos, sin, planes[0], planes[1], P + 1)
+
+    lm, fn = orc.lm_head_weight(seed), orc.final_norm(seed)
+    x16 = orc.synthetic((16, HIDDEN), seed, 79, 0.0, 1.0)
+
+    def c3(rows) -> None:
+        logits = orc.matmul(orc.rmsnorm(rows, fn), lm, out_f32=True)
+        for r in range(rows.shape[0]):
+            orc.argmax(logits[r])
+            orc.top_p(logits[r], 0.7, 0.9, 1234, r, 0)
+
+    S4 = 128
+    x4 = orc.synthetic((S4, HIDDEN), seed, 80, 0.0, 1.0)
+    p4 = np.zeros((2, 8, S4, 128), np.uint16)
+
+    def c4() -> None:
+        orc.decoder_layer(x4.copy(), w, 0, cos, sin, p4[0], p4[1], S4)
+
+    def layer_flops(S: int) -> float:
+        return 2.0 * S * (LAYER_GEMM_PARAMS) + 4.0 * 32 * 128 * S * (S + 1) / 2
+
+    t1, t2, t3a, t3b = timed(c1), timed(c2), timed(lambda: c3(x)), timed(lambda: c3(x16))
+    t4 = timed(c4, 1)
+    t4_full = t4 * (LAYERS * layer_flops(2048) + 2.0 * VOCAB * HIDDEN) / layer_flops(S4)
+    return {"config1_ffn_block_us": round(t1 * 1e6, 1), "config2_layer_us": round(t2 * 1e6, 1),
+            "config3_b1_us": round(t3a * 1e6, 1), "config3_b16_us": round(t3b * 1e6, 1),
+            "config4_prefill_2048_ms": round(t4_full * 1e3, 1),
+            "config4_sample": f"one layer at {S4} rows ({t4 * 1e3:.1f} ms), extrapolated by flops",
+            "cores": len(os.sched_getaffinity(0)), "kind": "port"}
+
+
 def calibration_copy(nbytes: int = 256 << 20) -> None:
     """A plain device-to-device copy of known size, for scaling the HBM
     FETCH_SIZE / WRITE_SIZE counters of a --pmc run."""
@@ -193,6 +255,103 @@ def prefill_gemms(ctx, P: int) -> dict:
     return gemms
 
 
+def config_legs(ctx, W, iters: int = 32) -> dict:
+    """BASELINE configs 1-3 timed alone with HIP events on the engine stream: 8 untimed launches,
+    then `iters` launches rotating through the 32 layers' weights (config 3: through two
+    [128256][4096] tables, the lm_head and the embedding), so the 256 MB Infinity Cache cannot
+    serve repeats.  Bytes are the algorithmic weight (+ K/V) bytes per launch.
+      config1  the FFN block of one decode token (ie_ffn_block_decode): RMSNorm, gate/up GEMV +
+               SwiGLU, down GEMV + residual
+      config2  one decoder layer decode step at position 2047 over 2047 cached K/V rows
+               (ie_decoder_layer_decode)
+      config3  final RMSNorm + lm_head to fp32 logits, argmax, temperature 0.7 / top-p 0.9
+               sampling: B = 1 (the decode step's GEMV) and B = 16 (the batched step's RMSNorm +
+               skinny MFMA product)"""
+    import ctypes as C
+
+    import torch
+
+    from infengine_amd import check, lib
+    from infengine_amd.engine import ptr
+
+    st = ctx.stream
+
+    def timed(launch) -> float:
+        for i in range(8):
+            launch(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for i in range(iters):
+            launch(8 + i)
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / iters
+
+    def leg(us: float, nbytes: int) -> dict:
+        gbps = nbytes / (us * 1e-6) / 1e9
+        return {"us": round(us, 2), "bytes": nbytes, "GBps": round(gbps, 1),
+                "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+    L = W.s.layers
+    ws = torch.zeros(lib.ie_batch_workspace_size(16), dtype=torch.uint8, device="cuda")
+    x = (torch.randn(1, HIDDEN, device="cuda")).to(torch.bfloat16)
+    x0 = x.clone()
+
+    def ffn(i: int) -> None:
+        l = L[i % LAYERS]
+        check(lib.ie_ffn_block_decode(ctx.handle, ptr(x), C.c_void_p(l.post_attention_layernorm),
+                                      C.c_void_p(l.ffn_block.w_gate), C.c_void_p(l.ffn_block.w_up),
+                                      C.c_void_p(l.ffn_block.w_down), ptr(ws)))
+        if i % LAYERS == LAYERS - 1:
+            x.copy_(x0)           # keep the residual stream at unit scale
+    c1 = leg(timed(ffn), 3 * FFN * HIDDEN * 2 + 2 * HIDDEN * 2)
+
+    pos = 2047
+    kv = torch.zeros(lib.ie_kv_cache_size() // 2, dtype=torch.int16, device="cuda")
+    kv6 = kv.view(LAYERS, 2, 8, 8192, 128)
+    for l in range(LAYERS):
+        kv6[l, :, :, :pos] = torch.randn(2, 8, pos, 128, device="cuda").to(torch.bfloat16).view(torch.int16)
+    attn = torch.zeros(1, HIDDEN, dtype=torch.bfloat16, device="cuda")
+
+    def layer(i: int) -> None:
+        check(lib.ie_decoder_layer_decode(ctx.handle, W.ref(), i % LAYERS, pos + 1, ptr(x),
+                                          ptr(attn), ptr(ws), ptr(kv)))
+        if i % LAYERS == LAYERS - 1:
+            x.copy_(x0)
+    layer_w = (HIDDEN * HIDDEN * 2 + 2 * 1024 * HIDDEN + 3 * FFN * HIDDEN + 2 * HIDDEN) * 2
+    c2 = leg(timed(layer), layer_w + KV_BYTES_PER_POS // LAYERS * (pos + 1))
+    del kv, kv6
+
+    tables = (W.s.lm_head, W.s.emb_lookup)
+    c3 = {}
+    for B in (1, 16):
+        xb = torch.randn(B, HIDDEN, device="cuda").to(torch.bfloat16)
+        xn = torch.empty_like(xb)
+        logits = torch.empty(B, VOCAB, dtype=torch.float32, device="cuda")
+        out = torch.zeros(B, dtype=torch.int32, device="cuda")
+        out2 = torch.zeros(B, dtype=torch.int32, device="cuda")
+        tws = torch.zeros(lib.ie_top_p_workspace_size(B, VOCAB), dtype=torch.uint8, device="cuda")
+
+        def head(i: int, B=B, xb=xb, xn=xn, logits=logits, out=out, out2=out2, tws=tws) -> None:
+            table = C.c_void_p(tables[i % 2])
+            if B == 1:
+                check(lib.ie_final_norm_lm_head(ctx.handle, 1, ptr(xb), C.c_void_p(W.s.final_norm),
+                                                table, ptr(logits)))
+                check(lib.ie_sample_token_amax(ctx.handle, ptr(logits), ptr(out)))
+            else:
+                check(lib.ie_rmsnorm(B, ptr(xb), C.c_void_p(W.s.final_norm), ptr(xn), ptr_stream))
+                check(lib.ie_gemm_ex(ctx.handle, 2, B, HIDDEN, VOCAB, ptr(xn), table, table,
+                                     ptr(logits)))
+                check(lib.ie_sample_argmax_rows(ctx.handle, B, VOCAB, ptr(logits), ptr(out)))
+            check(lib.ie_sample_top_p(ctx.handle, B, VOCAB, ptr(logits), 0.7, 0.9, 1234, i,
+                                      ptr(out2), ptr(tws)))
+        ptr_stream = C.c_void_p(st.cuda_stream)
+        c3[f"b{B}"] = leg(timed(head), VOCAB * HIDDEN * 2 + HIDDEN * 2)
+        del xb, xn, logits, out, out2, tws
+    return {"config1_ffn_block": c1, "config2_layer_pos2047": c2, "config3_head_sampling": c3,
+            "iters": iters}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -212,6 +371,8 @@ def main() -> int:
     ap.add_argument("--attn-only", action="store_true",
                     help="only the prefill attention at S = --prefill-len (for profiling it); "
                          "prints its JSON")
+    ap.add_argument("--no-config-legs", action="store_true",
+                    help="skip the configs 1-3 legs (GPU) and the per-config CPU figures")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -332,6 +493,12 @@ def main() -> int:
         del pool, table
         del kvs, toks, bdata, battn, blogits, bout, bws
 
+    # ---- configs 1-3, each timed alone
+    configs = None
+    if not args.no_config_legs:
+        log("configs 1-3 (FFN block, one layer at position 2047, head + sampling)")
+        configs = config_legs(ctx, W)
+
     # ---- config 4: 2048-token prefill, and its four GEMM shapes against the MFMA peak
     prefill2048 = None
     if args.prefill_len > 0:
@@ -402,6 +569,7 @@ def main() -> int:
                     "tokens_per_s": round(args.prompt / prefill_s, 1)},
         "batched": batched,
         "batched_paged": batched_paged,
+        "configs": configs,
         "prefill_2048": prefill2048,
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4096, SwiGLU, RMSNorm> (gate/up)",
                      "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -415,6 +583,17 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle)")
         out["cpu_baseline"] = cpu_baseline(args.prompt)
+        if not args.no_config_legs:
+            log("cpu configs 1-4 (oracle)")
+            cpu = cpu_config_legs()
+            out["cpu_configs"] = cpu
+            if configs is not None:
+                configs["config1_ffn_block"]["cpu_us"] = cpu["config1_ffn_block_us"]
+                configs["config2_layer_pos2047"]["cpu_us"] = cpu["config2_layer_us"]
+                configs["config3_head_sampling"]["b1"]["cpu_us"] = cpu["config3_b1_us"]
+                configs["config3_head_sampling"]["b16"]["cpu_us"] = cpu["config3_b16_us"]
+            if prefill2048 is not None:
+                prefill2048["cpu_ms_extrapolated"] = cpu["config4_prefill_2048_ms"]
     print(json.dumps(out), flush=True)
     return 0
 

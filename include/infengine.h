@@ -283,11 +283,13 @@ IE_API int ie_sample_top_p(ie_context* ctx, int rows, int vocab, const float* d_
                            int* d_output, void* workspace);
 /* No reference counterpart: ie_sample_top_p without the workspace, for callers that cannot
  * allocate (HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
- * allocates nothing: the [rows][vocab] fp32 scratch is a static device array of the library,
- * one per GPU (rows * vocab <= 16 * 131072 = IE_TOP_P_NOALLOC_MAX; larger calls return
- * IE_ERR_INVALID_ARG).  Same results as ie_sample_top_p.  Calls that overlap on one GPU (any
- * context, any stream) share that array and race. */
+ * allocates nothing: its workspace is a static device array of the library, one per GPU, of
+ * 10 MiB (rows <= IE_TOP_P_NOALLOC_ROWS and rows * vocab <= 16 * 131072 =
+ * IE_TOP_P_NOALLOC_MAX; larger calls return IE_ERR_INVALID_ARG).  Same results as
+ * ie_sample_top_p.  Calls that overlap on one GPU (any context, any stream) share that array
+ * and race. */
 #define IE_TOP_P_NOALLOC_MAX (16 * 131072)
+#define IE_TOP_P_NOALLOC_ROWS 16
 IE_API int ie_sample_top_p_noalloc(ie_context* ctx, int rows, int vocab, const float* d_logits,
                                    float temperature, float top_p, uint64_t seed, uint64_t step,
                                    int* d_output);

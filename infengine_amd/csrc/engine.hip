@@ -1398,7 +1398,7 @@ int ie_sample_argmax_rows(ie_context* c, int rows, int vocab, const float* d_log
 }
 
 size_t ie_top_p_workspace_size(int rows, int vocab) {
-  return (size_t)(rows < 1 ? 1 : rows) * (size_t)(vocab < 1 ? 1 : vocab) * sizeof(float);
+  return top_p_workspace_bytes(rows < 1 ? 1 : rows, vocab < 1 ? 1 : vocab);
 }
 
 int ie_sample_top_p(ie_context* c, int rows, int vocab, const float* d_logits, float temperature,
@@ -1418,10 +1418,11 @@ int ie_sample_top_p_noalloc(ie_context* c, int rows, int vocab, const float* d_l
   CTX_OK(c);
   IE_REQUIRE(d_logits && d_output, "sample_top_p_noalloc: null pointer");
   IE_REQUIRE(rows >= 1 && vocab >= 1, "sample_top_p_noalloc: rows=%d vocab=%d", rows, vocab);
-  IE_REQUIRE((size_t)rows * (size_t)vocab <= kTopPScratchFloats,
-             "sample_top_p_noalloc: rows x vocab = %d x %d exceeds the static scratch of %zu "
-             "logits (use ie_sample_top_p with a workspace)",
-             rows, vocab, kTopPScratchFloats);
+  IE_REQUIRE(rows <= kTopPNoallocRows && (size_t)rows * (size_t)vocab <= kTopPScratchFloats &&
+                 top_p_workspace_bytes(rows, vocab) <= kTopPScratchBytes,
+             "sample_top_p_noalloc: rows x vocab = %d x %d exceeds the static scratch (%d rows, "
+             "%zu logits; use ie_sample_top_p with a workspace)",
+             rows, vocab, kTopPNoallocRows, kTopPScratchFloats);
   float* ws = top_p_scratch(c->device);
   IE_REQUIRE(ws != nullptr, "sample_top_p_noalloc: scratch of device %d not initialised",
              c->device);

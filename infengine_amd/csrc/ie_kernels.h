@@ -125,6 +125,12 @@ int launch_top_p(int rows, int vocab, const float* logits, float temperature, fl
 // floats.  top_p_scratch_init(device) resolves the device address of that device's copy (the
 // device must be current; idempotent); top_p_scratch(device) returns it (nullptr before init).
 constexpr size_t kTopPScratchFloats = (size_t)IE_TOP_P_NOALLOC_MAX;
+constexpr int kTopPNoallocRows = IE_TOP_P_NOALLOC_ROWS;
+// the exponentials plus kTopPNoallocRows per-row blocks of the sampler's state (< 128 KiB each)
+constexpr size_t kTopPScratchBytes = kTopPScratchFloats * sizeof(float) + (size_t)kTopPNoallocRows * (128 << 10);
+// Workspace of launch_top_p: the [rows][vocab] fp32 exponentials (256-byte aligned), then the
+// per-row state.
+size_t top_p_workspace_bytes(int rows, int vocab);
 int top_p_scratch_init(int device);
 float* top_p_scratch(int device);
 

@@ -71,7 +71,9 @@ def test_sizes(hip):
     assert lib.ie_ffn_workspace_size(S) >= S * 14336 * 2
     # decode needs a fixed amount, so a small-S workspace still serves long decodes
     assert lib.ie_attn_workspace_size(1) == lib.ie_attn_workspace_size(0)
-    assert lib.ie_top_p_workspace_size(16, 128256) == 16 * 128256 * 4
+    # top-p: the fp32 exponentials, then per-row state (< 128 KiB a row)
+    assert 16 * 128256 * 4 < lib.ie_top_p_workspace_size(16, 128256) <= 16 * 128256 * 4 + 16 * (128 << 10)
+    assert lib.ie_top_p_workspace_size(1, 128256) < lib.ie_top_p_workspace_size(2, 128256)
 
 
 BOGUS = C.c_void_p(0x1000)   # never dereferenced: every call below fails validation first

@@ -654,6 +654,30 @@ def test_top_p_fixture_and_oracle(hip, ctx):
                 assert tok == want, (r, step, tok, want)
 
 
+def test_top_p_ties_and_flat_rows(hip, ctx):
+    """Rows whose cut bin holds more tokens than the sampler's candidate list (all logits equal; a
+    20000-way tie at the top; a near-flat row), where it selects over the row itself, and a
+    sharp row: the kept set and the sample equal the oracle's (masses in exact fixed point)."""
+    say("top-p on tied and flat rows")
+    rng = np.random.default_rng(17)
+    rows = [np.zeros(V, np.float32),
+            np.where(np.arange(V) < 20000, 3.0, -1.0).astype(np.float32),
+            (rng.standard_normal(V) * 0.01).astype(np.float32),
+            (rng.standard_normal(V) * 8.0).astype(np.float32)]
+    lg = np.stack(rows)
+    R = lg.shape[0]
+    logits = torch.from_numpy(lg).cuda()
+    out = torch.empty(R, dtype=torch.int32, device="cuda")
+    ws = torch.empty(hip.lib.ie_top_p_workspace_size(R, V), dtype=torch.uint8, device="cuda")
+    for step in range(4):
+        hip.check(hip.lib.ie_sample_top_p(ctx.handle, R, V, P(logits), 0.7, 0.9, 555, step,
+                                          P(out), P(ws)))
+        sync()
+        for r in range(R):
+            want, info = orc.top_p(lg[r], 0.7, 0.9, 555, r, step)
+            assert int(out[r].item()) == want, (r, step, int(out[r].item()), want)
+
+
 def test_final_norm_lm_head_sampling_config3(hip, ctx):
     """Config 3: final RMSNorm + lm_head GEMV -> fp32 logits, argmax and top-p, B=1 and B=16."""
     say("final_norm_lm_head rows=16 + argmax + top-p")

@@ -66,7 +66,7 @@ def test_top_p_noalloc_rejects_past_its_scratch(hip, ctx):
     say("top-p noalloc: over-limit shapes are rejected on the host")
     logits = torch.zeros(8, dtype=torch.float32, device="cuda")
     out = torch.zeros(17, dtype=torch.int32, device="cuda")
-    for rows, vocab in ((17, 131072), (1, NOALLOC_MAX + 1)):
+    for rows, vocab in ((17, 131072), (1, NOALLOC_MAX + 1), (17, 1000)):
         rc = hip.lib.ie_sample_top_p_noalloc(ctx.handle, rows, vocab, P(logits), 0.7, 0.9, 1, 0,
                                              P(out))
         assert rc == IE_ERR_INVALID_ARG
