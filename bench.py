@@ -574,6 +574,9 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4096, SwiGLU, RMSNorm> (gate/up)",
                      "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2.000) and WRITE_SIZE "
+                                       "(x1.000) per dispatch, factors from a 256 MiB copy: "
+                                       "profiles/decode_gemv_hbm_traffic.md",
                      "avg_launch_us": round(k_us, 2), "bytes_per_launch": GATE_UP_BYTES},
     }
     del req
