@@ -318,6 +318,7 @@ int ie_context_create(ie_context** out, int device, void* stream) {
     if (hipMalloc(&c->d_counters, kNumCounters * sizeof(unsigned int)) != hipSuccess ||
         hipMalloc(&c->d_slots, kNumSlots * kSlotStride * sizeof(unsigned long long)) != hipSuccess ||
         hipMalloc(&c->d_params, 64 * sizeof(int)) != hipSuccess ||
+        hipMalloc(&c->d_sk_part, kSkPartBytes) != hipSuccess ||
         hipHostMalloc(&c->h_params, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc(&c->h_token, 64 * sizeof(int), hipHostMallocMapped) != hipSuccess) {
       rc = IE_ERR_OOM;
@@ -360,6 +361,7 @@ int ie_context_destroy(ie_context* c) {
   (void)hipFree(c->d_counters);
   (void)hipFree(c->d_slots);
   (void)hipFree(c->d_params);
+  (void)hipFree(c->d_sk_part);
   if (c->h_params) (void)hipHostFree(c->h_params);
   if (c->h_token) (void)hipHostFree(c->h_token);
   if (c->capture) (void)hipStreamDestroy(c->capture);
@@ -553,8 +555,17 @@ namespace {
 // data_buffer at positions start_pos.., in place: RMSNorm, the Q/K/V product, RoPE and the K/V
 // write-out, causal attention, the O product + residual, RMSNorm, gate/up + SwiGLU, down +
 // residual.  The workspace holds q/k/v and the rotated q, then h.
-int prefill_layer(hipStream_t st, const ie_model_weights& W, int l, int start_pos, int S,
-                  ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
+// K halves of a skinny (M <= 16) product's tiles (gemm_skinny_split): partials in `part`
+// (kSkPartBytes), the context's arrival counters.
+void skinny_split(Context* c, int epi, GemmParams& g, float* part) {
+  if (g.M > 16) return;
+  g.sk_tail = gemm_skinny_split(epi, g.N, g.K);
+  g.sk_part = part;
+  g.sk_cnt = c->d_counters + kCntSkinny;
+}
+
+int prefill_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, int start_pos,
+                  int S, ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
                   void* workspace, void* kv_cache, const int* block_table, int n_pages) {
   char* wsb = static_cast<char*>(workspace);
   uint16_t* qkv = reinterpret_cast<uint16_t*>(wsb);
@@ -580,6 +591,7 @@ int prefill_layer(hipStream_t st, const ie_model_weights& W, int l, int start_po
   // split K's partials after q/k/v and the rotated q (the rest of the workspace)
   g.split_ws = reinterpret_cast<float*>(wsb + prefill_attn_bytes(S));
   g.split_ws_bytes = (long long)(ie_attn_workspace_size(S) - prefill_attn_bytes(S));
+  skinny_split(c, kGemmBf16, g, c->d_sk_part);
   IE_TRY(launch_gemm(kGemmBf16, g, st));
   IE_TRY(launch_qkv_rope_scatter(S, start_pos, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl,
                                  nullptr, 0, st, block_table, n_pages));
@@ -596,6 +608,7 @@ int prefill_layer(hipStream_t st, const ie_model_weights& W, int l, int start_po
   o.ldy = kHidden;
   o.split_ws = reinterpret_cast<float*>(wsb);  // q/k/v and rotated q are dead
   o.split_ws_bytes = (long long)std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S));
+  skinny_split(c, kGemmResid, o, c->d_sk_part);
   IE_TRY(launch_gemm(kGemmResid, o, st));
   IE_TRY(launch_rmsnorm(S, data_buffer, L.post_attention_layernorm, aux_buffer, st));
   GemmParams gu{};
@@ -610,6 +623,7 @@ int prefill_layer(hipStream_t st, const ie_model_weights& W, int l, int start_po
   gu.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
   gu.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
                                   align256((size_t)S * kFFN * 2));
+  skinny_split(c, kGemmSwiglu, gu, c->d_sk_part);
   IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
   GemmParams dn{};
   dn.x = h;
@@ -623,6 +637,7 @@ int prefill_layer(hipStream_t st, const ie_model_weights& W, int l, int start_po
   dn.split_ws = reinterpret_cast<float*>(wsb + align256((size_t)S * kFFN * 2));  // after h
   dn.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
                                   align256((size_t)S * kFFN * 2));
+  skinny_split(c, kGemmResid, dn, c->d_sk_part);
   IE_TRY(launch_gemm(kGemmResid, dn, st));
   return IE_OK;
 }
@@ -653,8 +668,8 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int start_pos, 
 
   IE_TRY(launch_emblookup(S, tokenid_buff + start_pos, W.emb_lookup, data_buffer, nullptr, 0, st));
   for (int l = 0; l < kLayers; ++l)
-    IE_TRY(prefill_layer(st, W, l, start_pos, S, data_buffer, aux_buffer, attn_buffer, workspace,
-                         kv_cache, block_table, n_pages));
+    IE_TRY(prefill_layer(c, st, W, l, start_pos, S, data_buffer, aux_buffer, attn_buffer,
+                         workspace, kv_cache, block_table, n_pages));
   // prefill.cu:41-43: final norm, lm_head on the last row only, argmax
   IE_TRY(gemv_plain(kHidden, kEpiF32, data_buffer + (size_t)(S - 1) * kHidden, W.final_norm,
                     W.lm_head, nullptr, kVocab / 2, nullptr, output_distr, 1, kVocab, st));
@@ -707,7 +722,7 @@ int ie_decoder_layer_prefill(ie_context* c, const ie_model_weights* weights, int
              seq_len, kMaxCtx);
   IE_REQUIRE(data_buffer && aux_buffer && attn_buffer && workspace && kv_cache,
              "decoder_layer_prefill: null buffer");
-  return prefill_layer(c->stream, *weights, layer_idx, 0, seq_len, data_buffer, aux_buffer,
+  return prefill_layer(c, c->stream, *weights, layer_idx, 0, seq_len, data_buffer, aux_buffer,
                        attn_buffer, workspace, kv_cache, nullptr, 0);
 }
 
@@ -749,9 +764,7 @@ int batched_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
   g.ss_in = w.ss;
   g.ss_parts = kNormParts;
   g.x_norm_w = L.input_layernorm;
-  g.sk_tail = gemm_skinny_tail(kQKVDim);
-  g.sk_part = w.sk_part;
-  g.sk_cnt = c->d_counters + kCntSkinny;
+  skinny_split(c, kGemmQkvRope, g, w.sk_part);
   IE_TRY(launch_gemm(kGemmQkvRope, g, st));
   IE_TRY(attn_decode(w.q, kvl, attn_buffer, w, d_sl, 0, len_class, batch, cstride, true, st,
                      block_table, table_stride, n_pages, true));
@@ -765,6 +778,7 @@ int batched_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
   o.K = kHidden;
   o.ldy = kHidden;
   o.ss_out = w.ss;
+  skinny_split(c, kGemmResid, o, w.sk_part);
   IE_TRY(launch_gemm(kGemmResid, o, st));
   GemmParams gu{};
   gu.x = data_buffer;
@@ -778,9 +792,7 @@ int batched_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
   gu.ss_in = w.ss;
   gu.ss_parts = kNormParts;
   gu.x_norm_w = L.post_attention_layernorm;
-  gu.sk_tail = gemm_skinny_tail(kFFN);
-  gu.sk_part = w.sk_part;
-  gu.sk_cnt = c->d_counters + kCntSkinny;
+  skinny_split(c, kGemmSwiglu, gu, w.sk_part);
   IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
   GemmParams dn{};
   dn.x = w.h;
@@ -792,6 +804,7 @@ int batched_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
   dn.K = kFFN;
   dn.ldy = kHidden;
   if (ss_next) dn.ss_out = w.ss;
+  skinny_split(c, kGemmResid, dn, w.sk_part);
   IE_TRY(launch_gemm(kGemmResid, dn, st));
   return IE_OK;
 }
@@ -828,6 +841,7 @@ int enqueue_batched(Context* c, hipStream_t st, const ie_model_weights& W, int b
   lm.N = kVocab;
   lm.K = kHidden;
   lm.ldy = kVocab;
+  skinny_split(c, kGemmF32, lm, w.sk_part);
   IE_TRY(launch_gemm(kGemmF32, lm, st));
   IE_TRY(launch_argmax_rows(batch, kVocab, output_distr, output_tokens, c->d_slots,
                             c->d_counters + kCntArgmax, st));
@@ -1183,6 +1197,7 @@ int ie_multiply_by_weight(ie_context* c, int m, int k, int n, const ie_bf16* d_i
   g.N = n;
   g.K = k;
   g.ldy = n;
+  skinny_split(c, kGemmBf16, g, c->d_sk_part);
   return launch_gemm(kGemmBf16, g, c->stream);
 }
 
@@ -1199,6 +1214,7 @@ int ie_gemm_bf16(ie_context* c, int m, int k, int n, const ie_bf16* d_x, const i
   g.N = n;
   g.K = k;
   g.ldy = n;
+  skinny_split(c, kGemmBf16, g, c->d_sk_part);
   return launch_gemm(kGemmBf16, g, c->stream);
 }
 
@@ -1257,6 +1273,7 @@ int ie_gemm_ex(ie_context* c, int epilogue, int m, int k, int n, const ie_bf16* 
   }
   g.split_ws = c->gemm_ws;
   g.split_ws_bytes = (long long)c->gemm_ws_bytes;
+  skinny_split(c, epilogue, g, c->d_sk_part);
   return launch_gemm(epilogue, g, c->stream);
 }
 
@@ -1283,6 +1300,7 @@ int ie_ffn(ie_context* c, int seq_len, const ie_bf16* d_in, ie_bf16* d_out, cons
   gu.N = kFFN;
   gu.K = kHidden;
   gu.ldy = kFFN;
+  skinny_split(c, kGemmSwiglu, gu, c->d_sk_part);
   IE_TRY(launch_gemm(kGemmSwiglu, gu, st));
   GemmParams dn{};
   dn.x = h;
@@ -1293,6 +1311,7 @@ int ie_ffn(ie_context* c, int seq_len, const ie_bf16* d_in, ie_bf16* d_out, cons
   dn.N = kHidden;
   dn.K = kFFN;
   dn.ldy = kHidden;
+  skinny_split(c, kGemmBf16, dn, c->d_sk_part);
   return launch_gemm(kGemmBf16, dn, st);
 }
 
@@ -1328,6 +1347,7 @@ int ie_attn(ie_context* c, const float* d_rope_cos, const float* d_rope_sin, int
   // split-K partials (both projections) after q/k/v and the rotated q
   g.split_ws = reinterpret_cast<float*>(wsb + prefill_attn_bytes(S));
   g.split_ws_bytes = (long long)(ie_attn_workspace_size(S) - prefill_attn_bytes(S));
+  skinny_split(c, kGemmBf16, g, c->d_sk_part);
   IE_TRY(launch_gemm(kGemmBf16, g, st));
   IE_TRY(launch_qkv_rope_scatter(S, 0, qkv, d_rope_cos, d_rope_sin, qrot, kvl,
                                  kvl + (size_t)kKVHeads * kKVPlane, nullptr, 0, st));
@@ -1345,6 +1365,7 @@ int ie_attn(ie_context* c, const float* d_rope_cos, const float* d_rope_sin, int
   o.ldy = kHidden;
   o.split_ws = g.split_ws;
   o.split_ws_bytes = g.split_ws_bytes;
+  skinny_split(c, kGemmBf16, o, c->d_sk_part);
   return launch_gemm(kGemmBf16, o, st);
 }
 

@@ -261,6 +261,8 @@ struct Context {
     unsigned long long used = 0;
   } bgraph[4];
   unsigned long long bgraph_tick = 0;
+  // the skinny GEMM's K-half partials (kSkPartBytes) for launches outside the batched step
+  float* d_sk_part = nullptr;
   // split-K partials of the op-level GEMM entry (allocated on first use)
   float* gemm_ws = nullptr;
   size_t gemm_ws_bytes = 0;

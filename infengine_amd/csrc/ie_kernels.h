@@ -181,10 +181,11 @@ struct GemmParams {
   float* split_ws;
   long long split_ws_bytes;
   int k_splits;  // set by the launcher for the wide kernel (0 / 1: no split)
-  // Skinny GEMM (SwiGLU / QKV + RoPE epilogues): the last sk_tail of the N / 16 tiles run as two
-  // workgroups each, one per K half, so that every CU gets the same share of the weight stream
-  // (gemm_skinny_tail gives the count).  sk_part: fp32 partials [sk_tail][2][2][64][4];
-  // sk_cnt: one zeroed arrival counter per tile, kCntStride apart (reset by the tile's finisher).
+  // Skinny GEMM (M <= 16): the last sk_tail of its tiles (16 rows; 32 for the fp32 epilogue
+  // at K = 4096 or 14336) run as two workgroups each, one per K half, so that every CU gets the
+  // same share of the weight stream (gemm_skinny_split gives the count).  sk_part: fp32
+  // partials [sk_tail][2][2][64][4]; sk_cnt: one zeroed arrival counter per tile, kCntStride
+  // apart (reset by the tile's finisher).
   float* sk_part;
   unsigned int* sk_cnt;
   int sk_tail;
@@ -214,6 +215,9 @@ int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st);
 // Tiles of an N-column skinny product to split in K halves (the part of the last round of
 // tiles that would leave CUs idle), 0 for none.
 int gemm_skinny_tail(int N);
+// The same for any skinny epilogue at its own tile size (the fp32 epilogue's 32-row tiles at
+// K = 4096 or 14336; 0 for the other plain epilogues).
+int gemm_skinny_split(int epi, int N, int K);
 // 16 < M <= 48 (short prompts): the streaming kernel over 2-3 X row-blocks
 bool gemm_skinny_mb_fits(int epi, const GemmParams& p);
 int launch_gemm_skinny_mb(int epi, const GemmParams& p, hipStream_t st);

@@ -719,7 +719,7 @@ namespace pp {
 // Tile: BN W rows x BM X rows x 64 k per stage.  BM = 256 (KG = 1): the two wave groups split the
 // W rows.  BM = 128 (KG = 2): each group owns the whole tile and multiplies one k32 half of every
 // stage, and group 1's sums are added to group 0's through LDS at the end.
-template <int BN_, int BM_>
+template <int BN_, int BM_, int NW_ = 3>
 struct PC {
   static constexpr int BN = BN_, BM = BM_, BK = 64;
   static constexpr int KG = BM == 256 ? 1 : 2;
@@ -733,14 +733,15 @@ struct PC {
   static constexpr int WL = W_CHUNKS / 64 / 4; // W loads per group-0 wave per stage
   static constexpr int XL = X_CHUNKS / 64 / 4; // X loads per group-1 wave per stage
   static constexpr int PL = WL > XL ? WL : XL;
-  // The W and X halves have rings of their own: 3 W slots (the W rows come from HBM; stage
-  // k + 3 is issued four phases before it is read), and 3 X slots where they fit beside them
-  // in the 160 KiB of LDS, else 2.  X slots follow the W slots.
-  static constexpr int NW = 3;
+  // The W and X halves have rings of their own: NW W slots (the W rows come from HBM; stage
+  // k + NW is issued 2 NW - 2 phases before it is read), and 3 X slots where they fit beside
+  // them in the 160 KiB of LDS, else 2.  X slots follow the W slots.
+  static constexpr int NW = NW_;
   static constexpr int NX = (NW * W_CHUNKS + 3 * X_CHUNKS) * 16 <= 160 * 1024 ? 3 : 2;
   static constexpr int X_BASE = NW * W_CHUNKS;  // chunk offset of X slot 0
   static constexpr int TOTAL = NW * W_CHUNKS + NX * X_CHUNKS;
   static_assert(BM == 256 || (BM == 128 && BN == 256), "tile shapes");
+  static_assert(NW == 3 || NW == 4, "W ring depth");
   static_assert(TOTAL * 16 <= 160 * 1024, "LDS");
   static __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 };
@@ -819,10 +820,10 @@ struct OutSwz {
   }
 };
 
-template <int EPI, int BN, int BM>
+template <int EPI, int BN, int BM, int NWR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_pp_kernel(GemmParams p, int m_tiles) {
-  using C = PC<BN, BM>;
+  using C = PC<BN, BM, NWR>;
   constexpr int NA = C::NA, NB = C::NB, WL = C::WL, XL = C::XL, PL = C::PL, KS = C::KS;
   static_assert(EPI == kGemmBf16 || EPI == kGemmResid || EPI == kGemmSwiglu, "bf16 epilogues");
   static_assert(EPI != kGemmSwiglu || BN == 256, "SwiGLU tiles are 256 W rows");
@@ -888,7 +889,9 @@ void gemm_pp_kernel(GemmParams p, int m_tiles) {
       const int swn = sw + 1 == NW ? 0 : sw + 1, sxn = sx + 1 == NX ? 0 : sx + 1;
       // phase 2k+1: multiply k-step k
       compute<C, WL, false>(acc, fa, fb, lds, rs, vo, 0, 0);
-      if (k + 2 < KT) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NW - 2) * WL) : "memory");
+      // stage k+1 must have landed; stages k+2 .. min(k+NW-1, KT-1) may stay in flight
+      if (NW == 4 && k + 3 < KT) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * WL) : "memory");
+      else if (k + 2 < KT) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(WL) : "memory");
       else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
       // phase 2k+2: fragments of k-step k+1, then the W half of stage k+NW into W slot sw
       if (k + 1 < KT) read<C>(lds, swn * WSB, XB0 + sxn * XSB, aA, aB, fa, fb);
@@ -1016,13 +1019,13 @@ int launch_wide(const GemmParams& p, hipStream_t st) {
   return IE_OK;
 }
 
-template <int EPI, int WBN, int XBM = 256>
+template <int EPI, int WBN, int XBM = 256, int NW = 3>
 int launch_pp(const GemmParams& p, hipStream_t st) {
   const int m_tiles = (p.M + XBM - 1) / XBM;
   const int n_tiles = (EPI == kGemmSwiglu) ? (p.N + WBN / 2 - 1) / (WBN / 2) : (p.N + WBN - 1) / WBN;
   const long long blocks = (long long)m_tiles * n_tiles;
   IE_REQUIRE(blocks <= 0x7fffffff && p.k_splits <= 1, "gemm: ping-pong tiles");
-  hipLaunchKernelGGL((wide::pp::gemm_pp_kernel<EPI, WBN, XBM>), dim3((unsigned)blocks), dim3(512), 0,
+  hipLaunchKernelGGL((wide::pp::gemm_pp_kernel<EPI, WBN, XBM, NW>), dim3((unsigned)blocks), dim3(512), 0,
                      st, p, m_tiles);
   IE_CHECK_LAUNCH();
   return IE_OK;
@@ -1048,8 +1051,9 @@ int launch_e(const GemmParams& p, hipStream_t st) {
 enum { kTileSmall, kTileWide, kTileBig, kTileBig192, kTileKinds };
 
 // Kernel of the bf16 wide tiles: 0 = the DMA-ring wide kernels; 1 = the ping-pong kernel for
-// the 256-row X tiles; 2 (default) = the ping-pong kernel for those and for the 128-row X tiles.
-// Outputs are bit-identical across the three (same per-accumulator MFMA order).
+// the 256-row X tiles; 2 (default) = the ping-pong kernel for those and for the 128-row X tiles;
+// 3 = as 2 with 4 W ring slots (2 X slots) on the 256 x 128 and 192 x 256 tiles.
+// Outputs are bit-identical across all (same per-accumulator MFMA order).
 int g_gemm_schedule = 2;
 
 struct TileKind {
@@ -1082,7 +1086,20 @@ double tile_cost(int kind, int epi, int M, int N) {
 }
 
 int launch_kind(int kind, int epi, const GemmParams& p, hipStream_t st) {
-  if (g_gemm_schedule == 2 && kind == kTileWide && epi != kGemmF32) {
+  if (g_gemm_schedule == 3 && kind == kTileWide && epi != kGemmF32) {
+    switch (epi) {
+      case kGemmBf16: return launch_pp<kGemmBf16, 256, 128, 4>(p, st);
+      case kGemmResid: return launch_pp<kGemmResid, 256, 128, 4>(p, st);
+      case kGemmSwiglu: return launch_pp<kGemmSwiglu, 256, 128, 4>(p, st);
+    }
+  }
+  if (g_gemm_schedule == 3 && kind == kTileBig192) {
+    switch (epi) {
+      case kGemmBf16: return launch_pp<kGemmBf16, 192, 256, 4>(p, st);
+      case kGemmResid: return launch_pp<kGemmResid, 192, 256, 4>(p, st);
+    }
+  }
+  if (g_gemm_schedule >= 2 && kind == kTileWide && epi != kGemmF32) {
     switch (epi) {
       case kGemmBf16: return launch_pp<kGemmBf16, 256, 128>(p, st);
       case kGemmResid: return launch_pp<kGemmResid, 256, 128>(p, st);
@@ -1315,7 +1332,7 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
 }  // namespace ie
 
 extern "C" int ie_tune_gemm_schedule(int schedule) {
-  IE_REQUIRE(schedule >= 0 && schedule <= 2, "tune_gemm_schedule: %d not in [0, 2]", schedule);
+  IE_REQUIRE(schedule >= 0 && schedule <= 3, "tune_gemm_schedule: %d not in [0, 3]", schedule);
   ie::g_gemm_schedule = schedule;
   return IE_OK;
 }

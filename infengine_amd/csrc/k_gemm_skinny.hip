@@ -187,21 +187,29 @@ __global__ __launch_bounds__(kSkSplit * 64) __attribute__((
     amdgpu_waves_per_eu(KC > 0 ? (NORM && EPI == kGemmSwiglu ? 2 : 4) : 1)))
 void gemm_skinny_kernel(GemmParams p) {
   constexpr bool SW = EPI == kGemmSwiglu;
-  constexpr int NT = SW ? 2 : 1;  // 16-row W tiles: the weight rows, or gate and up rows
+  // The fp32 epilogue (the lm_head: 8016 16-row tiles) at a compile-time K takes 32-row tiles:
+  // two 16-row W tiles against each X step, which halves the X re-reads per weight byte (as
+  // many bytes as the weights for a 16-row tile); lm_head at M = 16 183.6 -> 163.5 us.  The
+  // 4096-column projections keep 16-row tiles: at 32 rows their 128 tiles need K halves to fill
+  // the chip, and the halves' hand-off (write-through stores, arrival counter, reads) ends these
+  // short kernels ~2 us later (O 9.05 -> 10.34 us, down 22.69 -> 22.52 in the batched step).
+  constexpr bool WIDE = KC > 0 && EPI == kGemmF32;
+  constexpr int NT = (SW || WIDE) ? 2 : 1;  // 16-row W tiles: rows n0.. and n0+16.., or gate and up
+  constexpr int TROWS = WIDE ? 2 * kSkRows : kSkRows;  // output columns per tile
   __shared__ u32x4_t tr[kSkSplit][2][256];  // per wave: a W tile and the X rows
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, q = lane >> 4;
   // tiles 0 .. tfull-1 are one workgroup each; each of the p.sk_tail tiles after them is two,
   // K half 0 then K half 1 (the second to arrive sums the halves and runs the epilogue)
-  constexpr bool TAIL = KC > 0 && (SW || EPI == kGemmQkvRope);  // (the launcher checks sk_tail)
+  constexpr bool TAIL = KC > 0 && (SW || WIDE || EPI == kGemmQkvRope);  // (the launcher checks sk_tail)
   const int tfull = gridDim.x - 2 * p.sk_tail;
   int tile = blockIdx.x, half = -1;
   if (TAIL && (int)blockIdx.x >= tfull) {
     tile = tfull + ((blockIdx.x - tfull) >> 1);
     half = (blockIdx.x - tfull) & 1;
   }
-  const int n0 = tile * kSkRows;
+  const int n0 = tile * TROWS;
   const int K = KC > 0 ? KC : p.K;
 
   SkSrc src;
@@ -235,6 +243,8 @@ void gemm_skinny_kernel(GemmParams p) {
       else if (n0 < e1) base = p.w1 + (size_t)(n0 - e0) * K, end = e1;
       else base = p.w2 + (size_t)(n0 - e1) * K, end = p.N;
       src.w[0] = sk_rsrc(base, min(kSkRows, end - n0), K);
+      if constexpr (WIDE)
+        src.w[1] = sk_rsrc(base + (size_t)kSkRows * K, max(0, min(kSkRows, end - n0 - kSkRows)), K);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) wrow[j] = 4 * j + q;
@@ -282,11 +292,16 @@ void gemm_skinny_kernel(GemmParams p) {
   // Epilogue operands, loaded ahead of the weight stream so that the epilogue does not end the
   // workgroup on load latencies: the residual columns, or the RoPE position (then its angles and
   // page below).  Every wave loads them (wave 0 stores the outputs): no load is conditional.
-  const int em = min(r, max(p.M - 1, 0)), en = min(n0 + 4 * q, max(p.N - 4, 0));
+  const int em = min(r, max(p.M - 1, 0));
   int epos = 0;  // (the sequence length here; the position after the weight loads are issued)
-  uint2 eold = make_uint2(0u, 0u);
+  uint2 eold[NT];
   if constexpr (EPI == kGemmQkvRope) epos = p.d_seq_len[em];
-  if constexpr (EPI == kGemmResid) eold = *reinterpret_cast<const uint2*>(p.y + (size_t)em * p.ldy + en);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    eold[t] = make_uint2(0u, 0u);
+    const int en = min(n0 + kSkRows * t + 4 * q, max(p.N - 4, 0));
+    if constexpr (EPI == kGemmResid) eold[t] = *reinterpret_cast<const uint2*>(p.y + (size_t)em * p.ldy + en);
+  }
   __builtin_amdgcn_sched_barrier(0);
   sk_load_w<NT>(src, kbase, w0);
   sk_load_x(src, kbase, xv);
@@ -352,13 +367,13 @@ void gemm_skinny_kernel(GemmParams p) {
   // sum the K quarters: waves 1..3 hand their tiles to wave 0 through their own W tile slots
   // (each wave's last reads of its slot precede these writes)
   tr[wave][0][lane] = __builtin_bit_cast(u32x4_t, acc0);
-  if constexpr (SW) tr[wave][0][64 + lane] = __builtin_bit_cast(u32x4_t, acc1);
+  if constexpr (NT == 2) tr[wave][0][64 + lane] = __builtin_bit_cast(u32x4_t, acc1);
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int w = 1; w < kSkSplit; ++w) {
     acc0 += __builtin_bit_cast(f32x4_t, tr[w][0][lane]);
-    if constexpr (SW) acc1 += __builtin_bit_cast(f32x4_t, tr[w][0][64 + lane]);
+    if constexpr (NT == 2) acc1 += __builtin_bit_cast(f32x4_t, tr[w][0][64 + lane]);
   }
   if constexpr (TAIL) {
     if (half >= 0) {
@@ -373,7 +388,7 @@ void gemm_skinny_kernel(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         __hip_atomic_store(mine + i, acc0[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if constexpr (SW)
+        if constexpr (NT == 2)
           __hip_atomic_store(mine + 256 + i, acc1[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -384,7 +399,7 @@ void gemm_skinny_kernel(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         acc0[i] += __hip_atomic_load(other + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if constexpr (SW)
+        if constexpr (NT == 2)
           acc1[i] +=
               __hip_atomic_load(other + 256 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -395,22 +410,28 @@ void gemm_skinny_kernel(GemmParams p) {
   const int m = r, n = n0 + 4 * q;
   if constexpr (EPI == kGemmResid) {
     if (p.ss_out) {
-      // the new residual rows and this workgroup's share of each row's sum of squares (for the
-      // next projection's RMSNorm; lanes q = 0..3 hold 4 columns each)
-      float v[4] = {0.f, 0.f, 0.f, 0.f};
-      if (m < p.M && n < p.N) {
-        uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n);
-        const uint2 old = eold;
-        v[0] = bf2f(f2bf(bf_lo(old.x) + bf2f(f2bf(acc0[0]))));
-        v[1] = bf2f(f2bf(bf_hi(old.x) + bf2f(f2bf(acc0[1]))));
-        v[2] = bf2f(f2bf(bf_lo(old.y) + bf2f(f2bf(acc0[2]))));
-        v[3] = bf2f(f2bf(bf_hi(old.y) + bf2f(f2bf(acc0[3]))));
-        *dst = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+      // the new residual rows and each 16-column tile's share of each row's sum of squares (for
+      // the next projection's RMSNorm: partial n / 16 of kNormParts; lanes q = 0..3 hold 4
+      // columns each)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x4_t a = t == 0 ? acc0 : acc1;
+        const int nt = n + kSkRows * t;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (m < p.M && nt < p.N) {
+          uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + nt);
+          const uint2 old = eold[t];
+          v[0] = bf2f(f2bf(bf_lo(old.x) + bf2f(f2bf(a[0]))));
+          v[1] = bf2f(f2bf(bf_hi(old.x) + bf2f(f2bf(a[1]))));
+          v[2] = bf2f(f2bf(bf_lo(old.y) + bf2f(f2bf(a[2]))));
+          v[3] = bf2f(f2bf(bf_hi(old.y) + bf2f(f2bf(a[3]))));
+          *dst = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+        }
+        float sq = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], v[3] * v[3])));
+        sq += __shfl_xor(sq, 16);
+        sq += __shfl_xor(sq, 32);
+        if (q == 0) p.ss_out[m * kNormParts + (n0 >> 4) + t] = sq;
       }
-      float sq = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], v[3] * v[3])));
-      sq += __shfl_xor(sq, 16);
-      sq += __shfl_xor(sq, 32);
-      if (q == 0) p.ss_out[m * gridDim.x + blockIdx.x] = sq;
       return;
     }
   }
@@ -459,16 +480,27 @@ void gemm_skinny_kernel(GemmParams p) {
     return;
   }
   if (m >= p.M || n >= p.N) return;
-  if constexpr (EPI == kGemmF32) {
-    *reinterpret_cast<float4*>(p.yf + (size_t)m * p.ldy + n) =
-        make_float4(acc0[0], acc0[1], acc0[2], acc0[3]);
-  } else if constexpr (EPI == kGemmResid) {
-    uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n);
-    const uint2 old = eold;
-    *dst = make_uint2(
-        pack_bf2(bf_lo(old.x) + bf2f(f2bf(acc0[0])), bf_hi(old.x) + bf2f(f2bf(acc0[1]))),
-        pack_bf2(bf_lo(old.y) + bf2f(f2bf(acc0[2])), bf_hi(old.y) + bf2f(f2bf(acc0[3]))));
-  } else if constexpr (SW) {
+  if constexpr (!SW) {
+    // the plain epilogues, per 16-column tile (columns n0 + 16 t + 4 q ..)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const f32x4_t a = t == 0 ? acc0 : acc1;
+      const int nt = n + kSkRows * t;
+      if (nt >= p.N) break;
+      if constexpr (EPI == kGemmF32) {
+        *reinterpret_cast<float4*>(p.yf + (size_t)m * p.ldy + nt) = make_float4(a[0], a[1], a[2], a[3]);
+      } else if constexpr (EPI == kGemmResid) {
+        uint2* dst = reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + nt);
+        const uint2 old = eold[t];
+        *dst = make_uint2(
+            pack_bf2(bf_lo(old.x) + bf2f(f2bf(a[0])), bf_hi(old.x) + bf2f(f2bf(a[1]))),
+            pack_bf2(bf_lo(old.y) + bf2f(f2bf(a[2])), bf_hi(old.y) + bf2f(f2bf(a[3]))));
+      } else {
+        *reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + nt) =
+            make_uint2(pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3]));
+      }
+    }
+  } else {
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -477,9 +509,6 @@ void gemm_skinny_kernel(GemmParams p) {
     }
     *reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n) =
         make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
-  } else {
-    *reinterpret_cast<uint2*>(p.y + (size_t)m * p.ldy + n) =
-        make_uint2(pack_bf2(acc0[0], acc0[1]), pack_bf2(acc0[2], acc0[3]));
   }
 }
 
@@ -649,9 +678,16 @@ int launch_mb_e(const GemmParams& p, hipStream_t st) {
   return launch_mb_k<EPI, 3>(p, st);
 }
 
+// Output columns per workgroup tile: 32 for the fp32 epilogue at a compile-time K (two 16-row
+// W tiles), else 16.
+int skinny_tile_rows(int epi, int K) {
+  return epi == kGemmF32 && (K == 4096 || K == 14336) ? 2 * kSkRows : kSkRows;
+}
+
 template <int EPI, bool NORM>
 int launch_sn(const GemmParams& p, hipStream_t st) {
-  const int blocks = (p.N + kSkRows - 1) / kSkRows + p.sk_tail;
+  const int tr = skinny_tile_rows(EPI, p.K);
+  const int blocks = (p.N + tr - 1) / tr + p.sk_tail;
   if constexpr (EPI == kGemmQkvRope) {
     IE_REQUIRE(p.K == kHidden && p.N == kQKVDim && p.n0 == kHidden && p.n1 == kKVDim && p.y &&
                    p.k_cache && p.v_cache && p.d_seq_len && p.rope_cos && p.rope_sin,
@@ -700,6 +736,15 @@ int gemm_skinny_tail(int N) {
   return tiles > 256 ? std::min(tiles % 256, kSkTailMax) : 0;
 }
 
+int gemm_skinny_split(int epi, int N, int K) {
+  if (epi == kGemmSwiglu || epi == kGemmQkvRope) return gemm_skinny_tail(N);
+  const int tr = skinny_tile_rows(epi, K);
+  if (tr == kSkRows) return 0;  // (the run-time-K instance has no K halves)
+  // the last partial round of 32-row tiles (the lm_head: 168 of 4008)
+  const int tiles = (N + tr - 1) / tr;
+  return tiles > 256 ? std::min(tiles % 256, kSkTailMax) : 0;
+}
+
 bool gemm_skinny_fits(const GemmParams& p) {
   return p.M >= 1 && p.M <= kSkRows && p.K % (kSkSplit * kSkStep) == 0;
 }
@@ -730,15 +775,16 @@ int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {
              "gemm_skinny: RMSNorm of the X rows (SwiGLU / QKV projections) needs the norm weight "
              "and %d partial sums per row",
              kNormParts);
-  IE_REQUIRE(!p.ss_out || (epi == kGemmResid && p.N % 16 == 0),
-             "gemm_skinny: the sums-of-squares output is a residual-epilogue option");
+  IE_REQUIRE(!p.ss_out || (epi == kGemmResid && p.N == 16 * kNormParts),
+             "gemm_skinny: the sums-of-squares output is a residual-epilogue option for N = %d",
+             16 * kNormParts);
+  const int trows = skinny_tile_rows(epi, p.K);
   IE_REQUIRE(p.sk_tail == 0 ||
-                 ((epi == kGemmSwiglu || epi == kGemmQkvRope) && p.sk_part && p.sk_cnt &&
-                  p.sk_tail > 0 && p.sk_tail <= kSkTailMax &&
-                  p.sk_tail <= (p.N + kSkRows - 1) / kSkRows &&
+                 (p.sk_part && p.sk_cnt && p.sk_tail > 0 && p.sk_tail <= kSkTailMax &&
+                  p.sk_tail <= (p.N + trows - 1) / trows &&
                   (p.ss_in || epi == kGemmQkvRope || p.K == 4096 || p.K == 14336)),
-             "gemm_skinny: K-half tail tiles (sk_tail=%d) need the SwiGLU or QKV epilogue, K 4096 "
-             "or 14336, at most %d tiles, partials and counters",
+             "gemm_skinny: K-half tiles (sk_tail=%d) need K 4096 or 14336, at most %d tiles, "
+             "partials and counters",
              p.sk_tail, kSkTailMax);
   switch (epi) {
     case kGemmSwiglu: return launch_s<kGemmSwiglu>(p, st);
@@ -750,11 +796,11 @@ int launch_gemm_skinny(int epi, const GemmParams& p, hipStream_t st) {
       set_error("gemm_skinny: bad epilogue %d", epi);
       return IE_ERR_INVALID_ARG;
   }
-  // a workgroup's 16 rows are read from one weight matrix
+  // a workgroup's rows are read from one weight matrix
   const int e0 = std::min(p.n0, p.N), e1 = std::min(p.n0 + p.n1, p.N);
-  IE_REQUIRE((e0 == p.N || e0 % kSkRows == 0) && (e1 == p.N || e1 % kSkRows == 0),
+  IE_REQUIRE((e0 == p.N || e0 % trows == 0) && (e1 == p.N || e1 % trows == 0),
              "gemm_skinny: weight matrix boundaries must fall on multiples of %d rows (n0=%d n1=%d)",
-             kSkRows, p.n0, p.n1);
+             trows, p.n0, p.n1);
   if (epi == kGemmResid) return launch_s<kGemmResid>(p, st);
   if (epi == kGemmF32) return launch_s<kGemmF32>(p, st);
   return launch_s<kGemmBf16>(p, st);

@@ -353,9 +353,9 @@ def test_gemm_epilogues(hip, ctx, epi, m, n):
                                        ("swiglu", 2048, 4096, 14336), ("bf16", 2048, 4096, 6144),
                                        ("bf16", 555, 4096, 1000)])
 def test_gemm_schedules_bit_identical(hip, ctx, epi, m, k, n):
-    """The prefill GEMM's three tile schedules (ie_tune_gemm_schedule: the DMA-ring kernels, the
-    ping-pong kernel for 256-row tiles, for all bf16 tiles) give identical bits: the MFMAs of every
-    accumulator run in the same k order."""
+    """The prefill GEMM's tile schedules (ie_tune_gemm_schedule: the DMA-ring kernels, the
+    ping-pong kernel for 256-row tiles, for all bf16 tiles, and with 4 W ring slots) give
+    identical bits: the MFMAs of every accumulator run in the same k order."""
     say(f"gemm schedules {epi} m={m} k={k} n={n}")
     x = dev(orc.synthetic((m, k), 31, m, 0.0, 1.0))
     w0 = dev(orc.synthetic((n, k), 31, n + 1, 0.0, 0.02))
@@ -363,7 +363,7 @@ def test_gemm_schedules_bit_identical(hip, ctx, epi, m, k, n):
     y0 = dev(orc.synthetic((m, n), 31, n + 3, 0.0, 1.0))
     outs = []
     try:
-        for sched in (0, 1, 2):
+        for sched in (0, 1, 2, 3):
             hip.check(hip.lib.ie_tune_gemm_schedule(sched))
             out = y0.clone()
             hip.check(hip.lib.ie_gemm_ex(ctx.handle, GEMM_EPI[epi], m, k, n, P(x), P(w0), P(w1),
@@ -372,8 +372,47 @@ def test_gemm_schedules_bit_identical(hip, ctx, epi, m, k, n):
             outs.append(host(out))
     finally:
         hip.check(hip.lib.ie_tune_gemm_schedule(2))
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
     assert np.isfinite(orc.bf16_to_f32(outs[2])).all() and outs[2][[0, m // 2, m - 1]].any()
+
+
+# The skinny kernel at M <= 16: the fp32 epilogue's 32-row tiles (K = 4096 / 14336) with the
+# last partial round in K halves (n = 8224: 257 tiles, one split; the lm_head's 128256 columns:
+# 4008 tiles, 168 split) or none (n = 4100: 129 tiles, the last with 4 rows), and the bf16 /
+# residual 16-row tiles at ragged widths.
+@pytest.mark.parametrize("epi,m,k,n", [("bf16", 16, 4096, 4096), ("resid", 9, 4096, 4112),
+                                       ("resid", 16, 14336, 4096), ("f32", 1, 14336, 4100),
+                                       ("f32", 3, 4096, 8224), ("f32", 16, 4096, 128256),
+                                       ("f32", 7, 14336, 8224)])
+def test_gemm_skinny_wide_tiles(hip, ctx, epi, m, k, n):
+    """M <= 16 products, the split tiles handing partials over through device-scope stores and
+    an arrival counter: against the oracle, and bit-identical on a second call (the counters were
+    reset by the first call's finishers)."""
+    say(f"gemm_ex skinny 32-row tiles {epi} m={m} k={k} n={n}")
+    x = orc.synthetic((m, k), 41, m, 0.0, 1.0)
+    w0 = orc.synthetic((n, k), 41, n + 1, 0.0, 0.02)
+    y0 = orc.synthetic((m, n), 41, n + 3, 0.0, 1.0)
+    dx, dw = dev(x), dev(w0)
+    outs = []
+    for _ in range(2):
+        if epi == "f32":
+            out = torch.empty(m, n, dtype=torch.float32, device="cuda")
+        else:
+            out = dev(y0) if epi == "resid" else bf16_empty(m, n)
+        hip.check(hip.lib.ie_gemm_ex(ctx.handle, GEMM_EPI[epi], m, k, n, P(dx), P(dw), P(dw),
+                                     P(out)))
+        sync()
+        outs.append(host(out))
+    assert np.array_equal(outs[0], outs[1])
+    got = outs[0]
+    if epi == "f32":
+        assert_close(got, orc.matmul(x, w0, out_f32=True), tol=1e-4, what="skinny f32")
+        return
+    want = orc.matmul(x, w0) if epi == "bf16" else orc.residual_add(y0, orc.matmul(x, w0))
+    assert_close(orc.bf16_to_f32(got), orc.bf16_to_f32(want), what=f"skinny {epi}")
+    assert_bf16_close(got, want, ulps=2, what=f"skinny {epi}",
+                      outlier_frac=1e-3 if epi == "resid" else 0.0)
 
 
 @pytest.mark.parametrize("epi", ["bf16", "resid"])
