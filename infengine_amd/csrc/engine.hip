@@ -591,10 +591,26 @@ int prefill_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
   // split K's partials after q/k/v and the rotated q (the rest of the workspace)
   g.split_ws = reinterpret_cast<float*>(wsb + prefill_attn_bytes(S));
   g.split_ws_bytes = (long long)(ie_attn_workspace_size(S) - prefill_attn_bytes(S));
-  skinny_split(c, kGemmBf16, g, c->d_sk_part);
-  IE_TRY(launch_gemm(kGemmBf16, g, st));
-  IE_TRY(launch_qkv_rope_scatter(S, start_pos, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl,
-                                 nullptr, 0, st, block_table, n_pages));
+  // RoPE and the K/V scatter in the product's epilogue where the product runs on the 192 x 256
+  // ping-pong tiles (long prompts), else the product to [S][6144] and the scatter kernel
+  GemmParams f = g;
+  f.y = qrot;
+  f.ldy = kHidden;
+  f.rope_cos = W.rope.cos;
+  f.rope_sin = W.rope.sin;
+  f.k_cache = kvl;
+  f.v_cache = vpl;
+  f.block_table = block_table;
+  f.n_pages = n_pages;
+  f.start_pos = start_pos;
+  const int fused = launch_qkv_rope_prefill(f, st);
+  if (fused < 0) return fused;
+  if (fused != IE_OK) {
+    skinny_split(c, kGemmBf16, g, c->d_sk_part);
+    IE_TRY(launch_gemm(kGemmBf16, g, st));
+    IE_TRY(launch_qkv_rope_scatter(S, start_pos, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl,
+                                   nullptr, 0, st, block_table, n_pages));
+  }
   AttnPrefillParams a{qrot, kvl, vpl, attn_buffer, S, start_pos, block_table, n_pages};
   IE_TRY(launch_attn_prefill(a, st));
   GemmParams o{};

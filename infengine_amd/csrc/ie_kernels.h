@@ -140,9 +140,11 @@ enum GemmEpi : int {
   kGemmResid = 1,   // Y = bf16(Y + bf16(acc))
   kGemmF32 = 2,     // Yf = acc
   kGemmSwiglu = 3,  // Y[:, j] = bf16(silu(bf16(acc_gate)) * bf16(acc_up)) (two weights)
-  // Batched-decode QKV projection (skinny GEMM only, M <= 16, the [q|k|v] weights as w0/w1/w2):
-  // bf16(acc), RoPE on q and k at position d_seq_len[m] - 1, q to q_out [M][32][128], k and v to
-  // sequence m's cache row (rope.cu:53-64, attn.cu:345-352).
+  // QKV projection with RoPE and the K/V cache write (the [q|k|v] weights as w0/w1/w2):
+  // bf16(acc), RoPE on q and k, q to y [M][32][128], k and v to the cache (rope.cu:53-64,
+  // attn.cu:345-352).  Batched decode (skinny GEMM, M <= 16): row m at position d_seq_len[m] - 1
+  // of sequence m's cache.  Prefill (launch_qkv_rope_prefill, the 192 x 256 ping-pong tiles): row
+  // m at position start_pos + m of one sequence's cache.
   kGemmQkvRope = 4,
 };
 struct GemmParams {
@@ -164,7 +166,8 @@ struct GemmParams {
   const int* block_table;  // paged KV: [M][table_stride] page ids; k/v_cache = this layer's K/V
   int table_stride;        // head-0 planes of page 0 (pages kPageElems apart); ids outside
   int n_pages;             // [0, n_pages) are not written
-  const int* d_seq_len;    // [M]
+  const int* d_seq_len;    // [M] (batched decode)
+  int start_pos;           // prefill: position of row 0 (block_table: one sequence's table)
   // Skinny GEMM (M <= 16) only: RMSNorm of the X rows inside the projection (rmsnorm.cu:49-61).
   // Consumer (SwiGLU / QKV + RoPE): x holds the raw rows, x_norm_w the norm weight [K] and ss_in
   // [16][ss_parts] partial sums of squares of the rows (rows past M zero); the product uses the
@@ -172,8 +175,8 @@ struct GemmParams {
   const float* ss_in;
   int ss_parts;
   const uint16_t* x_norm_w;
-  // Producer (kGemmResid): also writes this workgroup's sums of squares of the 16 new rows to
-  // ss_out[row][blockIdx] (N / 16 per row).
+  // Producer (kGemmResid, N = 16 kNormParts): also writes the sums of squares of each 16
+  // columns of the new rows to ss_out[row][n / 16].
   float* ss_out;
   // Split K (bf16 / residual / SwiGLU epilogues, 16 < M <= kSplitMaxRows): scratch for
   // fp32 partial products [splits][M][N]; when set and the tiles would fill at most half the
@@ -199,6 +202,11 @@ inline size_t gemm_split_bytes(int M, int n) {
   return M <= kSplitMaxRows ? (size_t)(4 * M > 2048 ? 4 * M : 2048) * n * sizeof(float) : 0;
 }
 int launch_gemm(int epi, const GemmParams& p, hipStream_t st);
+// Prefill QKV projection with RoPE and the K/V scatter in the GEMM epilogue (kGemmQkvRope,
+// start_pos): launched when the bf16 product would run as one launch of the 192 x 256
+// ping-pong tiles; returns 1 without launching otherwise (the caller then runs the bf16
+// product and the scatter kernel, with the same results bit for bit).
+int launch_qkv_rope_prefill(const GemmParams& p, hipStream_t st);
 
 // ------------------------------------------------------------ weight arena (engine.hip)
 constexpr int kLayerFields = 9;

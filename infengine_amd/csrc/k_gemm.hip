@@ -278,7 +278,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t w_group(const GemmParams& p, i
     base = ((r & 63) < 32 ? p.w0 : p.w1) + (size_t)col * p.K;
     rows = p.N - col;
   } else {
-    const int R = ntile * BN + r;
+    int R = ntile * BN + r;
+    if constexpr (EPI == kGemmQkvRope) {
+      // tile rows 0..95: the first halves (dims 0..63) of RoPE pairs P = 96 ntile + r, rows
+      // 96..191 the second halves (dims 64..127) of the same pairs; pair P is dim P % 64 of head
+      // P / 64 of [q|k|v] (a group of 8 rows stays within one half-head: consecutive rows)
+      static_assert(BN == 192, "QKV + RoPE tiles hold 96 pairs");
+      const int half = r >= 96 ? 1 : 0, P = ntile * 96 + r - 96 * half;
+      R = (P >> 6) * kHeadDim + 64 * half + (P & 63);
+    }
     const int e0 = min(p.n0, p.N), e1 = min(p.n0 + p.n1, p.N);
     if (R < e0) {
       base = p.w0 + (size_t)R * p.K;
@@ -489,6 +497,60 @@ __device__ __forceinline__ void tile_copy_out(const GemmParams& p, const uint2* 
       if (n + 8 <= p.N) store16(dst, lo, hi, ld16);
       else *reinterpret_cast<uint2*>(dst) = lo;
     }
+  }
+}
+
+// Copy-out of the prefill QKV + RoPE tile staged in LDS as [256][48] 8-byte units: unit u < 24
+// holds the first halves of pairs 96 ntile + 4u .. +3 (pair P: head P / 64, dims P % 64 and
+// P % 64 + 64), unit 24 + u their second halves.  Each thread takes 4 pairs of one row: RoPE at
+// position start_pos + m on q and k (the scatter kernel's pairing and roundings, on the same
+// bf16 values), q to y [M][32][128], k and v to this layer's cache planes (or pages).
+template <int THREADS, class SW>
+__device__ __forceinline__ void rope_copy_out(const GemmParams& p, const uint2* ot, int m0,
+                                              int ntile, int tid, SW swz) {
+  constexpr int UPR = 48, QUADS = 24;
+#pragma unroll 4
+  for (int it = tid; it < 256 * QUADS; it += THREADS) {
+    const int r = it / QUADS, u = it % QUADS;
+    const int m = m0 + r;
+    if (m >= p.M) continue;
+    const uint2 lo = ot[r * UPR + swz(u, r)], hi = ot[r * UPR + swz(QUADS + u, r)];
+    const int P = ntile * 96 + 4 * u;
+    const int head = P >> 6, j = P & 63;
+    const int pos = p.start_pos + m;
+    uint2 o0 = lo, o1 = hi;
+    if (head < kQHeads + kKVHeads) {
+      const float4 c = *reinterpret_cast<const float4*>(p.rope_cos + (size_t)pos * 64 + j);
+      const float4 sn = *reinterpret_cast<const float4*>(p.rope_sin + (size_t)pos * 64 + j);
+      const float a[4] = {bf_lo(lo.x), bf_hi(lo.x), bf_lo(lo.y), bf_hi(lo.y)};
+      const float b[4] = {bf_lo(hi.x), bf_hi(hi.x), bf_lo(hi.y), bf_hi(hi.y)};
+      const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {sn.x, sn.y, sn.z, sn.w};
+      float va[4], vb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        va[e] = rope_lo(a[e], b[e], cc[e], ss[e]);
+        vb[e] = rope_hi(a[e], b[e], cc[e], ss[e]);
+      }
+      o0 = make_uint2(pack_bf2(va[0], va[1]), pack_bf2(va[2], va[3]));
+      o1 = make_uint2(pack_bf2(vb[0], vb[1]), pack_bf2(vb[2], vb[3]));
+    }
+    uint16_t* dst;
+    if (head < kQHeads) {
+      dst = p.y + ((size_t)m * kQHeads + head) * kHeadDim;
+    } else {
+      const bool is_k = head < kQHeads + kKVHeads;
+      const int kvh = head - kQHeads - (is_k ? 0 : kKVHeads);
+      uint16_t* const plane = is_k ? p.k_cache : p.v_cache;
+      if (p.block_table) {  // paged: row pos % kPagePos of the page holding block pos / kPagePos
+        const int page = p.block_table[pos / kPagePos];
+        if (page < 0 || page >= p.n_pages) continue;
+        dst = plane + (size_t)page * kPageElems + ((size_t)kvh * kPagePos + pos % kPagePos) * kHeadDim;
+      } else {
+        dst = plane + ((size_t)kvh * kMaxCtx + pos) * kHeadDim;
+      }
+    }
+    *reinterpret_cast<uint2*>(dst + j) = o0;
+    *reinterpret_cast<uint2*>(dst + j + 64) = o1;
   }
 }
 
@@ -825,8 +887,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_pp_kernel(GemmParams p, int m_tiles) {
   using C = PC<BN, BM, NWR>;
   constexpr int NA = C::NA, NB = C::NB, WL = C::WL, XL = C::XL, PL = C::PL, KS = C::KS;
-  static_assert(EPI == kGemmBf16 || EPI == kGemmResid || EPI == kGemmSwiglu, "bf16 epilogues");
+  static_assert(EPI == kGemmBf16 || EPI == kGemmResid || EPI == kGemmSwiglu || EPI == kGemmQkvRope,
+                "bf16 epilogues");
   static_assert(EPI != kGemmSwiglu || BN == 256, "SwiGLU tiles are 256 W rows");
+  static_assert(EPI != kGemmQkvRope || (BN == 192 && BM == 256), "QKV + RoPE: 192 x 256 tiles");
   __shared__ u32x4_t lds[C::TOTAL];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1000,7 +1064,8 @@ void gemm_pp_kernel(GemmParams p, int m_tiles) {
     }
   }
   __syncthreads();
-  tile_copy_out<512, BM, UPR, EPI>(p, ot, y, m0, ntile * OUTN, tid, swz);
+  if constexpr (EPI == kGemmQkvRope) rope_copy_out<512>(p, ot, m0, ntile, tid, swz);
+  else tile_copy_out<512, BM, UPR, EPI>(p, ot, y, m0, ntile * OUTN, tid, swz);
 }
 
 }  // namespace pp
@@ -1327,6 +1392,30 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
   const int rc = launch_split(epi, p, st);
   if (rc != 1) return rc;
   return launch_tiled(epi, p, st, true);
+}
+
+}  // namespace ie
+
+namespace ie {
+
+int launch_qkv_rope_prefill(const GemmParams& p, hipStream_t st) {
+  IE_REQUIRE(p.N == kQKVDim && p.K == kHidden && p.n0 == kHidden && p.n1 == kKVDim && p.y &&
+                 p.k_cache && p.v_cache && p.rope_cos && p.rope_sin && !p.d_seq_len &&
+                 p.start_pos >= 0,
+             "qkv_rope_prefill: the [q|k|v] projection of one sequence");
+  if (g_gemm_schedule < 1 || gemm_skinny_fits(p) || gemm_skinny_mb_fits(kGemmBf16, p)) return 1;
+  // the bf16 product's own choice (launch_gemm): no K split (up to kSplitMaxRows rows the
+  // launcher may split, and picks smaller tiles), the 192 x 256 tile, whole rounds
+  if (p.M <= kSplitMaxRows) return 1;
+  int best = kTileSmall;
+  for (int k = kTileWide; k < kTileKinds; ++k)
+    if (tile_ok(k, kGemmBf16, p) &&
+        tile_cost(k, kGemmBf16, p.M, p.N) < tile_cost(best, kGemmBf16, p.M, p.N))
+      best = k;
+  const long long tiles = tile_count(kTileBig192, kGemmBf16, p.M, p.N);
+  if (best != kTileBig192 || (tiles > 256 && tiles % 256 != 0)) return 1;
+  if (g_gemm_schedule == 3) return launch_pp<kGemmQkvRope, 192, 256, 4>(p, st);
+  return launch_pp<kGemmQkvRope, 192, 256>(p, st);
 }
 
 }  // namespace ie

@@ -143,6 +143,58 @@ def test_prefill_2048_config4(hip, model, oracle_model, noise_floor):
         report_close(orc.bf16_to_f32(gkv[1, 1, :, p]), orc.bf16_to_f32(v1), what=f"layer-1 V row {p}")
 
 
+@pytest.mark.parametrize("S", [2048, 2000])
+def test_prefill_fused_qkv_rope_equals_scatter(hip, model, S):
+    """The prefill QKV projection with RoPE and the K/V write in its epilogue (ping-pong 192 x 256
+    tiles, ie_tune_gemm_schedule >= 1) against the bf16 product + scatter kernel (schedule 0: the
+    DMA-ring kernels, no fusion): residual rows, every K/V row and the logits bit for bit, on the
+    reference-layout cache (S = 2000: a last row tile of 208 rows) and for a chunk at start
+    position 1000 over shuffled pages."""
+    from infengine_amd.engine import Context, Request
+    rng = np.random.default_rng(S)
+    ids = rng.integers(0, V, S + 1000).astype(np.int32)
+    c = Context(0, graph=False)
+    page_elems = hip.lib.ie_kv_page_size() // 2
+    nblk = (S + 1000 + 63) // 64
+    order = rng.permutation(nblk + 2)[:nblk].astype(np.int32)
+    d_table = torch.from_numpy(order).cuda()
+    outs = {}
+    try:
+        for sched in (0, 2):
+            hip.check(hip.lib.ie_tune_gemm_schedule(sched))
+            say(f"ie_prefill S={S}, gemm schedule {sched}")
+            req = Request(c, model, max_seq_len=S + 1008)
+            req.tokens[:S + 1000] = torch.from_numpy(ids).cuda()
+            tok = req.prefill(S)
+            torch.cuda.synchronize()
+            res = [tok, host(req.logits).copy(), host(req.data[:S].view(torch.int16)).copy(),
+                   req.kv.clone()]
+            say(f"ie_prefill_paged_chunk start 1000, {S} tokens, gemm schedule {sched}")
+            pool = torch.zeros((nblk + 2) * page_elems, dtype=torch.int16, device="cuda")
+            lg = torch.zeros(V, dtype=torch.float32, device="cuda")
+            out = torch.zeros(1, dtype=torch.int32, device="cuda")
+            # positions 0..999 first (the chunk attends to them), then the chunk under test
+            hip.check(hip.lib.ie_prefill_paged_chunk(
+                c.handle, model.ref(), 0, 1000, _ptr(req.tokens), _ptr(req.data), _ptr(req.aux),
+                _ptr(req.attn), _ptr(lg), _ptr(out), _ptr(req.workspace), _ptr(pool), nblk + 2,
+                _ptr(d_table)))
+            tok_c = hip.check(hip.lib.ie_prefill_paged_chunk(
+                c.handle, model.ref(), 1000, S, _ptr(req.tokens), _ptr(req.data), _ptr(req.aux),
+                _ptr(req.attn), _ptr(lg), _ptr(out), _ptr(req.workspace), _ptr(pool), nblk + 2,
+                _ptr(d_table)))
+            torch.cuda.synchronize()
+            res += [tok_c, host(lg).copy(), pool.clone()]
+            outs[sched] = res
+            del req, pool
+    finally:
+        hip.check(hip.lib.ie_tune_gemm_schedule(2))
+    a, b = outs[0], outs[2]
+    assert a[0] == b[0] and np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2])
+    assert torch.equal(a[3], b[3])
+    assert a[4] == b[4] and np.array_equal(a[5], b[5]) and torch.equal(a[6], b[6])
+    c.close()
+
+
 # ---------------------------------------------------------------- config 5, bs = 1
 def test_generate_512_then_256_config5(hip, model, oracle_model, noise_floor):
     """ie_generate with a 512-token prompt and 256 decode steps (KV to 768 positions) equals the
