@@ -371,6 +371,9 @@ def main() -> int:
     ap.add_argument("--attn-only", action="store_true",
                     help="only the prefill attention at S = --prefill-len (for profiling it); "
                          "prints its JSON")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the --prefill-len prefill of the full model, 3 untimed + 3 timed "
+                         "(for a kernel trace of whole prefills); prints its JSON")
     ap.add_argument("--no-config-legs", action="store_true",
                     help="skip the configs 1-3 legs (GPU) and the per-config CPU figures")
     ap.add_argument("--calibration-copy", action="store_true",
@@ -402,6 +405,28 @@ def main() -> int:
     if args.attn_only:
         print(json.dumps({"prefill_attention": prefill_attention(ctx, args.prefill_len or 2048)}),
               flush=True)
+        ctx.close()
+        return 0
+    if args.prefill_only:
+        P = args.prefill_len or 2048
+        W = ModelWeights.random_init(seed=0, std=0.02)
+        req = Request(ctx, W, max_seq_len=P + 8)
+        req.tokens[:P] = torch.from_numpy(
+            np.random.default_rng(0).integers(0, VOCAB, P).astype(np.int32)).cuda()
+        for _ in range(3):
+            req.prefill(P)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            tok = req.prefill(P)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / 3 * 1e3
+        flops = 2.0 * P * LAYER_GEMM_PARAMS * LAYERS
+        print(json.dumps({"prefill": {"seq_len": P, "ms": round(ms, 3), "token": tok,
+                                      "layer_gemm_tflops_per_s": round(flops / ms / 1e9, 1)}}),
+              flush=True)
+        del req
+        W.free()
         ctx.close()
         return 0
     log("random-init weights (16.06 GB)")

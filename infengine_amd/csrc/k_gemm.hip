@@ -882,16 +882,16 @@ struct OutSwz {
   }
 };
 
+// Tile b of the nb tiles of p (the LDS ring: at least PC<BN, BM, NWR>::TOTAL chunks).
 template <int EPI, int BN, int BM, int NWR>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gemm_pp_kernel(GemmParams p, int m_tiles) {
+__device__ __forceinline__ void pp_tile(const GemmParams& p, int m_tiles, int b, int nb,
+                                        u32x4_t* lds) {
   using C = PC<BN, BM, NWR>;
   constexpr int NA = C::NA, NB = C::NB, WL = C::WL, XL = C::XL, PL = C::PL, KS = C::KS;
   static_assert(EPI == kGemmBf16 || EPI == kGemmResid || EPI == kGemmSwiglu || EPI == kGemmQkvRope,
                 "bf16 epilogues");
   static_assert(EPI != kGemmSwiglu || BN == 256, "SwiGLU tiles are 256 W rows");
   static_assert(EPI != kGemmQkvRope || (BN == 192 && BM == 256), "QKV + RoPE: 192 x 256 tiles");
-  __shared__ u32x4_t lds[C::TOTAL];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -899,7 +899,7 @@ void gemm_pp_kernel(GemmParams p, int m_tiles) {
   // the wave's output block: W rows wn * WTN .., X rows wm * 64 ..; with KG = 2 its k32 half grp
   const int wn = C::KG == 1 ? grp : gw >> 1, wm = C::KG == 1 ? gw : gw & 1;
   int mtile, ntile;
-  tile_of<1>(blockIdx.x, gridDim.x, m_tiles, mtile, ntile);
+  tile_of<1>(b, nb, m_tiles, mtile, ntile);
   const int m0 = mtile * BM;
   const int KT = p.K / 64;
 
@@ -1068,6 +1068,28 @@ void gemm_pp_kernel(GemmParams p, int m_tiles) {
   else tile_copy_out<512, BM, UPR, EPI>(p, ot, y, m0, ntile * OUTN, tid, swz);
 }
 
+template <int EPI, int BN, int BM, int NWR>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_pp_kernel(GemmParams p, int m_tiles) {
+  __shared__ u32x4_t lds[PC<BN, BM, NWR>::TOTAL];
+  pp_tile<EPI, BN, BM, NWR>(p, m_tiles, blockIdx.x, gridDim.x, lds);
+}
+
+// Two column ranges of one product in one launch: workgroups 0 .. nb1-1 take the BM1-row X
+// tiles of p1, the rest the BM2-row tiles of p2 (gate/up at S = 2048: three rounds of 256 x 256
+// tiles, then the last 2048 columns as 256 x 128 tiles, each starting on a CU as soon as the CU's
+// third big tile ends instead of after a kernel boundary).
+template <int EPI, int BN, int BM1, int BM2>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_pp_dual_kernel(GemmParams p1, int m_tiles1, int nb1, GemmParams p2, int m_tiles2) {
+  constexpr int T1 = PC<BN, BM1, 3>::TOTAL, T2 = PC<BN, BM2, 3>::TOTAL;
+  __shared__ u32x4_t lds[T1 > T2 ? T1 : T2];
+  if ((int)blockIdx.x < nb1)
+    pp_tile<EPI, BN, BM1, 3>(p1, m_tiles1, blockIdx.x, nb1, lds);
+  else
+    pp_tile<EPI, BN, BM2, 3>(p2, m_tiles2, blockIdx.x - nb1, gridDim.x - nb1, lds);
+}
+
 }  // namespace pp
 
 }  // namespace wide
@@ -1092,6 +1114,20 @@ int launch_pp(const GemmParams& p, hipStream_t st) {
   IE_REQUIRE(blocks <= 0x7fffffff && p.k_splits <= 1, "gemm: ping-pong tiles");
   hipLaunchKernelGGL((wide::pp::gemm_pp_kernel<EPI, WBN, XBM, NW>), dim3((unsigned)blocks), dim3(512), 0,
                      st, p, m_tiles);
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
+template <int EPI>
+int launch_pp_dual(const GemmParams& head, const GemmParams& tail, hipStream_t st) {
+  const int m1 = (head.M + 255) / 256, m2 = (tail.M + 127) / 128;
+  const int n1 = (EPI == kGemmSwiglu) ? (head.N + 127) / 128 : (head.N + 255) / 256;
+  const int n2 = (EPI == kGemmSwiglu) ? (tail.N + 127) / 128 : (tail.N + 255) / 256;
+  const long long b1 = (long long)m1 * n1, b2 = (long long)m2 * n2;
+  IE_REQUIRE(b1 + b2 <= 0x7fffffff && head.k_splits <= 1 && tail.k_splits <= 1,
+             "gemm: ping-pong tiles");
+  hipLaunchKernelGGL((wide::pp::gemm_pp_dual_kernel<EPI, 256, 256, 128>), dim3((unsigned)(b1 + b2)),
+                     dim3(512), 0, st, head, m1, (int)b1, tail, m2);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
@@ -1235,7 +1271,8 @@ GemmParams column_tail(int epi, const GemmParams& p, int c) {
 // a second launch over the remaining output columns with the shape that fills the chip for
 // them (gate/up at S = 2048: 3 rounds of 256 x 256 tiles, then the last 2048 columns as one
 // round of 256 x 128 tiles, in place of a half-empty fourth round).
-int launch_tiled(int epi, const GemmParams& p, hipStream_t st, bool split) {
+// Cheapest tile shape for p.
+int best_kind(int epi, const GemmParams& p) {
   int best = kTileSmall;
   double best_cost = tile_cost(kTileSmall, epi, p.M, p.N);
   for (int k = kTileWide; k < kTileKinds; ++k) {
@@ -1243,6 +1280,12 @@ int launch_tiled(int epi, const GemmParams& p, hipStream_t st, bool split) {
     const double c = tile_cost(k, epi, p.M, p.N);
     if (c < best_cost) best = k, best_cost = c;
   }
+  return best;
+}
+
+int launch_tiled(int epi, const GemmParams& p, hipStream_t st, bool split) {
+  const int best = best_kind(epi, p);
+  const double best_cost = tile_cost(best, epi, p.M, p.N);
   if (split) {
     const TileKind& t = kTiles[best];
     const int tn = epi == kGemmSwiglu ? t.tn_swiglu : t.tn;
@@ -1257,6 +1300,14 @@ int launch_tiled(int epi, const GemmParams& p, hipStream_t st, bool split) {
       if ((double)(tiles / 256) * t.unit + tail_cost < best_cost) {
         GemmParams head = p;
         head.N = c;
+        // 256 x 256 then 256 x 128 ping-pong tiles: one launch
+        if (g_gemm_schedule >= 2 && best == kTileBig && best_kind(epi, tail) == kTileWide) {
+          switch (epi) {
+            case kGemmBf16: return launch_pp_dual<kGemmBf16>(head, tail, st);
+            case kGemmResid: return launch_pp_dual<kGemmResid>(head, tail, st);
+            case kGemmSwiglu: return launch_pp_dual<kGemmSwiglu>(head, tail, st);
+          }
+        }
         const int rc = launch_kind(best, epi, head, st);
         if (rc != IE_OK) return rc;
         return launch_tiled(epi, tail, st, false);
