@@ -134,9 +134,9 @@ int attn_decode(const uint16_t* q, uint16_t* kvl, uint16_t* out, const DecodeWs&
   // kAttnDirectMaxCtx one split per pair writes the output (no merge launch).  At every batch
   // size, so that a sequence's results do not depend on how many others share its step.
   a.max_splits = (batched && merge && max_len <= kAttnDirectMaxCtx) ? 1
-                 : max_len <= kAttnFusedMaxCtx                        ? kAttnFusedSplits
+                 : max_len <= kAttnFusedMaxCtx                        ? attn_fused_splits(max_len)
                                                                      : kAttnSplits;
-  IE_REQUIRE(merge || a.max_splits == kAttnFusedSplits,
+  IE_REQUIRE(merge || a.max_splits <= kAttnFusedSplitsLong,
              "attn_decode: contexts past %d need the merge kernel", kAttnFusedMaxCtx);
   return launch_attn_decode(a, batch, merge, st);
 }
@@ -183,7 +183,7 @@ int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, 
     p.pos = seq_len;
     p.attn_part_o = w.part_o;
     p.attn_part_ml = w.part_ml;
-    p.attn_max_splits = kAttnFusedSplits;
+    p.attn_max_splits = attn_fused_splits(seq_len);
     IE_TRY(launch_gemv(kHidden, kEpiResid, false, p, 1, st));
   } else {
     IE_TRY(gemv_plain(kHidden, kEpiResid, attn_out, nullptr, L.transformer.w_o, nullptr,
@@ -435,8 +435,12 @@ int decode_step_impl(Context* c, const ie_model_weights* weights, int seq_len, i
     const void* key[12] = {(const void*)weights, tokenid_buff, data_buffer, attn_buffer,
                            output_distr, output_token, workspace, kv_cache,
                            (const void*)(uintptr_t)hash_bytes(weights, sizeof(*weights)),
-                           // the captured attention path depends on the context length
-                           (const void*)(uintptr_t)(attn_fused(seq_len) ? 1 : 2), wb_buf,
+                           // the captured attention path and split cap depend on the context
+                           // length
+                           (const void*)(uintptr_t)(attn_fused(seq_len)
+                                                        ? (seq_len <= kAttnFusedShortCtx ? 1 : 3)
+                                                        : 2),
+                           wb_buf,
                            nullptr};
     if (!c->graph_exec || std::memcmp(key, c->graph_key, sizeof key) != 0) {
       if (c->graph_exec) {

@@ -67,11 +67,17 @@ __host__ __device__ inline int attn_decode_splits(int ntiles, int max_splits) {
   const int n = (ntiles + 3) / 4;
   return n < 1 ? 1 : (n < max_splits ? n : max_splits);
 }
-// The O projection merges the partials itself while the context needs at most this many
-// splits (<= 1024 rows at one tile per wave; longer contexts run several tiles per wave).
-// Every O-projection workgroup reads all of them, so the cap is small: 4 measured 0.5% faster
-// per decode step than 8 at p = 600 (and 4% on the bs=16 batched step).
+// The O projection merges the partials itself (up to kAttnFusedMaxCtx).  Every O-projection
+// workgroup reads all the slots it merges, so the cap is small: 4 splits up to
+// kAttnFusedShortCtx (4 measured 0.5% faster per decode step than 8 at p = 600, and 4% on the
+// bs=16 batched step); beyond, 8 (at p = 2047 the 4-split attention took 9.2 us, twice its time
+// at p = 600, on 32 CUs).
 constexpr int kAttnFusedSplits = 4;
+constexpr int kAttnFusedSplitsLong = 8;
+constexpr int kAttnFusedShortCtx = 1024;
+inline int attn_fused_splits(int max_len) {
+  return max_len <= kAttnFusedShortCtx ? kAttnFusedSplits : kAttnFusedSplitsLong;
+}
 constexpr int kAttnFusedMaxCtx = 4096;  // beyond: merge kernel + up to kAttnSplits splits
 constexpr int kAttnDirectMaxCtx = 2048; // batched contexts up to this: one split, output written directly
 // merge = also launch the merge kernel (bf16 output in p.out)

@@ -146,21 +146,23 @@ __device__ __forceinline__ void load_step(const u32x4_t* a, const u32x4_t* b, in
 // into the staged input vector: 8 dims of one q head per item, same arithmetic as the merge
 // kernel (weights exp(m_s - max m), o = sum_s w_s o_s / sum_s w_s l_s).  The loads of an item
 // are issued before the weight stream (attn_load) and merged after it is in flight (attn_merge).
+template <int MS>
 struct AttnItem {
-  float2 ml[kAttnFusedSplits];
-  float4 oa[kAttnFusedSplits], ob[kAttnFusedSplits];
+  float2 ml[MS];
+  float4 oa[MS], ob[MS];
 };
 
-// All kAttnFusedSplits slots are loaded (they lie inside the partials buffer, which holds
-// kAttnSplits per kv head; attn_merge reads only the first ns).  The loads neither branch nor
-// depend on ns (a device value in graph replays): either would let the compiler issue them
-// after the weight stream, or make its wait at the merge conservative, and the staging would
-// then wait for the weights.
-__device__ __forceinline__ void attn_load(const GemvParams& p, int i, AttnItem& a) {
+// All MS slots are loaded (they lie inside the partials buffer, which holds kAttnSplits per kv
+// head; attn_merge reads only the first ns).  The loads neither branch nor depend on ns (a
+// device value in graph replays): either would let the compiler issue them after the weight
+// stream, or make its wait at the merge conservative, and the staging would then wait for the
+// weights.
+template <int MS>
+__device__ __forceinline__ void attn_load(const GemvParams& p, int i, AttnItem<MS>& a) {
   const int h = i >> 4, c = i & 15;
   const size_t slot0 = ((size_t)(h / kGQA) * kAttnSplits) * kGQA + (h % kGQA);
 #pragma unroll
-  for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
+  for (int sp = 0; sp < MS; ++sp) {
     const size_t slot = slot0 + (size_t)sp * kGQA;
     a.ml[sp] = *reinterpret_cast<const float2*>(p.attn_part_ml + slot * 2);
     const float4* po = reinterpret_cast<const float4*>(p.attn_part_o + slot * kHeadDim + c * 8);
@@ -169,14 +171,15 @@ __device__ __forceinline__ void attn_load(const GemvParams& p, int i, AttnItem& 
   }
 }
 
-__device__ __forceinline__ u32x4_t attn_merge(const AttnItem& a, int ns) {
+template <int MS>
+__device__ __forceinline__ u32x4_t attn_merge(const AttnItem<MS>& a, int ns) {
   float M = -INFINITY;
 #pragma unroll
-  for (int sp = 0; sp < kAttnFusedSplits; ++sp)
+  for (int sp = 0; sp < MS; ++sp)
     if (sp < ns) M = fmaxf(M, a.ml[sp].x);
   float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int sp = 0; sp < kAttnFusedSplits; ++sp) {
+  for (int sp = 0; sp < MS; ++sp) {
     if (sp < ns) {
       const float w = a.ml[sp].y > 0.f ? __expf(a.ml[sp].x - M) : 0.f;
       L = fmaf(a.ml[sp].y, w, L);
@@ -231,7 +234,9 @@ __device__ __forceinline__ void consume_step(const GemvParams& p, const u32x4_t*
 // ONE: one pair per wave (the default), unrolled at compile time so every wait is exact; the
 // general loop for more pairs per wave is a separate instance because its conditional loads
 // more than double the register count.
-template <int K, int EPI, bool NORM, int WAVES, bool ATTN, bool ONE>
+// ATTN: 0, or the split slots (kAttnFusedSplits / kAttnFusedSplitsLong) the O projection merges
+// into its input.
+template <int K, int EPI, bool NORM, int WAVES, int ATTN, bool ONE>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   constexpr int T = WAVES * 64;
   constexpr int NC = K / 512;                 // 16-byte chunks per lane per row
@@ -256,9 +261,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   // join conservative, which would stall the staging until the weights arrive.
   const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(p.x + (size_t)row * p.x_stride);
   u32x4_t xin[XC], nwin[XC];
-  AttnItem ai[ATTN ? AI : 1];
+  AttnItem<ATTN ? ATTN : 1> ai[ATTN ? AI : 1];
   int ns = 0;
-  if constexpr (ATTN) {
+  if constexpr (ATTN != 0) {
     static_assert(K == kQHeads * kHeadDim && !NORM, "attention input: the O projection only");
 #pragma unroll
     for (int j = 0; j < AI; ++j) attn_load(p, min(tid + j * T, kQHeads * kHeadDim / 8 - 1), ai[j]);
@@ -282,7 +287,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   issue_step<K, EPI, G, NG>(p, first, lane, 0, a0, b0);
   issue_step<K, EPI, G, NG>(p, first, lane, 1, a1, b1);
 
-  if constexpr (ATTN) {
+  if constexpr (ATTN != 0) {
 #pragma unroll
     for (int j = 0; j < AI; ++j)
       if (tid + j * T < kQHeads * kHeadDim / 8) xs[tid + j * T] = attn_merge(ai[j], ns);
@@ -334,13 +339,17 @@ int launch_o(const GemvParams& p, int rows, hipStream_t st) {
   dim3 grid((waves + WAVES - 1) / WAVES, rows);
   if constexpr (K == kQHeads * kHeadDim && EPI == kEpiResid && !NORM) {
     if (p.attn_part_o) {
-      hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, true, ONE>), grid, dim3(WAVES * 64), 0,
-                         st, p);
+      if (p.attn_max_splits <= kAttnFusedSplits)
+        hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, kAttnFusedSplits, ONE>), grid,
+                           dim3(WAVES * 64), 0, st, p);
+      else
+        hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, kAttnFusedSplitsLong, ONE>), grid,
+                           dim3(WAVES * 64), 0, st, p);
       IE_CHECK_LAUNCH();
       return IE_OK;
     }
   }
-  hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, false, ONE>), grid, dim3(WAVES * 64), 0, st, p);
+  hipLaunchKernelGGL((gemv_kernel<K, EPI, NORM, WAVES, 0, ONE>), grid, dim3(WAVES * 64), 0, st, p);
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
@@ -418,7 +427,7 @@ int launch_gemv(int K, int epi, bool norm, GemvParams p, int rows, hipStream_t s
              "launch_gemv: epilogue %d supports one row only", epi);
   IE_REQUIRE(!p.attn_part_o || (K == kQHeads * kHeadDim && epi == kEpiResid && !norm && rows == 1 &&
                                 p.attn_part_ml && p.attn_max_splits >= 1 &&
-                                p.attn_max_splits <= kAttnFusedSplits &&
+                                p.attn_max_splits <= kAttnFusedSplitsLong &&
                                 (p.d_seq_len || (p.pos >= 1 && p.pos <= kMaxCtx))),
              "launch_gemv: attention-partials input is for the O projection only");
   if (p.ppw <= 0) p.ppw = default_ppw(p.n_pairs);
