@@ -568,9 +568,15 @@ void skinny_split(Context* c, int epi, GemmParams& g, float* part) {
   g.sk_cnt = c->d_counters + kCntSkinny;
 }
 
+// aux_ready: aux_buffer already holds this layer's input RMSNorm of data_buffer (written by
+// the previous layer's down-projection reduction).  next_norm_w: the next layer's input norm
+// weight, or nullptr; *aux_next is set when this layer left that norm in aux_buffer (the down
+// projection ran with K split and its reduction applied the norm).
 int prefill_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, int start_pos,
                   int S, ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
-                  void* workspace, void* kv_cache, const int* block_table, int n_pages) {
+                  void* workspace, void* kv_cache, const int* block_table, int n_pages,
+                  bool aux_ready, const uint16_t* next_norm_w, bool* aux_next) {
+  if (aux_next) *aux_next = false;
   char* wsb = static_cast<char*>(workspace);
   uint16_t* qkv = reinterpret_cast<uint16_t*>(wsb);
   uint16_t* qrot = reinterpret_cast<uint16_t*>(wsb + align256((size_t)S * kQKVDim * 2));
@@ -579,7 +585,7 @@ int prefill_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
   uint16_t* kvl = block_table ? static_cast<uint16_t*>(kv_cache) + (size_t)l * kPageLayer
                               : kv_layer(kv_cache, l);
   uint16_t* vpl = kvl + (size_t)kKVHeads * (block_table ? kPageHead : kKVPlane);
-  IE_TRY(launch_rmsnorm(S, data_buffer, L.input_layernorm, aux_buffer, st));
+  if (!aux_ready) IE_TRY(launch_rmsnorm(S, data_buffer, L.input_layernorm, aux_buffer, st));
   GemmParams g{};
   g.x = aux_buffer;
   g.w0 = L.transformer.w_q;
@@ -629,8 +635,13 @@ int prefill_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
   o.split_ws = reinterpret_cast<float*>(wsb);  // q/k/v and rotated q are dead
   o.split_ws_bytes = (long long)std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S));
   skinny_split(c, kGemmResid, o, c->d_sk_part);
+  // with K split the reduction applies the post-attention RMSNorm too
+  int normed = 0;
+  o.rn_w = L.post_attention_layernorm;
+  o.rn_out = aux_buffer;
+  o.rn_done = &normed;
   IE_TRY(launch_gemm(kGemmResid, o, st));
-  IE_TRY(launch_rmsnorm(S, data_buffer, L.post_attention_layernorm, aux_buffer, st));
+  if (!normed) IE_TRY(launch_rmsnorm(S, data_buffer, L.post_attention_layernorm, aux_buffer, st));
   GemmParams gu{};
   gu.x = aux_buffer;
   gu.w0 = L.ffn_block.w_gate;
@@ -658,7 +669,14 @@ int prefill_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
   dn.split_ws_bytes = (long long)(std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
                                   align256((size_t)S * kFFN * 2));
   skinny_split(c, kGemmResid, dn, c->d_sk_part);
+  int next_normed = 0;
+  if (next_norm_w) {
+    dn.rn_w = next_norm_w;
+    dn.rn_out = aux_buffer;
+    dn.rn_done = &next_normed;
+  }
   IE_TRY(launch_gemm(kGemmResid, dn, st));
+  if (aux_next) *aux_next = next_normed != 0;
   return IE_OK;
 }
 
@@ -687,9 +705,11 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int start_pos, 
   const int S = seq_len;
 
   IE_TRY(launch_emblookup(S, tokenid_buff + start_pos, W.emb_lookup, data_buffer, nullptr, 0, st));
+  bool aux_ready = false;
   for (int l = 0; l < kLayers; ++l)
     IE_TRY(prefill_layer(c, st, W, l, start_pos, S, data_buffer, aux_buffer, attn_buffer,
-                         workspace, kv_cache, block_table, n_pages));
+                         workspace, kv_cache, block_table, n_pages, aux_ready,
+                         l + 1 < kLayers ? W.layers[l + 1].input_layernorm : nullptr, &aux_ready));
   // prefill.cu:41-43: final norm, lm_head on the last row only, argmax
   IE_TRY(gemv_plain(kHidden, kEpiF32, data_buffer + (size_t)(S - 1) * kHidden, W.final_norm,
                     W.lm_head, nullptr, kVocab / 2, nullptr, output_distr, 1, kVocab, st));
@@ -743,7 +763,7 @@ int ie_decoder_layer_prefill(ie_context* c, const ie_model_weights* weights, int
   IE_REQUIRE(data_buffer && aux_buffer && attn_buffer && workspace && kv_cache,
              "decoder_layer_prefill: null buffer");
   return prefill_layer(c, c->stream, *weights, layer_idx, 0, seq_len, data_buffer, aux_buffer,
-                       attn_buffer, workspace, kv_cache, nullptr, 0);
+                       attn_buffer, workspace, kv_cache, nullptr, 0, false, nullptr, nullptr);
 }
 
 // ---------------------------------------------------------------- batched decode

@@ -189,6 +189,12 @@ struct GemmParams {
   // chip, K is split across workgroups and a reduction applies the epilogue.
   float* split_ws;
   long long split_ws_bytes;
+  // Residual epilogue with K split, N = 4096: when rn_out is set the reduction also writes
+  // rmsnorm(y) with weight rn_w to rn_out (the RMSNorm of the rows that follows the product in
+  // the layer) and sets *rn_done; otherwise the caller runs that RMSNorm itself.
+  const uint16_t* rn_w;
+  uint16_t* rn_out;
+  int* rn_done;
   int k_splits;  // set by the launcher for the wide kernel (0 / 1: no split)
   // Skinny GEMM (M <= 16): the last sk_tail of its tiles (16 rows; 32 for the fp32 epilogue
   // at K = 4096 or 14336) run as two workgroups each, one per K half, so that every CU gets the

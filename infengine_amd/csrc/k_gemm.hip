@@ -1369,6 +1369,122 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, in
   }
 }
 
+// The residual reduction followed by the RMSNorm of the same rows (N = 4096, one 256-thread
+// workgroup per row): y = bf16(y + bf16(sum)), then rn_out = bf16(bf16(y * r) * w) with r from
+// the fp32 sum of squares of the new y -- each thread owns 16-byte chunks t and t + 256 of the
+// row and sums their squares in the same order as rmsnorm_kernel, so both outputs equal the
+// reduction followed by that kernel bit for bit, without writing and re-reading y between them.
+__global__ __launch_bounds__(256) void split_reduce_norm_kernel(const float* part, int splits,
+                                                                int M, uint16_t* y, int ldy,
+                                                                const uint16_t* w,
+                                                                uint16_t* out) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t plane = (size_t)M * kHidden;
+  uint4 v[2], wv[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int n = (tid + 256 * k) * 8;
+    float4 a, b;
+    split_sum8(part + (size_t)m * kHidden + n, plane, splits, a, b);
+    const uint4 o = make_uint4(pack_bf2(a.x, a.y), pack_bf2(a.z, a.w), pack_bf2(b.x, b.y),
+                               pack_bf2(b.z, b.w));
+    uint16_t* dst = y + (size_t)m * ldy + n;
+    const uint4 r = *reinterpret_cast<const uint4*>(dst);
+    v[k] = make_uint4(pack_bf2(bf_lo(r.x) + bf_lo(o.x), bf_hi(r.x) + bf_hi(o.x)),
+                      pack_bf2(bf_lo(r.y) + bf_lo(o.y), bf_hi(r.y) + bf_hi(o.y)),
+                      pack_bf2(bf_lo(r.z) + bf_lo(o.z), bf_hi(r.z) + bf_hi(o.z)),
+                      pack_bf2(bf_lo(r.w) + bf_lo(o.w), bf_hi(r.w) + bf_hi(o.w)));
+    *reinterpret_cast<uint4*>(dst) = v[k];
+    wv[k] = reinterpret_cast<const uint4*>(w)[tid + 256 * k];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ss = fmaf(bf_lo(e[q]), bf_lo(e[q]), ss);
+      ss = fmaf(bf_hi(e[q]), bf_hi(e[q]), ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  const float rr = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)kHidden + kRmsEps);
+  uint4* o4 = reinterpret_cast<uint4*>(out + (size_t)m * kHidden);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+    const uint32_t f[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float lo = bf2f(f2bf(bf_lo(e[q]) * rr)) * bf_lo(f[q]);
+      const float hi = bf2f(f2bf(bf_hi(e[q]) * rr)) * bf_hi(f[q]);
+      o[q] = pack_bf2(lo, hi);
+    }
+    o4[tid + 256 * k] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// The QKV reduction with RoPE and the K/V scatter (prefill, kGemmQkvRope): each thread sums 4
+// RoPE pairs of one row (dims j..j+3 and j+64..j+67 of one head of [q|k|v]) over the split
+// planes in plane order, rounds to bf16 (the bf16 reduction's values), rotates q and k with the
+// scatter kernel's arithmetic at position start_pos + m, and stores q to y [M][32][128], k and v
+// to the cache (or its pages).
+__global__ __launch_bounds__(256) void split_reduce_rope_kernel(const float* part, int splits,
+                                                                GemmParams p) {
+  constexpr int kQuads = (kQHeads + 2 * kKVHeads) * 16;  // 4-pair groups per row
+  const size_t plane = (size_t)p.M * kQKVDim;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < (size_t)p.M * kQuads;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int m = (int)(i / kQuads), qd = (int)(i % kQuads);
+    const int head = qd >> 4, j = (qd & 15) * 4;
+    const float* src = part + (size_t)m * kQKVDim + head * kHeadDim + j;
+    float4 a = *reinterpret_cast<const float4*>(src);
+    float4 b = *reinterpret_cast<const float4*>(src + 64);
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4 c = *reinterpret_cast<const float4*>(src + sp * plane);
+      const float4 d = *reinterpret_cast<const float4*>(src + sp * plane + 64);
+      a.x += c.x, a.y += c.y, a.z += c.z, a.w += c.w;
+      b.x += d.x, b.y += d.y, b.z += d.z, b.w += d.w;
+    }
+    const float av[4] = {bf2f(f2bf(a.x)), bf2f(f2bf(a.y)), bf2f(f2bf(a.z)), bf2f(f2bf(a.w))};
+    const float bv[4] = {bf2f(f2bf(b.x)), bf2f(f2bf(b.y)), bf2f(f2bf(b.z)), bf2f(f2bf(b.w))};
+    const int pos = p.start_pos + m;
+    float lo[4], hi[4];
+    if (head < kQHeads + kKVHeads) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float c = p.rope_cos[(size_t)pos * 64 + j + e], sn = p.rope_sin[(size_t)pos * 64 + j + e];
+        lo[e] = rope_lo(av[e], bv[e], c, sn);
+        hi[e] = rope_hi(av[e], bv[e], c, sn);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lo[e] = av[e], hi[e] = bv[e];
+    }
+    uint16_t* dst;
+    if (head < kQHeads) {
+      dst = p.y + ((size_t)m * kQHeads + head) * kHeadDim;
+    } else {
+      const bool is_k = head < kQHeads + kKVHeads;
+      const int kvh = head - kQHeads - (is_k ? 0 : kKVHeads);
+      uint16_t* const plane_kv = is_k ? p.k_cache : p.v_cache;
+      if (p.block_table) {  // paged: row pos % kPagePos of the page holding block pos / kPagePos
+        const int page = p.block_table[pos / kPagePos];
+        if (page < 0 || page >= p.n_pages) continue;
+        dst = plane_kv + (size_t)page * kPageElems + ((size_t)kvh * kPagePos + pos % kPagePos) * kHeadDim;
+      } else {
+        dst = plane_kv + ((size_t)kvh * kMaxCtx + pos) * kHeadDim;
+      }
+    }
+    *reinterpret_cast<uint2*>(dst + j) = make_uint2(pack_bf2(lo[0], lo[1]), pack_bf2(lo[2], lo[3]));
+    *reinterpret_cast<uint2*>(dst + j + 64) = make_uint2(pack_bf2(hi[0], hi[1]), pack_bf2(hi[2], hi[3]));
+  }
+}
+
 // Split K when the best tiling is a single round that leaves at least half the chip idle, or
 // one of 128 x 128 tiles: the wide kernel's tiles times the largest K split that divides the
 // k-steps, fits one round of 256 workgroups and whose partials fit p.split_ws (at least 2),
@@ -1379,13 +1495,15 @@ int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   if (!p.split_ws || epi == kGemmF32 || p.M > kSplitMaxRows || p.N % 8 != 0 || p.ldy % 8 != 0)
     return 1;
   const bool sw = epi == kGemmSwiglu;
+  const bool rope = epi == kGemmQkvRope;
+  const int te = rope ? kGemmBf16 : epi;  // the tiling of the plain product
   if (sw && p.N % 16 != 0) return 1;
   int best = kTileSmall;
   for (int k = kTileWide; k < kTileKinds; ++k)
-    if (tile_ok(k, epi, p) && tile_cost(k, epi, p.M, p.N) < tile_cost(best, epi, p.M, p.N)) best = k;
+    if (tile_ok(k, te, p) && tile_cost(k, te, p.M, p.N) < tile_cost(best, te, p.M, p.N)) best = k;
   // a single round that leaves half the chip idle, or one of 128 x 128 tiles (the older,
   // slower kernel)
-  const long long best_tiles = tile_count(best, epi, p.M, p.N);
+  const long long best_tiles = tile_count(best, te, p.M, p.N);
   if (best_tiles > 256 || (best_tiles > 128 && best != kTileSmall)) return 1;
   // SwiGLU: one fp32 product over the gate rows then the up rows (2N columns)
   const int NP = sw ? 2 * p.N : p.N;
@@ -1410,15 +1528,24 @@ int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   if (rc != IE_OK) return rc;
   const size_t total = (size_t)p.M * p.N / 8;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 2048);
-  if (sw)
+  if (sw) {
     hipLaunchKernelGGL(split_reduce_kernel<kGemmSwiglu>, dim3(blocks), dim3(256), 0, st,
                        p.split_ws, splits, p.M, p.N, p.y, p.ldy);
-  else if (epi == kGemmResid)
+  } else if (rope) {
+    const size_t items = (size_t)p.M * (kQHeads + 2 * kKVHeads) * 16;
+    hipLaunchKernelGGL(split_reduce_rope_kernel, dim3((unsigned)std::min<size_t>((items + 255) / 256, 2048)),
+                       dim3(256), 0, st, p.split_ws, splits, p);
+  } else if (epi == kGemmResid && p.rn_out) {
+    hipLaunchKernelGGL(split_reduce_norm_kernel, dim3(p.M), dim3(256), 0, st, p.split_ws, splits,
+                       p.M, p.y, p.ldy, p.rn_w, p.rn_out);
+    if (p.rn_done) *p.rn_done = 1;
+  } else if (epi == kGemmResid) {
     hipLaunchKernelGGL(split_reduce_kernel<kGemmResid>, dim3(blocks), dim3(256), 0, st,
                        p.split_ws, splits, p.M, p.N, p.y, p.ldy);
-  else
+  } else {
     hipLaunchKernelGGL(split_reduce_kernel<kGemmBf16>, dim3(blocks), dim3(256), 0, st,
                        p.split_ws, splits, p.M, p.N, p.y, p.ldy);
+  }
   IE_CHECK_LAUNCH();
   return IE_OK;
 }
@@ -1440,6 +1567,8 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
   IE_REQUIRE(epi >= kGemmBf16 && epi <= kGemmSwiglu, "gemm: epilogue %d needs M <= 16", epi);
   IE_REQUIRE(!p.ss_in && !p.ss_out, "gemm: the folded RMSNorm needs M <= 16");
   IE_REQUIRE(p.k_splits <= 1, "gemm: k_splits is the launcher's");
+  IE_REQUIRE(!p.rn_out || (epi == kGemmResid && p.N == kHidden && p.rn_w),
+             "gemm: the fused RMSNorm output follows a residual product of %d columns", kHidden);
   const int rc = launch_split(epi, p, st);
   if (rc != 1) return rc;
   return launch_tiled(epi, p, st, true);
@@ -1455,9 +1584,10 @@ int launch_qkv_rope_prefill(const GemmParams& p, hipStream_t st) {
                  p.start_pos >= 0,
              "qkv_rope_prefill: the [q|k|v] projection of one sequence");
   if (g_gemm_schedule < 1 || gemm_skinny_fits(p) || gemm_skinny_mb_fits(kGemmBf16, p)) return 1;
-  // the bf16 product's own choice (launch_gemm): no K split (up to kSplitMaxRows rows the
-  // launcher may split, and picks smaller tiles), the 192 x 256 tile, whole rounds
-  if (p.M <= kSplitMaxRows) return 1;
+  // up to kSplitMaxRows rows: K split with the RoPE / scatter reduction where the bf16 product
+  // would split
+  if (p.M <= kSplitMaxRows) return launch_split(kGemmQkvRope, p, st);
+  // above: the bf16 product's own choice (launch_gemm): the 192 x 256 tile in whole rounds
   int best = kTileSmall;
   for (int k = kTileWide; k < kTileKinds; ++k)
     if (tile_ok(k, kGemmBf16, p) &&

@@ -143,13 +143,13 @@ def test_prefill_2048_config4(hip, model, oracle_model, noise_floor):
         report_close(orc.bf16_to_f32(gkv[1, 1, :, p]), orc.bf16_to_f32(v1), what=f"layer-1 V row {p}")
 
 
-@pytest.mark.parametrize("S", [2048, 2000])
+@pytest.mark.parametrize("S", [2048, 2000, 512, 100])
 def test_prefill_fused_qkv_rope_equals_scatter(hip, model, S):
-    """The prefill QKV projection with RoPE and the K/V write in its epilogue (ping-pong 192 x 256
-    tiles, ie_tune_gemm_schedule >= 1) against the bf16 product + scatter kernel (schedule 0: the
-    DMA-ring kernels, no fusion): residual rows, every K/V row and the logits bit for bit, on the
-    reference-layout cache (S = 2000: a last row tile of 208 rows) and for a chunk at start
-    position 1000 over shuffled pages."""
+    """The prefill QKV projection with RoPE and the K/V write fused (ie_tune_gemm_schedule >= 1:
+    in the epilogue of the ping-pong 192 x 256 tiles at S = 2048 / 2000, in the K-split
+    reduction at S = 512 / 100) against the bf16 product + scatter kernel (schedule 0): residual
+    rows, every K/V row and the logits bit for bit, on the reference-layout cache (S = 2000: a
+    last row tile of 208 rows) and for a chunk at start position 1000 over shuffled pages."""
     from infengine_amd.engine import Context, Request
     rng = np.random.default_rng(S)
     ids = rng.integers(0, V, S + 1000).astype(np.int32)

@@ -101,6 +101,45 @@ def test_prefill_2048_layers(hip, model, oracle_model):
                                  f"prefill layer {l} row {p}")
 
 
+@pytest.mark.parametrize("S", [100, 512])
+def test_prefill_split_k_equals_chained_layers(hip, model, S):
+    """At prompt lengths whose projections split K, ie_prefill runs the residual reductions
+    together with the RMSNorm that follows (the down projection's with the next layer's input
+    norm) and the QKV reduction with RoPE and the K/V scatter; the per-layer entry point runs the
+    standalone RMSNorm for its input.  Residual rows, K/V cache and logits must agree bit for
+    bit."""
+    from infengine_amd.engine import Context, Request
+    ids = np.random.default_rng(S).integers(0, V, S).astype(np.int32)
+    c = Context(0, graph=False)
+    say(f"ie_prefill S={S}")
+    req = Request(c, model, max_seq_len=S + 8)
+    req.tokens[:S] = torch.from_numpy(ids).cuda()
+    tok = req.prefill(S)
+    want_x = host(req.data[:S].view(torch.int16)).copy()
+    want_logits = host(req.logits).copy()
+    want_kv = req.kv.clone()
+    del req
+    say(f"emblookup + 32 ie_decoder_layer_prefill calls, S={S}")
+    b = Request(c, model, max_seq_len=S + 8)
+    b.tokens[:S] = torch.from_numpy(ids).cuda()
+    hip.check(hip.lib.ie_emblookup(S, _ptr(b.tokens), _ptr(model.view(None, "emb_lookup")),
+                                   _ptr(b.data), c.stream_ptr))
+    for l in range(32):
+        hip.check(hip.lib.ie_decoder_layer_prefill(c.handle, model.ref(), l, S, _ptr(b.data),
+                                                   _ptr(b.aux), _ptr(b.attn), _ptr(b.workspace),
+                                                   _ptr(b.kv)))
+    logits = torch.zeros(V, dtype=torch.float32, device="cuda")
+    hip.check(hip.lib.ie_final_norm_lm_head(c.handle, 1, _ptr(b.data[S - 1]),
+                                            _ptr(model.view(None, "final_norm")),
+                                            _ptr(model.view(None, "lm_head")), _ptr(logits)))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(b.data[:S].view(torch.int16)), want_x)
+    assert np.array_equal(host(logits), want_logits) and tok == int(np.argmax(want_logits))
+    assert torch.equal(b.kv, want_kv)
+    del b, want_kv
+    c.close()
+
+
 # ---------------------------------------------------------------- batched decode, B = 16
 def test_batched16_layers(hip, model, oracle_model):
     """ie_decode_step_batched with 16 sequences at staggered contexts equals ie_emblookup + 32 x
