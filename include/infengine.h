@@ -340,8 +340,10 @@ IE_API int ie_tune_gemv_waves(int waves);
 /* Tuning (no reference counterpart): the kernel of the prefill GEMM's bf16 tiles of
  * 128 or 256 rows: 0 the DMA-ring kernels, 1 the ping-pong kernel for the 256-row
  * tiles only, 2 (default) the ping-pong kernel for both, 3 as 2 with 4 weight ring
- * slots on the 256 x 128 and 192 x 256 tiles.  Results are bit-identical; same scope
- * as above. */
+ * slots on the 256 x 128 and 192 x 256 tiles.  Results are bit-identical above 128
+ * rows.  At 17-128 rows schedules 2 and 3 run the 64-weight-row streaming kernel,
+ * 0 and 1 the older 17-48-row and split-K kernels (other K splits: results agree to
+ * bf16 rounding).  Same scope as above. */
 IE_API int ie_tune_gemm_schedule(int schedule);
 /* Plain GEMM Y[m,n] = X[m,k] . W[n,k]^T on the MFMA path (any m >= 1). */
 IE_API int ie_gemm_bf16(ie_context* ctx, int m, int k, int n, const ie_bf16* d_x,

@@ -1092,6 +1092,187 @@ void gemm_pp_dual_kernel(GemmParams p1, int m_tiles1, int nb1, GemmParams p2, in
 
 }  // namespace pp
 
+// ---------------------------------------------------------------------------
+// Medium-M kernel (17-128 rows: prompts of a few dozen tokens), where a product is bound by its
+// weight stream: 64 W rows x XR X rows (XR = 64 or 128) a workgroup, 4 waves each owning 16 W
+// rows and all XR X rows (XR / 16 MFMA blocks, v_mfma_f32_16x16x32_bf16), over a K range of
+// K / k_splits.  64-k stages (128-byte rows, 8-row direct-to-LDS loads: whole lines) in a ring
+// of S slots (8 at XR = 64, 6 at 128): stage k + S - 1 is issued at k-step k, so S - 1 stages
+// of weight rows (56 KiB at XR = 64) are in flight per CU -- what the HBM latency needs at the
+// per-CU share of the bandwidth.  One barrier per k-step: after it, every wave's loads of stage
+// k have landed and every wave is done with slot (k - 1) % S, which takes stage k + S - 1.
+// Epilogues: fp32 partial planes (split K, reduced by the split reductions), bf16, residual,
+// and SwiGLU over [32 gate | 32 up] W rows (output columns 32 t ..), through an fp32 LDS tile.
+// The X rows are re-read by every W tile from L2 (one K range: XR x K / k_splits x 2 bytes).
+namespace mid {
+
+using pp::f32x4_t;
+
+template <int XR_>
+struct MC {
+  static constexpr int XR = XR_;
+  static constexpr int NB = XR / 16;                 // X blocks per wave
+  static constexpr int W_CHUNKS = 64 * 8, X_CHUNKS = XR * 8;
+  static constexpr int STAGE = W_CHUNKS + X_CHUNKS;  // 16-byte chunks per stage
+  static constexpr int S = XR == 64 ? 4 : 3;         // ring slots
+  static constexpr int WL = 2, XL = XR / 32;         // loads (8 rows each) per wave per stage
+  static constexpr int L = WL + XL;
+  static_assert(XR == 64 || XR == 128, "X rows per tile");
+  static_assert(S * STAGE * 16 <= 160 * 1024, "LDS");
+};
+
+// This wave's loads of stage kt into ring slot `slot`: W groups wv + 4 j, then X groups.
+template <class C>
+__device__ __forceinline__ void mid_issue(u32x4_t* lds, const __amdgpu_buffer_rsrc_t* rs,
+                                          uint32_t vo, int wv, int slot, int kt) {
+  const uint32_t koff = (uint32_t)(kt * 128);
+#pragma unroll
+  for (int j = 0; j < C::L; ++j) {
+    const int g = wv + 4 * (j < C::WL ? j : j - C::WL);
+    const int dst = slot * C::STAGE + (j < C::WL ? 0 : C::W_CHUNKS) + g * 64;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs[j], (lds_void*)&lds[dst], 16, vo, koff, 0, 0);
+  }
+}
+
+// s_waitcnt vmcnt(n * L): n younger stages may stay in flight (n <= 6).
+template <int L>
+__device__ __forceinline__ void mid_wait(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L) : "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * L) : "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * L) : "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * L) : "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * L) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * L) : "memory"); break;
+  }
+}
+
+template <int EPI, int XR>
+__global__ __launch_bounds__(256) void gemm_mid_kernel(GemmParams p, int n_tiles) {
+  using C = MC<XR>;
+  constexpr int NB = C::NB, S = C::S;
+  static_assert(EPI == kGemmF32 || EPI == kGemmBf16 || EPI == kGemmResid || EPI == kGemmSwiglu,
+                "epilogues");
+  __shared__ u32x4_t lds[S * C::STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nsplit = max(1, p.k_splits);
+  const int split = blockIdx.x / n_tiles, ntile = blockIdx.x - split * n_tiles;
+  const int KT = p.K / 64 / nsplit;
+  const int k0 = split * KT * 64;
+
+  // loads: W groups g = wv + 4 j of 8 rows, X groups likewise; row 8 g + r has
+  // swz = (4 (g & 1) + r / 2) & 7 with g & 1 = wv & 1, so one lane offset serves every group
+  __amdgpu_buffer_rsrc_t rs[C::L];
+#pragma unroll
+  for (int j = 0; j < C::WL; ++j) rs[j] = w_group<EPI, 64>(p, ntile, (wv + 4 * j) * 8, k0);
+#pragma unroll
+  for (int j = 0; j < C::XL; ++j) rs[C::WL + j] = x_group(p, 0, (wv + 4 * j) * 8, k0);
+  const int rl = lane >> 3;
+  const uint32_t vo =
+      (uint32_t)((rl * p.K + (((lane & 7) ^ ((4 * (wv & 1) + (rl >> 1)) & 7)) * 8)) * 2);
+
+  // fragments: lane l reads row l % 16 of its block at chunk (l / 16 + 4 ks) ^ ((row >> 1) & 7)
+  const int fr = lane & 15, fq = lane >> 4;
+  const uint32_t sw0 = (uint32_t)((fq ^ ((fr >> 1) & 7)) * 16);
+  const uint32_t aA = (uint32_t)((wv * 16 + fr) * 128) + sw0;
+  const uint32_t aB = (uint32_t)(C::W_CHUNKS * 16 + fr * 128) + sw0;
+
+  f32x4_t acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int t = 0; t < S - 1; ++t)
+    if (t < KT) mid_issue<C>(lds, rs, vo, wv, t, t);
+  const char* base = reinterpret_cast<const char*>(lds);
+  int slot = 0;
+#pragma unroll 1
+  for (int k = 0; k < KT; ++k) {
+    // stage k has landed (stages k+1 .. min(k+S-2, KT-1) may stay in flight) for every wave
+    mid_wait<C::L>(min(S - 2, KT - 1 - k));
+    asm volatile("s_barrier" ::: "memory");
+    if (k + S - 1 < KT) mid_issue<C>(lds, rs, vo, wv, slot == 0 ? S - 1 : slot - 1, k + S - 1);
+    uint32_t ra = (uint32_t)(slot * C::STAGE * 16) + aA, rb = (uint32_t)(slot * C::STAGE * 16) + aB;
+    asm volatile("" : "+v"(ra), "+v"(rb));
+    bf16x8_t fa[2], fb[2][NB];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      fa[ks] = *reinterpret_cast<const bf16x8_t*>(base + (ra ^ (uint32_t)(ks << 6)));
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        fb[ks][j] = *reinterpret_cast<const bf16x8_t*>(base + (rb ^ (uint32_t)(ks << 6)) + j * 2048);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[ks], fb[ks][j], acc[j], 0, 0, 0);
+    slot = slot == S - 1 ? 0 : slot + 1;
+  }
+
+  // epilogue: acc[j][r] = D[W col 16 wv + 4 (lane / 16) + r][X row 16 j + lane % 16], staged as
+  // an fp32 [XR][64] tile (row m at 64 m floats, 16-byte unit u at u ^ (m & 15))
+  float4* ot = reinterpret_cast<float4*>(lds);
+  __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int m = 16 * j + fr, u = 4 * wv + fq;
+    ot[m * 16 + (u ^ (m & 15))] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+  }
+  __syncthreads();
+  if constexpr (EPI == kGemmF32) {
+    float* const yf = p.yf + (size_t)split * p.M * p.ldy;
+    for (int it = tid; it < XR * 16; it += 256) {
+      const int m = it >> 4, u = it & 15, n = ntile * 64 + 4 * u;
+      if (m < p.M && n < p.N)
+        *reinterpret_cast<float4*>(yf + (size_t)m * p.ldy + n) = ot[m * 16 + (u ^ (m & 15))];
+    }
+  } else if constexpr (EPI == kGemmSwiglu) {
+    // tile columns 0..31: gate of output columns 32 ntile + c, 32..63: up of the same
+    for (int it = tid; it < XR * 4; it += 256) {
+      const int m = it >> 2, c8 = it & 3, n = ntile * 32 + 8 * c8;
+      if (m >= p.M || n >= p.N) continue;
+      uint32_t o[4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 g = ot[m * 16 + ((2 * c8 + h) ^ (m & 15))];
+        const float4 up = ot[m * 16 + ((8 + 2 * c8 + h) ^ (m & 15))];
+        const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {up.x, up.y, up.z, up.w};
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float gt = bf2f(f2bf(gv[e])), ut = bf2f(f2bf(uv[e]));
+          v[e] = gt * (1.0f / (1.0f + expf(-gt))) * ut;
+        }
+        o[2 * h] = pack_bf2(v[0], v[1]);
+        o[2 * h + 1] = pack_bf2(v[2], v[3]);
+      }
+      *reinterpret_cast<uint4*>(p.y + (size_t)m * p.ldy + n) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  } else {
+    for (int it = tid; it < XR * 8; it += 256) {
+      const int m = it >> 3, c8 = it & 7, n = ntile * 64 + 8 * c8;
+      if (m >= p.M || n >= p.N) continue;
+      const float4 a = ot[m * 16 + ((2 * c8) ^ (m & 15))], b = ot[m * 16 + ((2 * c8 + 1) ^ (m & 15))];
+      uint4 o = make_uint4(pack_bf2(a.x, a.y), pack_bf2(a.z, a.w), pack_bf2(b.x, b.y), pack_bf2(b.z, b.w));
+      uint16_t* dst = p.y + (size_t)m * p.ldy + n;
+      if constexpr (EPI == kGemmResid) {
+        // y = bf16(y + bf16(acc)) (residual_add.cu:17-19)
+        const uint4 r = *reinterpret_cast<const uint4*>(dst);
+        o = make_uint4(pack_bf2(bf_lo(r.x) + bf_lo(o.x), bf_hi(r.x) + bf_hi(o.x)),
+                       pack_bf2(bf_lo(r.y) + bf_lo(o.y), bf_hi(r.y) + bf_hi(o.y)),
+                       pack_bf2(bf_lo(r.z) + bf_lo(o.z), bf_hi(r.z) + bf_hi(o.z)),
+                       pack_bf2(bf_lo(r.w) + bf_lo(o.w), bf_hi(r.w) + bf_hi(o.w)));
+      }
+      *reinterpret_cast<uint4*>(dst) = o;
+    }
+  }
+}
+
+}  // namespace mid
+
 }  // namespace wide
 
 template <int EPI, int BM = 128, int BK = 64, int STAGES = 3, int MAPG = 1, int WBN = 256, int KG = 1>
@@ -1490,6 +1671,35 @@ __global__ __launch_bounds__(256) void split_reduce_rope_kernel(const float* par
 // k-steps, fits one round of 256 workgroups and whose partials fit p.split_ws (at least 2),
 // fp32 partials into p.split_ws, then the reduction.  Returns
 // IE_OK after launching, 1 when split K does not apply.
+// The reduction of a split product: p.split_ws holds `splits` fp32 planes of M x NP (NP = 2N
+// for SwiGLU: gate then up), y = epilogue(sum) -- RoPE and the K/V scatter, residual + RMSNorm
+// (p.rn_out), residual, SwiGLU or bf16.
+int launch_split_reduce(int epi, const GemmParams& p, int splits, hipStream_t st) {
+  const bool sw = epi == kGemmSwiglu, rope = epi == kGemmQkvRope;
+  const size_t total = (size_t)p.M * p.N / 8;
+  const int blocks = (int)std::min<size_t>((total + 255) / 256, 2048);
+  if (sw) {
+    hipLaunchKernelGGL(split_reduce_kernel<kGemmSwiglu>, dim3(blocks), dim3(256), 0, st,
+                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
+  } else if (rope) {
+    const size_t items = (size_t)p.M * (kQHeads + 2 * kKVHeads) * 16;
+    hipLaunchKernelGGL(split_reduce_rope_kernel, dim3((unsigned)std::min<size_t>((items + 255) / 256, 2048)),
+                       dim3(256), 0, st, p.split_ws, splits, p);
+  } else if (epi == kGemmResid && p.rn_out) {
+    hipLaunchKernelGGL(split_reduce_norm_kernel, dim3(p.M), dim3(256), 0, st, p.split_ws, splits,
+                       p.M, p.y, p.ldy, p.rn_w, p.rn_out);
+    if (p.rn_done) *p.rn_done = 1;
+  } else if (epi == kGemmResid) {
+    hipLaunchKernelGGL(split_reduce_kernel<kGemmResid>, dim3(blocks), dim3(256), 0, st,
+                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
+  } else {
+    hipLaunchKernelGGL(split_reduce_kernel<kGemmBf16>, dim3(blocks), dim3(256), 0, st,
+                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
+  }
+  IE_CHECK_LAUNCH();
+  return IE_OK;
+}
+
 int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   // (below kWideMinRows too: a 128-row tile half empty still beats a few 128 x 128 tiles)
   if (!p.split_ws || epi == kGemmF32 || p.M > kSplitMaxRows || p.N % 8 != 0 || p.ldy % 8 != 0)
@@ -1526,28 +1736,61 @@ int launch_split(int epi, const GemmParams& p, hipStream_t st) {
   }
   const int rc = launch_wide<kGemmF32, 128, 64, 3, 1, 256, 2>(q, st);
   if (rc != IE_OK) return rc;
-  const size_t total = (size_t)p.M * p.N / 8;
-  const int blocks = (int)std::min<size_t>((total + 255) / 256, 2048);
-  if (sw) {
-    hipLaunchKernelGGL(split_reduce_kernel<kGemmSwiglu>, dim3(blocks), dim3(256), 0, st,
-                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
-  } else if (rope) {
-    const size_t items = (size_t)p.M * (kQHeads + 2 * kKVHeads) * 16;
-    hipLaunchKernelGGL(split_reduce_rope_kernel, dim3((unsigned)std::min<size_t>((items + 255) / 256, 2048)),
-                       dim3(256), 0, st, p.split_ws, splits, p);
-  } else if (epi == kGemmResid && p.rn_out) {
-    hipLaunchKernelGGL(split_reduce_norm_kernel, dim3(p.M), dim3(256), 0, st, p.split_ws, splits,
-                       p.M, p.y, p.ldy, p.rn_w, p.rn_out);
-    if (p.rn_done) *p.rn_done = 1;
-  } else if (epi == kGemmResid) {
-    hipLaunchKernelGGL(split_reduce_kernel<kGemmResid>, dim3(blocks), dim3(256), 0, st,
-                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
-  } else {
-    hipLaunchKernelGGL(split_reduce_kernel<kGemmBf16>, dim3(blocks), dim3(256), 0, st,
-                       p.split_ws, splits, p.M, p.N, p.y, p.ldy);
+  return launch_split_reduce(epi, p, splits, st);
+}
+
+// Medium M (16 < M <= 128, K a multiple of 64): the 64-W-row streaming kernel, with its fp32
+// partials reduced by the split reductions, or (gate/up and products of many tiles) unsplit
+// with the epilogue in the kernel.  1: not applicable.
+int launch_mid(int epi, const GemmParams& p, hipStream_t st) {
+  if (g_gemm_schedule < 2 || p.M <= 16 || p.M > 128 || p.K % 64 != 0 || p.K < 64 ||
+      p.N % 8 != 0 || p.ldy % 8 != 0 || epi == kGemmF32)
+    return 1;
+  const bool sw = epi == kGemmSwiglu, rope = epi == kGemmQkvRope;
+  const int kt = p.K / 64;
+  const bool x128 = p.M > 64;
+  // unsplit: SwiGLU over 32-column tiles, bf16 / residual over 64-column tiles, once the tiles
+  // alone fill most of the chip
+  if (!rope && !p.rn_out && (sw ? p.N / 32 : (p.N + 63) / 64) >= 192 && (!sw || p.N % 32 == 0)) {
+    const int n_tiles = sw ? p.N / 32 : (p.N + 63) / 64;
+    GemmParams q = p;
+    q.k_splits = 1;
+#define IE_MID(E, XR, G) \
+  hipLaunchKernelGGL((wide::mid::gemm_mid_kernel<E, XR>), dim3(G), dim3(256), 0, st, q, n_tiles)
+    switch (epi) {
+      case kGemmSwiglu: if (x128) IE_MID(kGemmSwiglu, 128, n_tiles); else IE_MID(kGemmSwiglu, 64, n_tiles); break;
+      case kGemmResid: if (x128) IE_MID(kGemmResid, 128, n_tiles); else IE_MID(kGemmResid, 64, n_tiles); break;
+      default: if (x128) IE_MID(kGemmBf16, 128, n_tiles); else IE_MID(kGemmBf16, 64, n_tiles); break;
+    }
+    IE_CHECK_LAUNCH();
+    return IE_OK;
   }
+  if (!p.split_ws) return 1;
+  // split K over fp32 planes of NP columns (SwiGLU: gate rows then up rows)
+  const int NP = sw ? 2 * p.N : p.N;
+  const int n_tiles = (NP + 63) / 64;
+  const size_t plane = (size_t)p.M * NP * sizeof(float);
+  int splits = 1;
+  for (int sp = 2; sp <= 16; ++sp)
+    if (kt % sp == 0 && (long long)n_tiles * sp <= 256 && (size_t)sp * plane <= (size_t)p.split_ws_bytes)
+      splits = sp;
+  if (splits < 2 && n_tiles < 128) return 1;
+  GemmParams q = p;
+  q.yf = p.split_ws;
+  q.ldy = NP;
+  q.k_splits = splits;
+  if (sw) {
+    q.N = NP;
+    q.n0 = p.N;  // rows [0, N) of w0 (gate), then [N, 2N) of w1 (up)
+    q.n1 = p.N;
+    q.w2 = p.w1;
+  }
+  const unsigned blocks = (unsigned)(n_tiles * splits);
+  if (x128) IE_MID(kGemmF32, 128, blocks);
+  else IE_MID(kGemmF32, 64, blocks);
+#undef IE_MID
   IE_CHECK_LAUNCH();
-  return IE_OK;
+  return launch_split_reduce(epi, p, splits, st);
 }
 
 }  // namespace
@@ -1563,6 +1806,10 @@ int launch_gemm(int epi, const GemmParams& p, hipStream_t st) {
              "gemm: weight split points n0=%d n0+n1=%d inside N=%d must be multiples of 16", p.n0,
              p.n0 + p.n1, p.N);
   if (gemm_skinny_fits(p)) return launch_gemm_skinny(epi, p, st);
+  if (epi >= kGemmBf16 && epi <= kGemmSwiglu && !p.ss_in && !p.ss_out && p.k_splits <= 1) {
+    const int rc = launch_mid(epi, p, st);
+    if (rc != 1) return rc;
+  }
   if (gemm_skinny_mb_fits(epi, p)) return launch_gemm_skinny_mb(epi, p, st);
   IE_REQUIRE(epi >= kGemmBf16 && epi <= kGemmSwiglu, "gemm: epilogue %d needs M <= 16", epi);
   IE_REQUIRE(!p.ss_in && !p.ss_out, "gemm: the folded RMSNorm needs M <= 16");
@@ -1583,7 +1830,12 @@ int launch_qkv_rope_prefill(const GemmParams& p, hipStream_t st) {
                  p.k_cache && p.v_cache && p.rope_cos && p.rope_sin && !p.d_seq_len &&
                  p.start_pos >= 0,
              "qkv_rope_prefill: the [q|k|v] projection of one sequence");
-  if (g_gemm_schedule < 1 || gemm_skinny_fits(p) || gemm_skinny_mb_fits(kGemmBf16, p)) return 1;
+  if (g_gemm_schedule < 1 || gemm_skinny_fits(p)) return 1;
+  {
+    const int rc = launch_mid(kGemmQkvRope, p, st);
+    if (rc != 1) return rc;
+  }
+  if (gemm_skinny_mb_fits(kGemmBf16, p)) return 1;
   // up to kSplitMaxRows rows: K split with the RoPE / scatter reduction where the bf16 product
   // would split
   if (p.M <= kSplitMaxRows) return launch_split(kGemmQkvRope, p, st);

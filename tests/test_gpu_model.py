@@ -135,9 +135,9 @@ def test_decode_steps_vs_oracle(hip, model, oracle_model, prior, noise_floor):
     assert_bf16_close(gkv[0, :, :, POS:POS + 2], kv[0, :, :, POS:POS + 2], what="layer-0 kv", outlier_frac=1e-3)
 
 
-# 16: the M <= 16 skinny projections; 24 / 40: the 2- and 3-row-block streaming projections;
-# 100 / 256: split-K projections (fp32 partials in the workspace, O aliased over q/k/v), the
-# SwiGLU split and 16-row flash-attention workgroups
+# 16: the M <= 16 skinny projections; 24 / 40 / 100: the 64-weight-row streaming projections
+# (64 and 128 X rows; K split into fp32 planes in the workspace, O aliased over q/k/v, SwiGLU in
+# the kernel); 256: split-K MFMA tiles, the SwiGLU split and 16-row flash-attention workgroups
 @pytest.mark.parametrize("S", [16, 24, 40, 100, 256])
 def test_prefill_then_decode_vs_oracle(hip, model, oracle_model, noise_floor, S):
     from infengine_amd.engine import Context, Request
@@ -235,9 +235,9 @@ def test_batched_decode_matches_single(hip, model, noise_floor, lens):
     c.close()
 
 
-# 40: the 17-48-row streaming projections; 100 / 600: split-K projections and 16-row attention
-# workgroups; 1024: the last split-K size; 1100: unsplit projections, 16-row workgroups; 1800:
-# the 32-row attention workgroups
+# 40 / 100: the 64-weight-row streaming projections (64 and 128 X rows); 600: split-K MFMA tiles
+# and 16-row attention workgroups; 1024: the last split-K size; 1100: unsplit projections, 16-row
+# workgroups; 1800: the 32-row attention workgroups
 @pytest.mark.parametrize("S", [40, 100, 600, 1024, 1100, 1800])
 def test_prefill_paged_equals_contiguous(hip, model, S):
     """ie_prefill_paged (K/V rows into pages scattered over a pool) against ie_prefill (reference-

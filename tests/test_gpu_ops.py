@@ -302,11 +302,11 @@ GEMM_EPI = {"bf16": 0, "resid": 1, "f32": 2, "swiglu": 3}
                                  (2048, 4096), (2048, 14336)])
 def test_gemm_epilogues(hip, ctx, epi, m, n):
     """Every fused epilogue of the MFMA GEMM on each kernel the launcher picks: the skinny
-    streaming kernel (m <= 16, ragged n), its 2- and 3-row-block forms (m = 17, 24, 32 and m = 33,
-    40, 48: bf16 / resid / SwiGLU), 128 x 128 tiles (m = 100, 300: f32 / SwiGLU; f32 at
-    m = 17..64), K split across workgroups with a reduction at m = 64 (n = 4096, and 14336 where
-    SwiGLU splits its 2 x 14336-column product), K split
-    across workgroups with a reduction (bf16 / resid at m = 100, 300, 512), and the prefill sizes:
+    streaming kernel (m <= 16, ragged n), the 64-weight-row streaming kernel at m = 17-100
+    (bf16 / resid / SwiGLU; 64 X rows up to m = 64, 128 at m = 100; K split with a reduction, or
+    SwiGLU in the kernel at n = 14336), 128 x 128 tiles (m = 300: f32 / SwiGLU; f32 at
+    m = 17..100), K split across workgroups with a reduction (bf16 / resid at m = 300, 512), and
+    the prefill sizes:
     192 x 256 tiles (bf16 / resid at n = 6144), 256 x 256 tiles (SwiGLU at n = 4096), 256 x 128
     tiles (the others at n = 4096 and 6144), and at n = 14336 a launch split by output columns
     (full rounds of the big tile, then the remaining columns with another shape: SwiGLU 256 x 256
@@ -418,10 +418,9 @@ def test_gemm_skinny_wide_tiles(hip, ctx, epi, m, k, n):
 @pytest.mark.parametrize("epi", ["bf16", "resid"])
 @pytest.mark.parametrize("m", [17, 24, 40, 64, 2048])
 def test_gemm_down_projection_shapes(hip, ctx, epi, m):
-    """The down projection (k 14336, n 4096) as prefill runs it: the 2- and 3-row-block streaming
-    kernel at 17, 24 and 40 rows (K = 14336 instantiations), K split across workgroups at 64 rows
-    and the 2048-row MFMA tiles of config 4; every row up to 64, sampled rows at 2048, against the
-    oracle."""
+    """The down projection (k 14336, n 4096) as prefill runs it: the 64-weight-row streaming
+    kernel at 17-64 rows (K split 4 ways, then the residual reduction) and the 2048-row MFMA tiles
+    of config 4; every row up to 64, sampled rows at 2048, against the oracle."""
     k, n = 14336, 4096
     say(f"gemm_ex down {epi} m={m} k={k} n={n}")
     x = orc.synthetic((m, k), 25, m, 0.0, 1.0)
@@ -440,6 +439,45 @@ def test_gemm_down_projection_shapes(hip, ctx, epi, m):
         want = orc.residual_add(np.ascontiguousarray(y0[rows]), want)
     assert_close(orc.bf16_to_f32(got), orc.bf16_to_f32(want), what=f"gemm down {epi} m={m}")
     assert_bf16_close(got, want, ulps=2, what=f"gemm down {epi} m={m}",
+                      outlier_frac=1e-3 if epi == "resid" else 0.0)
+
+
+@pytest.mark.parametrize("epi,m,k,n", [("bf16", 17, 4096, 6144), ("resid", 33, 4096, 4096),
+                                       ("swiglu", 64, 4096, 14336), ("resid", 65, 14336, 4096),
+                                       ("bf16", 100, 4096, 1000), ("swiglu", 128, 256, 520),
+                                       ("bf16", 128, 192, 16384), ("resid", 48, 4096, 4104),
+                                       ("swiglu", 96, 4096, 4104)])
+def test_gemm_medium_rows(hip, ctx, epi, m, k, n):
+    """17-128 rows (prompts of a few dozen tokens): the 64-weight-row streaming kernel with 64 X
+    rows (m <= 64) or 128.  K split into fp32 planes then reduced: 2 ways (bf16 n = 6144, resid
+    n = 4104), 4 (resid n = 4096 at k 4096 and 14336, SwiGLU n = 520 over its 1040-column gate|up
+    planes), 16 (bf16 n = 1000), and one plane (SwiGLU n = 4104: 129 tiles, no split divides);
+    unsplit with the epilogue in the kernel where the tiles alone fill the chip (SwiGLU n = 14336,
+    bf16 n = 16384 at k = 192, three stages).  Ragged n, every row against the oracle, and the
+    same bits on a second call."""
+    say(f"gemm_ex medium rows {epi} m={m} k={k} n={n}")
+    x = orc.synthetic((m, k), 27, m, 0.0, 1.0)
+    w0 = orc.synthetic((n, k), 27, n + 1, 0.0, 0.02)
+    w1 = orc.synthetic((n, k), 27, n + 2, 0.0, 0.02)
+    y0 = orc.synthetic((m, n), 27, n + 3, 0.0, 1.0)
+    dx, dw0, dw1 = dev(x), dev(w0), dev(w1)
+    outs = []
+    for _ in range(2):
+        out = dev(y0) if epi == "resid" else bf16_empty(m, n)
+        hip.check(hip.lib.ie_gemm_ex(ctx.handle, GEMM_EPI[epi], m, k, n, P(dx), P(dw0), P(dw1),
+                                     P(out)))
+        sync()
+        outs.append(host(out))
+    assert np.array_equal(outs[0], outs[1])
+    got = outs[0]
+    if epi == "bf16":
+        want = orc.matmul(x, w0)
+    elif epi == "resid":
+        want = orc.residual_add(y0, orc.matmul(x, w0))
+    else:
+        want = orc.swiglu(orc.matmul(x, w0), orc.matmul(x, w1))
+    assert_close(orc.bf16_to_f32(got), orc.bf16_to_f32(want), what=f"gemm medium {epi}")
+    assert_bf16_close(got, want, ulps=4 if epi == "swiglu" else 2, what=f"gemm medium {epi}",
                       outlier_frac=1e-3 if epi == "resid" else 0.0)
 
 
