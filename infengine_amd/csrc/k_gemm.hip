@@ -1108,27 +1108,30 @@ namespace mid {
 
 using pp::f32x4_t;
 
-template <int XR_>
+template <int XR_, int WR_>
 struct MC {
-  static constexpr int XR = XR_;
+  static constexpr int XR = XR_, WR = WR_;
+  static constexpr int NWV = WR / 16;                // waves, 16 W rows each
   static constexpr int NB = XR / 16;                 // X blocks per wave
-  static constexpr int W_CHUNKS = 64 * 8, X_CHUNKS = XR * 8;
+  static constexpr int W_CHUNKS = WR * 8, X_CHUNKS = XR * 8;
   static constexpr int STAGE = W_CHUNKS + X_CHUNKS;  // 16-byte chunks per stage
   static constexpr int S = XR == 64 ? 4 : 3;         // ring slots
-  static constexpr int WL = 2, XL = XR / 32;         // loads (8 rows each) per wave per stage
+  static constexpr int WL = WR / 8 / NWV, XL = XR / 8 / NWV;  // 8-row loads per wave per stage
   static constexpr int L = WL + XL;
+  static constexpr int U = WR / 4;                   // 16-byte units of an fp32 output row
   static_assert(XR == 64 || XR == 128, "X rows per tile");
+  static_assert(WR == 64 || WR == 128, "W rows per tile");
   static_assert(S * STAGE * 16 <= 160 * 1024, "LDS");
 };
 
-// This wave's loads of stage kt into ring slot `slot`: W groups wv + 4 j, then X groups.
+// This wave's loads of stage kt into ring slot `slot`: W groups wv + NWV j, then X groups.
 template <class C>
 __device__ __forceinline__ void mid_issue(u32x4_t* lds, const __amdgpu_buffer_rsrc_t* rs,
                                           uint32_t vo, int wv, int slot, int kt) {
   const uint32_t koff = (uint32_t)(kt * 128);
 #pragma unroll
   for (int j = 0; j < C::L; ++j) {
-    const int g = wv + 4 * (j < C::WL ? j : j - C::WL);
+    const int g = wv + C::NWV * (j < C::WL ? j : j - C::WL);
     const int dst = slot * C::STAGE + (j < C::WL ? 0 : C::W_CHUNKS) + g * 64;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs[j], (lds_void*)&lds[dst], 16, vo, koff, 0, 0);
   }
@@ -1148,9 +1151,10 @@ __device__ __forceinline__ void mid_wait(int n) {
   }
 }
 
-template <int EPI, int XR>
-__global__ __launch_bounds__(256) void gemm_mid_kernel(GemmParams p, int n_tiles) {
-  using C = MC<XR>;
+template <int EPI, int XR, int WR>
+__global__ __launch_bounds__(WR * 4) void gemm_mid_kernel(GemmParams p, int n_tiles) {
+  using C = MC<XR, WR>;
+  constexpr int U = C::U;
   constexpr int NB = C::NB, S = C::S;
   static_assert(EPI == kGemmF32 || EPI == kGemmBf16 || EPI == kGemmResid || EPI == kGemmSwiglu,
                 "epilogues");
@@ -1162,13 +1166,13 @@ __global__ __launch_bounds__(256) void gemm_mid_kernel(GemmParams p, int n_tiles
   const int KT = p.K / 64 / nsplit;
   const int k0 = split * KT * 64;
 
-  // loads: W groups g = wv + 4 j of 8 rows, X groups likewise; row 8 g + r has
+  // loads: W groups g = wv + NWV j of 8 rows, X groups likewise; row 8 g + r has
   // swz = (4 (g & 1) + r / 2) & 7 with g & 1 = wv & 1, so one lane offset serves every group
   __amdgpu_buffer_rsrc_t rs[C::L];
 #pragma unroll
-  for (int j = 0; j < C::WL; ++j) rs[j] = w_group<EPI, 64>(p, ntile, (wv + 4 * j) * 8, k0);
+  for (int j = 0; j < C::WL; ++j) rs[j] = w_group<EPI, WR>(p, ntile, (wv + C::NWV * j) * 8, k0);
 #pragma unroll
-  for (int j = 0; j < C::XL; ++j) rs[C::WL + j] = x_group(p, 0, (wv + 4 * j) * 8, k0);
+  for (int j = 0; j < C::XL; ++j) rs[C::WL + j] = x_group(p, 0, (wv + C::NWV * j) * 8, k0);
   const int rl = lane >> 3;
   const uint32_t vo =
       (uint32_t)((rl * p.K + (((lane & 7) ^ ((4 * (wv & 1) + (rl >> 1)) & 7)) * 8)) * 2);
@@ -1213,32 +1217,34 @@ __global__ __launch_bounds__(256) void gemm_mid_kernel(GemmParams p, int n_tiles
   }
 
   // epilogue: acc[j][r] = D[W col 16 wv + 4 (lane / 16) + r][X row 16 j + lane % 16], staged as
-  // an fp32 [XR][64] tile (row m at 64 m floats, 16-byte unit u at u ^ (m & 15))
+  // an fp32 [XR][WR] tile (row m at WR m floats, 16-byte unit u at u ^ (m % U))
   float4* ot = reinterpret_cast<float4*>(lds);
+  constexpr int T = 64 * C::NWV;
+  const auto at = [&](int m, int u) -> float4& { return ot[m * U + (u ^ (m & (U - 1)))]; };
   __syncthreads();  // every wave is done with the ring (its last wait was vmcnt(0))
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    const int m = 16 * j + fr, u = 4 * wv + fq;
-    ot[m * 16 + (u ^ (m & 15))] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
-  }
+  for (int j = 0; j < NB; ++j)
+    at(16 * j + fr, 4 * wv + fq) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
   __syncthreads();
   if constexpr (EPI == kGemmF32) {
     float* const yf = p.yf + (size_t)split * p.M * p.ldy;
-    for (int it = tid; it < XR * 16; it += 256) {
-      const int m = it >> 4, u = it & 15, n = ntile * 64 + 4 * u;
-      if (m < p.M && n < p.N)
-        *reinterpret_cast<float4*>(yf + (size_t)m * p.ldy + n) = ot[m * 16 + (u ^ (m & 15))];
+    for (int it = tid; it < XR * U; it += T) {
+      const int m = it / U, u = it % U, n = ntile * WR + 4 * u;
+      if (m < p.M && n < p.N) *reinterpret_cast<float4*>(yf + (size_t)m * p.ldy + n) = at(m, u);
     }
   } else if constexpr (EPI == kGemmSwiglu) {
-    // tile columns 0..31: gate of output columns 32 ntile + c, 32..63: up of the same
-    for (int it = tid; it < XR * 4; it += 256) {
-      const int m = it >> 2, c8 = it & 3, n = ntile * 32 + 8 * c8;
+    // W rows [32 gate | 32 up] x (WR / 64): tile columns 64 b .. 64 b + 31 are the gate of output
+    // columns ntile WR / 2 + 32 b + c, 64 b + 32 .. the up of the same
+    constexpr int CPR = WR / 16;  // 8-column output groups per row
+    for (int it = tid; it < XR * CPR; it += T) {
+      const int m = it / CPR, c = it % CPR, b = c >> 2, c8 = c & 3;
+      const int n = ntile * (WR / 2) + 32 * b + 8 * c8;
       if (m >= p.M || n >= p.N) continue;
       uint32_t o[4];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const float4 g = ot[m * 16 + ((2 * c8 + h) ^ (m & 15))];
-        const float4 up = ot[m * 16 + ((8 + 2 * c8 + h) ^ (m & 15))];
+        const float4 g = at(m, 16 * b + 2 * c8 + h);
+        const float4 up = at(m, 16 * b + 8 + 2 * c8 + h);
         const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {up.x, up.y, up.z, up.w};
         float v[4];
 #pragma unroll
@@ -1252,10 +1258,11 @@ __global__ __launch_bounds__(256) void gemm_mid_kernel(GemmParams p, int n_tiles
       *reinterpret_cast<uint4*>(p.y + (size_t)m * p.ldy + n) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   } else {
-    for (int it = tid; it < XR * 8; it += 256) {
-      const int m = it >> 3, c8 = it & 7, n = ntile * 64 + 8 * c8;
+    constexpr int CPR = WR / 8;  // 8-column groups per row
+    for (int it = tid; it < XR * CPR; it += T) {
+      const int m = it / CPR, c8 = it % CPR, n = ntile * WR + 8 * c8;
       if (m >= p.M || n >= p.N) continue;
-      const float4 a = ot[m * 16 + ((2 * c8) ^ (m & 15))], b = ot[m * 16 + ((2 * c8 + 1) ^ (m & 15))];
+      const float4 a = at(m, 2 * c8), b = at(m, 2 * c8 + 1);
       uint4 o = make_uint4(pack_bf2(a.x, a.y), pack_bf2(a.z, a.w), pack_bf2(b.x, b.y), pack_bf2(b.z, b.w));
       uint16_t* dst = p.y + (size_t)m * p.ldy + n;
       if constexpr (EPI == kGemmResid) {
@@ -1749,6 +1756,19 @@ int launch_mid(int epi, const GemmParams& p, hipStream_t st) {
   const bool sw = epi == kGemmSwiglu, rope = epi == kGemmQkvRope;
   const int kt = p.K / 64;
   const bool x128 = p.M > 64;
+  // 65-128 rows: SwiGLU over 64-column tiles (128 W rows, 8 waves: each tile re-reads the X
+  // rows from L2 for twice the weight rows), when they alone fill most of the chip (in situ at
+  // 100 and 128 rows 2.6% and 3.7% faster per prefill than 32-column tiles; at 64 rows and
+  // fewer, level or slower)
+  if (sw && x128 && p.N % 64 == 0 && p.N / 64 >= 192) {
+    const int n_tiles = p.N / 64;
+    GemmParams q = p;
+    q.k_splits = 1;
+    hipLaunchKernelGGL((wide::mid::gemm_mid_kernel<kGemmSwiglu, 128, 128>), dim3(n_tiles), dim3(512), 0,
+                       st, q, n_tiles);
+    IE_CHECK_LAUNCH();
+    return IE_OK;
+  }
   // unsplit: SwiGLU over 32-column tiles, bf16 / residual over 64-column tiles, once the tiles
   // alone fill most of the chip
   if (!rope && !p.rn_out && (sw ? p.N / 32 : (p.N + 63) / 64) >= 192 && (!sw || p.N % 32 == 0)) {
@@ -1756,7 +1776,7 @@ int launch_mid(int epi, const GemmParams& p, hipStream_t st) {
     GemmParams q = p;
     q.k_splits = 1;
 #define IE_MID(E, XR, G) \
-  hipLaunchKernelGGL((wide::mid::gemm_mid_kernel<E, XR>), dim3(G), dim3(256), 0, st, q, n_tiles)
+  hipLaunchKernelGGL((wide::mid::gemm_mid_kernel<E, XR, 64>), dim3(G), dim3(256), 0, st, q, n_tiles)
     switch (epi) {
       case kGemmSwiglu: if (x128) IE_MID(kGemmSwiglu, 128, n_tiles); else IE_MID(kGemmSwiglu, 64, n_tiles); break;
       case kGemmResid: if (x128) IE_MID(kGemmResid, 128, n_tiles); else IE_MID(kGemmResid, 64, n_tiles); break;

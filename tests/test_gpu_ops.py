@@ -446,15 +446,17 @@ def test_gemm_down_projection_shapes(hip, ctx, epi, m):
                                        ("swiglu", 64, 4096, 14336), ("resid", 65, 14336, 4096),
                                        ("bf16", 100, 4096, 1000), ("swiglu", 128, 256, 520),
                                        ("bf16", 128, 192, 16384), ("resid", 48, 4096, 4104),
-                                       ("swiglu", 96, 4096, 4104)])
+                                       ("swiglu", 96, 4096, 4104), ("swiglu", 100, 4096, 14336),
+                                       ("swiglu", 128, 256, 12288)])
 def test_gemm_medium_rows(hip, ctx, epi, m, k, n):
     """17-128 rows (prompts of a few dozen tokens): the 64-weight-row streaming kernel with 64 X
     rows (m <= 64) or 128.  K split into fp32 planes then reduced: 2 ways (bf16 n = 6144, resid
     n = 4104), 4 (resid n = 4096 at k 4096 and 14336, SwiGLU n = 520 over its 1040-column gate|up
     planes), 16 (bf16 n = 1000), and one plane (SwiGLU n = 4104: 129 tiles, no split divides);
-    unsplit with the epilogue in the kernel where the tiles alone fill the chip (SwiGLU n = 14336,
-    bf16 n = 16384 at k = 192, three stages).  Ragged n, every row against the oracle, and the
-    same bits on a second call."""
+    unsplit with the epilogue in the kernel where the tiles alone fill the chip (SwiGLU n = 14336
+    over 32-column tiles at m = 64; over 64-column tiles of 128 weight rows and 8 waves at m = 100
+    and 128, n = 14336 and 12288; bf16 n = 16384 at k = 192, three stages).  Ragged n, every row
+    against the oracle, and the same bits on a second call."""
     say(f"gemm_ex medium rows {epi} m={m} k={k} n={n}")
     x = orc.synthetic((m, k), 27, m, 0.0, 1.0)
     w0 = orc.synthetic((n, k), 27, n + 1, 0.0, 0.02)
