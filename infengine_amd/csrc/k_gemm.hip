@@ -1208,6 +1208,9 @@ __global__ __launch_bounds__(WR * 4) void gemm_mid_kernel(GemmParams p, int n_ti
       for (int j = 0; j < NB; ++j)
         fb[ks][j] = *reinterpret_cast<const bf16x8_t*>(base + (rb ^ (uint32_t)(ks << 6)) + j * 2048);
     }
+    // all of the step's reads issued before its first MFMA (left alone, the scheduler puts each
+    // read just before its use: one LDS round trip per MFMA)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
