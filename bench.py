@@ -46,6 +46,14 @@ GATE_UP_BYTES = 2 * FFN * HIDDEN * 2 + 2 * HIDDEN * 2 + FFN * 2
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0                   # dense bf16 MFMA, MI355X
 LAYER_GEMM_PARAMS = (6144 + 4096 + 2 * FFN) * HIDDEN + HIDDEN * FFN   # QKV, O, gate+up, down
+
+
+def prefill_gemm_flops(P: int) -> float:
+    """Flops of the layer products an ie_prefill of P tokens runs: 31 layers over P rows, then
+    the last layer's QKV over P rows (its K/V cache rows) and its O, gate/up and down products
+    over the last row only (the one row the final norm and lm_head read)."""
+    qkv = 6144 * HIDDEN
+    return 2.0 * (P * LAYER_GEMM_PARAMS * (LAYERS - 1) + P * qkv + (LAYER_GEMM_PARAMS - qkv))
 # HBM bytes per gate/up launch from rocprofv3 FETCH_SIZE (x2.000) + WRITE_SIZE (x1.000), each
 # factor calibrated on a 256 MiB copy; profiles/decode_gemv_hbm_traffic.md.
 GATE_UP_TRAFFIC = 235_190_000
@@ -421,7 +429,7 @@ def main() -> int:
             tok = req.prefill(P)
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) / 3 * 1e3
-        flops = 2.0 * P * LAYER_GEMM_PARAMS * LAYERS
+        flops = prefill_gemm_flops(P)
         print(json.dumps({"prefill": {"seq_len": P, "ms": round(ms, 3), "token": tok,
                                       "layer_gemm_tflops_per_s": round(flops / ms / 1e9, 1)}}),
               flush=True)
@@ -544,7 +552,7 @@ def main() -> int:
         del req2
         gemms = prefill_gemms(ctx, P)
         attention = prefill_attention(ctx, P)
-        flops = 2.0 * P * LAYER_GEMM_PARAMS * LAYERS
+        flops = prefill_gemm_flops(P)
         prefill2048 = {"seq_len": P, "ms": round(pdt * 1e3, 2), "tokens_per_s": round(P / pdt, 1),
                        "layer_gemm_tflops_per_s": round(flops / pdt / 1e12, 1),
                        "gemm": gemms, "attention": attention,

@@ -311,12 +311,22 @@ IE_API int ie_decoder_layer_decode(ie_context* ctx, const ie_model_weights* weig
  * seq_len rows (positions 0 .. seq_len-1) of data_buffer [seq_len][4096], in place, writing
  * that layer's K/V rows 0 .. seq_len-1 of kv_cache; aux/attn buffers and workspace
  * (max(ie_attn_workspace_size, ie_ffn_workspace_size)(seq_len) bytes) as ie_prefill.
- * ie_prefill is the embedding, these 32 calls, then final norm + lm_head on the last row and
- * argmax, bit for bit. */
+ * ie_prefill is the embedding, 31 of these calls, ie_decoder_layer_prefill_last_row for layer
+ * 31, then final norm + lm_head on the last row and argmax, bit for bit. */
 IE_API int ie_decoder_layer_prefill(ie_context* ctx, const ie_model_weights* weights,
                                     int layer_idx, int seq_len, ie_bf16* data_buffer,
                                     ie_bf16* aux_buffer, ie_bf16* attn_buffer, void* workspace,
                                     void* kv_cache);
+/* Decoder layer layer_idx of a prefill whose output is needed for the last row only (no
+ * reference counterpart: prefill.cu:17-38 runs every layer over all rows, but only the last
+ * row reaches the final norm and lm_head, prefill.cu:41-43): K/V rows 0 .. seq_len-1 as
+ * ie_decoder_layer_prefill writes them, the last row of data_buffer as a decode step at
+ * position seq_len-1 computes it (attention over the cache, O projection + residual, FFN);
+ * rows 0 .. seq_len-2 keep the layer's input.  ie_prefill runs it for its last layer. */
+IE_API int ie_decoder_layer_prefill_last_row(ie_context* ctx, const ie_model_weights* weights,
+                                             int layer_idx, int seq_len, ie_bf16* data_buffer,
+                                             ie_bf16* aux_buffer, ie_bf16* attn_buffer,
+                                             void* workspace, void* kv_cache);
 /* One decoder layer of ie_decode_step_batched (no reference counterpart: the reference decodes
  * one sequence) over batch rows [batch][4096] of data_buffer, in place; row b is sequence b at
  * position seq_lens[b]-1 of cache b (kv_caches as ie_decode_step_batched), workspace

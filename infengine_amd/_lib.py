@@ -110,6 +110,7 @@ SIGNATURES: dict[str, tuple] = {
     "ie_ffn_gate_up_decode": (_i, [_p, _p, _p, _p, _p, _p]),
     "ie_decoder_layer_decode": (_i, [_p, _W, _i, _i, _p, _p, _p, _p]),
     "ie_decoder_layer_prefill": (_i, [_p, _W, _i, _i, _p, _p, _p, _p, _p]),
+    "ie_decoder_layer_prefill_last_row": (_i, [_p, _W, _i, _i, _p, _p, _p, _p, _p]),
     "ie_decoder_layer_batched": (_i, [_p, _W, _i, _i, C.POINTER(_i), _p, _p, _p, _p]),
     "ie_final_norm_lm_head": (_i, [_p, _i, _p, _p, _p, _p]),
     "ie_gemm_bf16": (_i, [_p, _i, _i, _i, _p, _p, _p]),

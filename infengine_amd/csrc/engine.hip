@@ -163,15 +163,16 @@ bool attn_fused(int seq_len) { return seq_len <= kAttnFusedMaxCtx; }
 
 // seq_len: the context length; with d_seq_len set the kernels read it from there and seq_len
 // only bounds it on the host (it picks the attention path).
-int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, int layer,
-                         uint16_t* x, uint16_t* attn_out, const DecodeWs& w, void* kv,
-                         const int* d_seq_len, int seq_len) {
-  (void)c;
-  const ie_layer& L = W.layers[layer];
-  uint16_t* kvl = kv_layer(kv, layer);
-  IE_TRY(qkv_rope_gemv(L, W.rope, x, L.input_layernorm, w.q, kvl, d_seq_len, seq_len - 1, st));
+// The decode layer from its attention on (decode.cu:22-39): the row whose rotated q is at q
+// attends over positions 0 .. seq_len-1 of the layer's cache kvl (paged: the layer's base in
+// page 0, block_table the sequence's pages), then the O projection + residual into x and the
+// FFN block.  w.q is not read (q is).
+int decode_layer_tail(hipStream_t st, const ie_layer& L, const uint16_t* q, uint16_t* x,
+                      uint16_t* attn_out, const DecodeWs& w, uint16_t* kvl, const int* d_seq_len,
+                      int seq_len, const int* block_table = nullptr, int n_pages = 0) {
   const bool fused = attn_fused(seq_len);
-  IE_TRY(attn_decode(w.q, kvl, attn_out, w, d_seq_len, seq_len, seq_len, 1, 0, !fused, st));
+  IE_TRY(attn_decode(q, kvl, attn_out, w, d_seq_len, seq_len, seq_len, 1, 0, !fused, st,
+                     block_table, 0, n_pages));
   if (fused) {
     // O projection + residual, its input merged from the split partials in its prologue
     GemvParams p{};
@@ -194,6 +195,16 @@ int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, 
   IE_TRY(gemv_plain(kFFN, kEpiResid, w.h, nullptr, L.ffn_block.w_down, nullptr, kHidden / 2, x,
                     nullptr, 1, 0, st));
   return IE_OK;
+}
+
+int decoder_layer_decode(Context* c, hipStream_t st, const ie_model_weights& W, int layer,
+                         uint16_t* x, uint16_t* attn_out, const DecodeWs& w, void* kv,
+                         const int* d_seq_len, int seq_len) {
+  (void)c;
+  const ie_layer& L = W.layers[layer];
+  uint16_t* kvl = kv_layer(kv, layer);
+  IE_TRY(qkv_rope_gemv(L, W.rope, x, L.input_layernorm, w.q, kvl, d_seq_len, seq_len - 1, st));
+  return decode_layer_tail(st, L, w.q, x, attn_out, w, kvl, d_seq_len, seq_len);
 }
 
 // wb_buf: when set, the argmax also stores the token at wb_buf[seq_len] (the Manager loop's
@@ -572,10 +583,16 @@ void skinny_split(Context* c, int epi, GemmParams& g, float* part) {
 // the previous layer's down-projection reduction).  next_norm_w: the next layer's input norm
 // weight, or nullptr; *aux_next is set when this layer left that norm in aux_buffer (the down
 // projection ran with K split and its reduction applied the norm).
+// last_row: the layer's K/V rows for all S positions, its output for the last row only (the
+// rows before it keep the layer's input).  The final norm and lm_head of prefill.cu:41-43 read
+// the last row alone and the later positions' attention reads only the K/V cache, so the last
+// layer's attention, O projection and FFN over the other rows feed nothing: the last row runs
+// them as a decode step does.
 int prefill_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, int start_pos,
                   int S, ie_bf16* data_buffer, ie_bf16* aux_buffer, ie_bf16* attn_buffer,
                   void* workspace, void* kv_cache, const int* block_table, int n_pages,
-                  bool aux_ready, const uint16_t* next_norm_w, bool* aux_next) {
+                  bool aux_ready, const uint16_t* next_norm_w, bool* aux_next,
+                  bool last_row = false) {
   if (aux_next) *aux_next = false;
   char* wsb = static_cast<char*>(workspace);
   uint16_t* qkv = reinterpret_cast<uint16_t*>(wsb);
@@ -620,6 +637,16 @@ int prefill_layer(Context* c, hipStream_t st, const ie_model_weights& W, int l, 
     IE_TRY(launch_gemm(kGemmBf16, g, st));
     IE_TRY(launch_qkv_rope_scatter(S, start_pos, qkv, W.rope.cos, W.rope.sin, qrot, kvl, vpl,
                                    nullptr, 0, st, block_table, n_pages));
+  }
+  if (last_row) {
+    // the decode workspace after q/k/v and the rotated q (the split-K partials' room)
+    const size_t room = std::max(ie_attn_workspace_size(S), ie_ffn_workspace_size(S)) -
+                        prefill_attn_bytes(S);
+    IE_REQUIRE(decode_ws_bytes(1) <= room, "prefill: workspace too small for the last row");
+    const DecodeWs dw = decode_ws(wsb + prefill_attn_bytes(S), 1);
+    return decode_layer_tail(st, L, qrot + (size_t)(S - 1) * kHidden,
+                             data_buffer + (size_t)(S - 1) * kHidden, dw.attn1, dw, kvl, nullptr,
+                             start_pos + S, block_table, n_pages);
   }
   AttnPrefillParams a{qrot, kvl, vpl, attn_buffer, S, start_pos, block_table, n_pages};
   IE_TRY(launch_attn_prefill(a, st));
@@ -709,7 +736,8 @@ int prefill_impl(ie_context* c, const ie_model_weights* weights, int start_pos, 
   for (int l = 0; l < kLayers; ++l)
     IE_TRY(prefill_layer(c, st, W, l, start_pos, S, data_buffer, aux_buffer, attn_buffer,
                          workspace, kv_cache, block_table, n_pages, aux_ready,
-                         l + 1 < kLayers ? W.layers[l + 1].input_layernorm : nullptr, &aux_ready));
+                         l + 1 < kLayers ? W.layers[l + 1].input_layernorm : nullptr, &aux_ready,
+                         l == kLayers - 1));
   // prefill.cu:41-43: final norm, lm_head on the last row only, argmax
   IE_TRY(gemv_plain(kHidden, kEpiF32, data_buffer + (size_t)(S - 1) * kHidden, W.final_norm,
                     W.lm_head, nullptr, kVocab / 2, nullptr, output_distr, 1, kVocab, st));
@@ -764,6 +792,24 @@ int ie_decoder_layer_prefill(ie_context* c, const ie_model_weights* weights, int
              "decoder_layer_prefill: null buffer");
   return prefill_layer(c, c->stream, *weights, layer_idx, 0, seq_len, data_buffer, aux_buffer,
                        attn_buffer, workspace, kv_cache, nullptr, 0, false, nullptr, nullptr);
+}
+
+int ie_decoder_layer_prefill_last_row(ie_context* c, const ie_model_weights* weights,
+                                      int layer_idx, int seq_len, ie_bf16* data_buffer,
+                                      ie_bf16* aux_buffer, ie_bf16* attn_buffer, void* workspace,
+                                      void* kv_cache) {
+  CTX_OK(c);
+  IE_REQUIRE(weights && weights_complete(*weights),
+             "decoder_layer_prefill_last_row: incomplete weights");
+  IE_REQUIRE(layer_idx >= 0 && layer_idx < kLayers, "decoder_layer_prefill_last_row: layer %d",
+             layer_idx);
+  IE_REQUIRE(seq_len >= 1 && seq_len <= kMaxCtx,
+             "decoder_layer_prefill_last_row: seq_len %d out of [1, %d]", seq_len, kMaxCtx);
+  IE_REQUIRE(data_buffer && aux_buffer && attn_buffer && workspace && kv_cache,
+             "decoder_layer_prefill_last_row: null buffer");
+  return prefill_layer(c, c->stream, *weights, layer_idx, 0, seq_len, data_buffer, aux_buffer,
+                       attn_buffer, workspace, kv_cache, nullptr, 0, false, nullptr, nullptr,
+                       true);
 }
 
 // ---------------------------------------------------------------- batched decode

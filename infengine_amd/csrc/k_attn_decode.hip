@@ -332,8 +332,11 @@ size_t attn_decode_partials_bytes(int batch) {
 
 int launch_attn_decode(const AttnDecodeParams& p, int batch, bool merge, hipStream_t st) {
   IE_REQUIRE(batch >= 1 && batch <= 16, "attn_decode: batch %d out of range [1,16]", batch);
-  IE_REQUIRE(p.d_seq_len || (p.seq_len >= 1 && p.seq_len <= kMaxCtx && batch == 1),
-             "attn_decode: seq_len %d out of range [1,%d]", p.seq_len, kMaxCtx);
+  // (a host-side length: one sequence; the paged cache holds up to kMaxLongCtx positions)
+  IE_REQUIRE(p.d_seq_len || (p.seq_len >= 1 && batch == 1 &&
+                             p.seq_len <= (p.block_table ? kMaxLongCtx : kMaxCtx)),
+             "attn_decode: seq_len %d out of range [1,%d]", p.seq_len,
+             p.block_table ? kMaxLongCtx : kMaxCtx);
   IE_REQUIRE(p.max_splits >= 1 && p.max_splits <= kAttnSplits, "attn_decode: max_splits %d",
              p.max_splits);
   IE_REQUIRE(p.max_splits > 1 || (merge && p.out), "attn_decode: one split writes the output");

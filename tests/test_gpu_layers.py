@@ -3,7 +3,8 @@ Llama-3.1-8B, through the C-ABI (ie_decoder_layer_prefill, ie_decoder_layer_batc
 
 Two bars, as test_gpu_model holds the batch-1 decode to:
   * integration: ie_prefill / ie_decode_step_batched equal the embedding followed by the 32
-    per-layer calls, bit for bit (residual rows, K/V cache, prefill logits);
+    per-layer calls, bit for bit (residual rows, K/V cache, prefill logits; ie_prefill's last
+    layer is ie_decoder_layer_prefill_last_row, which computes the last row's output only);
   * per layer: a layer fed the GPU's own input matches the oracle's layer to 1e-2
     (tests/tolerance.py), so errors cannot hide in the accumulation across 32 layers.
 The prefill rows are checked at S = 2048 (the 8-wave flash-attention form and the M = 2048
@@ -18,7 +19,9 @@ import torch
 
 import oracle as orc
 from conftest import MODEL_SEED
-from gpu_util import assert_bf16_close, assert_delta_close, host, report_close, say
+from gpu_util import (assert_bf16_close, assert_delta_close, check_token, e2e_tol, host,
+                      report_close, say)
+from tolerance import assert_close
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 SEED = MODEL_SEED
@@ -44,10 +47,31 @@ PREFILL_LAYERS = (0, 1, 15, 31)
 PREFILL_ROWS = (0, 63, 64, 1000, 2047)
 
 
-def test_prefill_2048_layers(hip, model, oracle_model):
-    """ie_prefill(2048) equals ie_emblookup + 32 x ie_decoder_layer_prefill + the last row's
-    final norm / lm_head bit for bit; layers 0, 1, 15 and 31 at rows 0, 63, 64, 1000 and 2047
-    against the oracle fed the same input rows and the GPU's K/V rows of earlier positions."""
+def _last_layer_and_head(hip, c, model, b, S):
+    """Layer 31 of a chained prefill (b holds layers 0..30's output) as ie_prefill runs it
+    (ie_decoder_layer_prefill_last_row), then the final norm + lm_head of the last row; returns
+    (rows, logits, the layer's input rows).  b.data is left holding layer 31's input."""
+    x31 = b.data.clone()
+    hip.check(hip.lib.ie_decoder_layer_prefill_last_row(c.handle, model.ref(), 31, S, _ptr(b.data),
+                                                        _ptr(b.aux), _ptr(b.attn),
+                                                        _ptr(b.workspace), _ptr(b.kv)))
+    logits = torch.zeros(V, dtype=torch.float32, device="cuda")
+    hip.check(hip.lib.ie_final_norm_lm_head(c.handle, 1, _ptr(b.data[S - 1]),
+                                            _ptr(model.view(None, "final_norm")),
+                                            _ptr(model.view(None, "lm_head")), _ptr(logits)))
+    torch.cuda.synchronize()
+    rows = host(b.data[:S].view(torch.int16)).copy()
+    b.data.copy_(x31)
+    return rows, host(logits).copy(), x31
+
+
+def test_prefill_2048_layers(hip, model, oracle_model, noise_floor):
+    """ie_prefill(2048) equals ie_emblookup + 31 x ie_decoder_layer_prefill +
+    ie_decoder_layer_prefill_last_row + the last row's final norm / lm_head bit for bit; layers
+    0, 1, 15 and 31 (the full layer) at rows 0, 63, 64, 1000 and 2047 against the oracle fed the
+    same input rows and the GPU's K/V rows of earlier positions; the last-row-only layer 31
+    against the full one (its K/V rows bit for bit, its last row and the logits within the
+    tolerance of two summation orders)."""
     from infengine_amd.engine import Context, Request
     S = 2048
     ids = np.random.default_rng(2048).integers(0, V, S).astype(np.int32)
@@ -70,6 +94,13 @@ def test_prefill_2048_layers(hip, model, oracle_model):
     saved = {}
     for l in range(32):
         x_in = host(b.data[list(PREFILL_ROWS)].view(torch.int16)).copy() if l in PREFILL_LAYERS else None
+        if l == 31:
+            say("layer 31 as ie_prefill runs it (last row only)")
+            rows, logits, _ = _last_layer_and_head(hip, c, model, b, S)
+            assert np.array_equal(rows, want_x)
+            assert np.array_equal(logits, want_logits) and tok == int(np.argmax(want_logits))
+            assert torch.equal(b.kv, want_kv)
+            say("layer 31 over all rows")
         hip.check(hip.lib.ie_decoder_layer_prefill(c.handle, model.ref(), l, S, _ptr(b.data),
                                                    _ptr(b.aux), _ptr(b.attn), _ptr(b.workspace),
                                                    _ptr(b.kv)))
@@ -77,14 +108,19 @@ def test_prefill_2048_layers(hip, model, oracle_model):
             torch.cuda.synchronize()
             saved[l] = (x_in, host(b.data[list(PREFILL_ROWS)].view(torch.int16)).copy(),
                         host(kv6[l, :, :, :S].contiguous()))
-    logits = torch.zeros(V, dtype=torch.float32, device="cuda")
+    full_logits = torch.zeros(V, dtype=torch.float32, device="cuda")
     hip.check(hip.lib.ie_final_norm_lm_head(c.handle, 1, _ptr(b.data[S - 1]),
                                             _ptr(model.view(None, "final_norm")),
-                                            _ptr(model.view(None, "lm_head")), _ptr(logits)))
+                                            _ptr(model.view(None, "lm_head")), _ptr(full_logits)))
     torch.cuda.synchronize()
-    assert np.array_equal(host(b.data[:S].view(torch.int16)), want_x)
-    assert np.array_equal(host(logits), want_logits) and tok == int(np.argmax(want_logits))
-    assert torch.equal(b.kv, want_kv)
+    assert torch.equal(b.kv, want_kv)   # the full layer 31 writes the same K/V rows
+    # the last row through the decode kernels against the full layer's GEMMs and flash attention
+    report_close(orc.bf16_to_f32(want_x[S - 1]),
+                 orc.bf16_to_f32(host(b.data[S - 1].view(torch.int16))),
+                 what="layer 31 last row: last-row path vs full layer")
+    assert_close(want_logits, host(full_logits), tol=e2e_tol(noise_floor),
+                 what="logits: last-row layer 31 vs full layer 31")
+    check_token(tok, host(full_logits), want_logits, noise_floor)
     del b, want_kv
     c.close()
 
@@ -124,17 +160,13 @@ def test_prefill_split_k_equals_chained_layers(hip, model, S):
     b.tokens[:S] = torch.from_numpy(ids).cuda()
     hip.check(hip.lib.ie_emblookup(S, _ptr(b.tokens), _ptr(model.view(None, "emb_lookup")),
                                    _ptr(b.data), c.stream_ptr))
-    for l in range(32):
+    for l in range(31):
         hip.check(hip.lib.ie_decoder_layer_prefill(c.handle, model.ref(), l, S, _ptr(b.data),
                                                    _ptr(b.aux), _ptr(b.attn), _ptr(b.workspace),
                                                    _ptr(b.kv)))
-    logits = torch.zeros(V, dtype=torch.float32, device="cuda")
-    hip.check(hip.lib.ie_final_norm_lm_head(c.handle, 1, _ptr(b.data[S - 1]),
-                                            _ptr(model.view(None, "final_norm")),
-                                            _ptr(model.view(None, "lm_head")), _ptr(logits)))
-    torch.cuda.synchronize()
-    assert np.array_equal(host(b.data[:S].view(torch.int16)), want_x)
-    assert np.array_equal(host(logits), want_logits) and tok == int(np.argmax(want_logits))
+    rows, logits, _ = _last_layer_and_head(hip, c, model, b, S)
+    assert np.array_equal(rows, want_x)
+    assert np.array_equal(logits, want_logits) and tok == int(np.argmax(want_logits))
     assert torch.equal(b.kv, want_kv)
     del b, want_kv
     c.close()
