@@ -135,10 +135,11 @@ def test_decode_steps_vs_oracle(hip, model, oracle_model, prior, noise_floor):
     assert_bf16_close(gkv[0, :, :, POS:POS + 2], kv[0, :, :, POS:POS + 2], what="layer-0 kv", outlier_frac=1e-3)
 
 
-# 16: the M <= 16 skinny projections; 24 / 40 / 100: the 64-weight-row streaming projections
-# (64 and 128 X rows; K split into fp32 planes in the workspace, O aliased over q/k/v, SwiGLU in
-# the kernel); 256: split-K MFMA tiles, the SwiGLU split and 16-row flash-attention workgroups
-@pytest.mark.parametrize("S", [16, 24, 40, 100, 256])
+# 1 / 2 / 16: the M <= 16 skinny projections (at 1 the last layer's last row is its only row);
+# 24 / 40 / 100: the 64-weight-row streaming projections (64 and 128 X rows; K split into fp32
+# planes in the workspace, O aliased over q/k/v, SwiGLU in the kernel); 256: split-K MFMA tiles,
+# the SwiGLU split and 16-row flash-attention workgroups
+@pytest.mark.parametrize("S", [1, 2, 16, 24, 40, 100, 256])
 def test_prefill_then_decode_vs_oracle(hip, model, oracle_model, noise_floor, S):
     from infengine_amd.engine import Context, Request
     say(f"prefill seq_len={S} then decode_step vs oracle")
