@@ -96,6 +96,7 @@ BOGUS = C.c_void_p(0x1000)   # never dereferenced: every call below fails valida
     lambda l: l.ie_attn_prefill_core_paged(None, 1, 9000, BOGUS, BOGUS, 1, BOGUS, 0, BOGUS),
     lambda l: l.ie_decoder_layer_decode(None, None, 0, 1, BOGUS, BOGUS, BOGUS, BOGUS),
     lambda l: l.ie_decoder_layer_prefill(None, None, 0, 1, *[BOGUS] * 5),
+    lambda l: l.ie_decoder_layer_prefill_last_row(None, None, 0, 1, *[BOGUS] * 5),
     lambda l: l.ie_decoder_layer_batched(None, None, 0, 1, None, *[BOGUS] * 4),
 ])
 def test_host_side_validation(hip, call):
