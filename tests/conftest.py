@@ -44,6 +44,9 @@ def _gpu_stream(request):
     yield
     torch.cuda.synchronize()
     gpu_util.release()
+    # hand torch's cached blocks back to the device: the library allocates with hipMalloc
+    # (weights arenas, page pools), which torch's cache would otherwise crowd out over a session
+    torch.cuda.empty_cache()
 
 
 # ---------------------------------------------------------------- the full random-init model
