@@ -186,7 +186,9 @@ LENS16 = [101 + 97 * b for b in range(16)]
 LENS16_LONG = [513 + 3 * b for b in range(15)] + [2100]
 
 
-@pytest.mark.parametrize("lens", [[101, 257, 64], [2100, 257, 64], LENS16, LENS16_LONG])
+# B = 1; B = 7 with contexts at the first position and around the 64-position tile edges
+@pytest.mark.parametrize("lens", [[300], [1, 2, 63, 64, 65, 129, 500], [101, 257, 64],
+                                  [2100, 257, 64], LENS16, LENS16_LONG])
 def test_batched_decode_matches_single(hip, model, noise_floor, lens):
     from infengine_amd.engine import Context, Request, ptr
     B = len(lens)
