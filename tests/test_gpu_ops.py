@@ -664,11 +664,12 @@ def model31():
     W.free()
 
 
-@pytest.mark.parametrize("pos", [100, 2047, 3000, 5000])
+@pytest.mark.parametrize("pos", [100, 1023, 1024, 2047, 3000, 4095, 4096, 5000, 8191])
 def test_decoder_layer_decode_config2(hip, ctx, rope, model31, pos):
     """One full fused decoder layer, token at position pos (2047).  Up to
     4096 rows the O projection merges the attention partials itself (one tile per wave at
-    100, several at 2047 and 3000); 5001 rows take the merge kernel."""
+    100, several at 2047 and 3000; 4 splits up to 1024 rows, 8 from 1025); 4097 rows and more
+    take the merge kernel (up to 32 splits; 8192: the cache's last row)."""
     cos, sin, dcos, dsin = rope
     say(f"decoder_layer_decode layer 0 pos {pos} (random-init weights)")
     seed, layer = 31, 0
