@@ -138,8 +138,9 @@ def test_decode_steps_vs_oracle(hip, model, oracle_model, prior, noise_floor):
 # 1 / 2 / 16: the M <= 16 skinny projections (at 1 the last layer's last row is its only row);
 # 24 / 40 / 100: the 64-weight-row streaming projections (64 and 128 X rows; K split into fp32
 # planes in the workspace, O aliased over q/k/v, SwiGLU in the kernel); 256: split-K MFMA tiles,
-# the SwiGLU split and 16-row flash-attention workgroups
-@pytest.mark.parametrize("S", [1, 2, 16, 24, 40, 100, 256])
+# the SwiGLU split and 16-row flash-attention workgroups; 128 / 129: the last medium-row size and
+# the first split-K one
+@pytest.mark.parametrize("S", [1, 2, 16, 24, 40, 100, 128, 129, 256])
 def test_prefill_then_decode_vs_oracle(hip, model, oracle_model, noise_floor, S):
     from infengine_amd.engine import Context, Request
     say(f"prefill seq_len={S} then decode_step vs oracle")
