@@ -22,6 +22,8 @@ Also reported, on the same run:
                 on the engine stream after 150 ms of warm-up (median of 3 runs of 10
                 launches), as TFLOP/s and fraction of the 2.5 PFLOP/s dense bf16 MFMA peak,
                 with torch.matmul (hipBLASLt) on the same shapes and protocol beside them.
+  prefill_64    a 64-token prefill (mean of 3 warm calls): every weight is read once, so it
+                is reported against HBM as the weight bytes (32 layers + lm_head) per second.
   cpu_baseline  the CPU oracle (oracle/, OpenMP) decoding the same model on this
                 host: whole decode steps (32 layers + lm_head + argmax) for about
                 10 s after one untimed step.
@@ -558,6 +560,26 @@ def main() -> int:
                        "gemm": gemms, "attention": attention,
                        "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS}
 
+    # ---- a short prompt (64 tokens): every weight read once, so the prefill is HBM-bound;
+    # warm calls (two untimed, then the mean of three), bytes = the 32 layers' products + lm_head
+    log("prefill 64 tokens")
+    P64 = 64
+    req3 = Request(ctx, W, max_seq_len=P64 + 8)
+    req3.tokens[:P64] = torch.from_numpy(rng.integers(0, VOCAB, P64).astype(np.int32)).cuda()
+    for _ in range(2):
+        req3.prefill(P64)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        req3.prefill(P64)
+    torch.cuda.synchronize()
+    p64 = (time.perf_counter() - t0) / 3
+    del req3
+    w_bytes = 2 * (LAYERS * LAYER_GEMM_PARAMS + VOCAB * HIDDEN)
+    prefill64 = {"seq_len": P64, "ms": round(p64 * 1e3, 3), "tokens_per_s": round(P64 / p64, 1),
+                 "weight_GBps": round(w_bytes / p64 / 1e9, 1),
+                 "weight_hbm_frac": round(w_bytes / p64 / 1e9 / HBM_PEAK_GBPS, 4)}
+
     # ---- dominant kernel, timed live on its own stream with HIP events
     log("gate/up GEMV kernel timing")
     h = torch.empty(FFN, dtype=torch.bfloat16, device="cuda")
@@ -605,6 +627,7 @@ def main() -> int:
         "batched_paged": batched_paged,
         "configs": configs,
         "prefill_2048": prefill2048,
+        "prefill_64": prefill64,
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<4096, SwiGLU, RMSNorm> (gate/up)",
                      "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC,
