@@ -78,6 +78,17 @@ def test_rmsnorm(hip, ctx):
     sync()
     assert_bf16_close(host(out), g["y"], ulps=2, what="rmsnorm vs HF")
     assert (ulp_diff(host(out), g["y"]) == 0).mean() > 0.99
+    # fewer rows (1, 7, 126): each row as in the 128-row call, bit for bit, and nothing written
+    # past the last row
+    ref = bf16_empty(128, H)
+    hip.check(hip.lib.ie_rmsnorm(128, P(dev(x)), P(dev(w)), P(ref), ctx.stream_ptr))
+    for rows in (1, 7, 126):
+        say(f"rmsnorm rows={rows}")
+        o2 = torch.full((rows + 4, H), 0x40E0, dtype=torch.int16, device="cuda")  # bf16 7.0
+        hip.check(hip.lib.ie_rmsnorm(rows, P(dev(x)), P(dev(w)), P(o2), ctx.stream_ptr))
+        sync()
+        assert torch.equal(o2[:rows], ref[:rows]), rows
+        assert bool((o2[rows:] == 0x40E0).all()), rows
 
 
 def test_residual_add_bit_exact(hip, ctx):
