@@ -140,7 +140,7 @@ def test_decode_steps_vs_oracle(hip, model, oracle_model, prior, noise_floor):
 # planes in the workspace, O aliased over q/k/v, SwiGLU in the kernel); 256: split-K MFMA tiles,
 # the SwiGLU split and 16-row flash-attention workgroups; 128 / 129: the last medium-row size and
 # the first split-K one
-@pytest.mark.parametrize("S", [1, 2, 16, 24, 40, 100, 128, 129, 256])
+@pytest.mark.parametrize("S", [1, 2, 16, 17, 24, 40, 64, 65, 100, 128, 129, 256])
 def test_prefill_then_decode_vs_oracle(hip, model, oracle_model, noise_floor, S):
     from infengine_amd.engine import Context, Request
     say(f"prefill seq_len={S} then decode_step vs oracle")
