@@ -4,6 +4,18 @@
 // Reference: every prefill matmul is cublasGemmEx / cublasGemmStridedBatchedEx
 // with fp32 compute (kernels/ffn.cu:7-33, kernels/attn.cu:12-39, 265-293).
 //
+// Kernels of this file by the product's rows M (launch_gemm; M <= 16 goes to the skinny GEMM of
+// k_gemm_skinny.hip):
+//   17-128   gemm_mid_kernel: a workgroup streams 64 (or 128) weight rows, loaded nontemporal,
+//            against all X rows; K split into fp32 partial planes summed by a split reduction
+//            (RoPE + K/V write, residual + RMSNorm, SwiGLU or bf16), or unsplit with the
+//            epilogue in the kernel.
+//   to 1024  gemm_wide_kernel (128-row X tiles, direct-to-LDS rings) split over K, with the
+//            same reductions, where the best tiling is one round that leaves half the chip idle.
+//   beyond   launch_tiled: the ping-pong gemm_pp_kernel / gemm_pp_dual_kernel on 256 x 256,
+//            256 x 128 and 192 x 256 tiles, chosen by rounds of 256 tiles; the 128 x 128
+//            gemm_kernel described next takes what the larger tiles do not fit.
+//
 // Tile: 128 W-rows x 128 X-rows x 64 k per workgroup of 4 waves; each wave owns
 // a 64 x 64 block as 4 x 4 v_mfma_f32_16x16x32_bf16 tiles.  The MFMA computes
 // D = W_tile . X_tile^T, so a lane's 4 accumulator values are 4 consecutive
