@@ -242,7 +242,7 @@ def test_batched_decode_matches_single(hip, model, noise_floor, lens):
 # 40 / 100: the 64-weight-row streaming projections (64 and 128 X rows); 600: split-K MFMA tiles
 # and 16-row attention workgroups; 1024: the last split-K size; 1100: unsplit projections, 16-row
 # workgroups; 1800: the 32-row attention workgroups
-@pytest.mark.parametrize("S", [40, 100, 600, 1024, 1100, 1800])
+@pytest.mark.parametrize("S", [17, 40, 64, 65, 100, 129, 600, 1024, 1100, 1800])
 def test_prefill_paged_equals_contiguous(hip, model, S):
     """ie_prefill_paged (K/V rows into pages scattered over a pool) against ie_prefill (reference-
     layout cache): bit-identical logits and token, and every K/V row in its page."""
