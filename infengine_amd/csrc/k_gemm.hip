@@ -1111,8 +1111,9 @@ void gemm_pp_dual_kernel(GemmParams p1, int m_tiles1, int nb1, GemmParams p2, in
 // K / k_splits.  64-k stages (128-byte rows, 8-row direct-to-LDS loads: whole lines) in a ring
 // of S slots (4 at XR = 64: 64 KiB, two workgroups a CU; 3 at 128): stage k + S - 1 is issued at
 // k-step k, so S - 1 stages are in flight per workgroup.  The weight rows are read once per
-// launch and loaded nontemporal (cache policy nt, as the GEMV's); measured 2-5% faster per
-// 17-64-token prefill than the default policy, which the X rows, re-read by every tile, keep.
+// launch and loaded nontemporal (cache policy nt, as the GEMV's); measured 3-5% faster per
+// 17-64-token prefill (1-1.5% at 100-128) than the default policy, which the X rows, re-read by
+// every tile, keep.
 // One barrier per k-step: after it, every wave's loads of stage k have landed and every wave is
 // done with slot (k - 1) % S, which takes stage k + S - 1.
 // Epilogues: fp32 partial planes (split K, reduced by the split reductions), bf16, residual,
